@@ -1,0 +1,146 @@
+"""Benchmark: ResNet-18 fp32 at batch 32 through the HIP fused groups on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 32] [--conv-mode implicit]
+
+One step is one forward pass of the whole network over one batch of
+synthetic N(0,1) images already resident in device memory; random-init
+weights with the architecture and distributions of the benchmark config.
+Prints one JSON line with images/s, the dominant kernel's roofline (TFLOP/s
+against the fp32 MFMA peak, timed per launch with HIP events on the
+library's stream) and the NumPy oracle timed on host cores over a bounded
+sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "ResNet-18 b=32 fp32 images/sec; fused GEMM/conv TFLOP/s & % MFMA peak"
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+
+def cpu_baseline(graph, batch_seconds: float = 12.0) -> dict:
+    """The NumPy oracle (a restatement of the reference executor) on one
+    image at a time, repeated until ``batch_seconds`` have elapsed."""
+    from mdlc_amd.tools.build_resnet18 import make_input
+    from oracle.reference import ReferenceExecutor
+
+    ex = ReferenceExecutor(graph)
+    x = make_input(1, seed=7)
+    ex.run({"input": x})                       # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        ex.run({"input": x})
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= batch_seconds and n >= 2:
+            break
+    return {"value": n / el, "unit": "images/s", "cores": 1, "kind": "port",
+            "sample": f"{n} single-image ResNet-18 forwards of the fused graph through the "
+                      f"NumPy oracle (einsum conv, as the reference executor), {el:.1f} s, "
+                      f"1 thread, host of the GPU box"}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--conv-mode", default="implicit", choices=["implicit", "im2col"])
+    ap.add_argument("--graph", action="store_true", help="replay the plan as a hipGraph")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-iters", type=int, default=3)
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "inference shards by batch across GPUs, which is not part of this build",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+
+    from mdlc_amd.codegen.hip.hip_executor import HipExecutor
+    from mdlc_amd.compiler import compile_graph
+    from mdlc_amd.tools.build_resnet18 import build_resnet18, make_input
+
+    B = args.batch
+    x = make_input(B)
+    t0 = time.perf_counter()
+    c = compile_graph(build_resnet18(batch=B), feeds={"input": x}, conv_mode=args.conv_mode)
+    ex = HipExecutor(c.module, use_graph=args.graph)
+    print(f"[bench] compiled + loaded in {time.perf_counter() - t0:.1f} s; "
+          f"{len(c.module.plan)} launches, arena {ex.arena_bytes / 2**20:.1f} MiB", file=sys.stderr,
+          flush=True)
+    ex._upload_feeds({"input": x})
+    ex.plan.run(args.warmup)
+    ex.ctx.synchronize()
+    ms_per_step = ex.plan.time_ms(0, args.steps)
+    value = B * 1000.0 / ms_per_step
+    print(f"[bench] {ms_per_step:.3f} ms/step, {value:.1f} images/s", file=sys.stderr, flush=True)
+
+    # Per-launch timing -> per-kernel totals; the dominant kernel is the one
+    # with the most device time per step.
+    prof = ex.profile(args.profile_iters)
+    per_kernel: dict = {}
+    for launch, ms in prof:
+        d = per_kernel.setdefault(launch.kernel_name, {"ms": 0.0, "flops": 0, "bytes": 0,
+                                                       "launches": 0, "kind": launch.kind})
+        d["ms"] += ms
+        d["flops"] += launch.meta.get("flops", 0)
+        d["bytes"] += launch.meta.get("bytes", 0)
+        d["launches"] += 1
+    total_ms = sum(d["ms"] for d in per_kernel.values())
+    for name, d in sorted(per_kernel.items(), key=lambda kv: -kv[1]["ms"]):
+        rate = (f"{d['flops'] / d['ms'] / 1e9:8.1f} TFLOP/s" if d["flops"]
+                else f"{d['bytes'] / d['ms'] / 1e6:8.1f} GB/s")
+        print(f"[bench]   {name:56s} {d['launches']:3d}x {d['ms']:8.3f} ms {rate}",
+              file=sys.stderr)
+    dom_name, dom = max(per_kernel.items(), key=lambda kv: kv[1]["ms"])
+    avg_ms = dom["ms"] / dom["launches"]
+    if dom["flops"]:
+        achieved = dom["flops"] / dom["launches"] / (avg_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_MFMA_TFLOPS,
+                "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA_TFLOPS, "traffic": None}
+    else:
+        achieved = dom["bytes"] / dom["launches"] / (avg_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": achieved / PEAK_HBM_GBS, "traffic": None}
+    roof.update({"kernel": dom_name, "launches_per_step": dom["launches"],
+                 "avg_launch_ms": avg_ms, "share_of_step": dom["ms"] / total_ms})
+    all_flops = sum(l.meta.get("flops", 0) for l in c.module.plan)
+    gemm_ms = sum(d["ms"] for d in per_kernel.values() if d["flops"])
+    ex.close()
+
+    line = {
+        "metric": METRIC, "value": value, "unit": "images/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic N(0,1) images, random-init weights (Kaiming-normal conv/FC, "
+                "BN gamma U(0.5,1.5) beta N(0,0.1) mean N(0,0.1) var U(0.5,1.5))",
+        "config": {"workload": f"resnet18_fp32_b{B}", "batch": B, "image": [3, 224, 224],
+                   "conv_mode": args.conv_mode, "launches": len(c.module.plan),
+                   "gflop_per_step": all_flops / 1e9,
+                   "conv_gemm_tflops": all_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms else None,
+                   "network_tflops": all_flops / (ms_per_step * 1e-3) / 1e12},
+        "roofline": roof,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(c.graph if B == 1 else
+                                            compile_graph(build_resnet18(batch=1)).graph)
+    print(json.dumps(line), flush=True)
+    _ = np
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,227 @@
+"""Run a ``HipModule`` on one MI355X: one arena, one stream, one C++ plan.
+
+Replaces the reference's ``GpuExecutor`` (mdlc/codegen/cuda/gpu_executor.py:
+26-114). Differences that matter on the device:
+
+* Memory is one ``hipMalloc`` arena laid out at construction: constants
+  (weights and packed device layouts), runtime inputs, the planner's pooled
+  activation buffers at their 256-byte-aligned offsets, and one scratch
+  region shared by every column matrix (column matrices are used strictly in
+  stream order, so they never overlap in time). Weights are uploaded once.
+* The launch loop is the C++ plan runner of libmdlc_hip.so (optionally a
+  captured hipGraph); Python only packs it once.
+* No host fallbacks: every launch is a device kernel.
+
+``run(feeds, timing=False)`` returns ``{"outputs": ..., "ms": ...}`` like the
+reference. ``run_all`` returns every tensor the plan produces (launch by
+launch, read back after each), and ``run_isolated`` runs each launch group on
+externally supplied inputs, so a single group's error can be told apart from
+drift accumulated along the chain.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import numpy as np
+
+from mdlc_amd.codegen.hip.emit import HipModule, Launch
+from mdlc_amd.codegen.hip.hiprtc_runtime import Arg, HipContext, HipError, Plan, compile_code_object
+from mdlc_amd.ir import DType
+from mdlc_amd.runtime.memory_planner import align_up, plan_memory
+
+
+class HipExecutor:
+    def __init__(self, module: HipModule, ctx: Optional[HipContext] = None, *,
+                 use_graph: bool = False) -> None:
+        self.module = module
+        self.ctx = ctx or HipContext()
+        g = module.graph
+        self.code = self.ctx.load_code(compile_code_object(module.sources(), arch=self.ctx.arch))
+        self.funcs = {name: self.code.func(name) for name in module.kernels}
+        for l in module.plan:
+            if l.kernel_name not in self.funcs:
+                self.funcs[l.kernel_name] = self.code.func(l.kernel_name)
+
+        # ---- arena layout ------------------------------------------------
+        self.mem_plan = plan_memory(g)
+        self.offsets: dict = {}
+        self.shapes: dict = {}
+        self.dtypes: dict = {}
+        cur = 0
+        const_vals: dict = {}
+        for l in module.plan:
+            for e in l.inputs:
+                if e in module.device_constants:
+                    const_vals[e] = module.device_constants[e]
+                elif g.is_constant(e):
+                    const_vals[e] = np.asarray(g.initializers[e])
+        for name in sorted(const_vals):
+            arr = np.ascontiguousarray(const_vals[name])
+            const_vals[name] = arr
+            self.offsets[name] = cur
+            self.shapes[name], self.dtypes[name] = arr.shape, arr.dtype
+            cur += align_up(arr.nbytes)
+        for name in g.runtime_inputs:
+            info = g.info(name)
+            self.offsets[name] = cur
+            self.shapes[name] = tuple(info.shape)
+            self.dtypes[name] = DType.to_numpy(info.dtype)
+            cur += align_up(info.nbytes())
+        act_base = cur
+        for t, bid in self.mem_plan.assignment.items():
+            info = g.info(t)
+            self.offsets[t] = act_base + self.mem_plan.offsets[bid]
+            self.shapes[t] = tuple(info.shape)
+            self.dtypes[t] = DType.to_numpy(info.dtype)
+        cur = act_base + self.mem_plan.arena_bytes
+        scratch = max([r * ld * 4 for r, ld in module.scratch_shapes.values()] + [0])
+        for name, (r, ld) in module.scratch_shapes.items():
+            self.offsets[name] = cur
+            self.shapes[name], self.dtypes[name] = (r, ld), np.dtype(np.float32)
+        cur += align_up(scratch)
+        self.arena_bytes = cur
+        self.arena = self.ctx.malloc(max(cur, 256))
+        self.base = int(self.arena.value)
+        for name, arr in const_vals.items():
+            self.ctx.htod(self.base + self.offsets[name], arr)
+
+        self.launch_records = [self._record(l) for l in module.plan]
+        self.plan = Plan(self.launch_records)
+        if use_graph:
+            self.plan.use_graph(True)
+        self._single: Optional[list] = None
+
+    # ---- plan packing -----------------------------------------------------
+
+    def ptr(self, name: str) -> int:
+        if name not in self.offsets:
+            raise HipError(f"tensor {name!r} has no arena slot")
+        return self.base + self.offsets[name]
+
+    def _record(self, l: Launch) -> tuple:
+        m = l.meta
+        P = lambda e: Arg.ptr(self.ptr(e))  # noqa: E731
+        I = Arg.i32  # noqa: E741
+        k = l.kind
+        if k == "gemm":
+            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+            args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["ldb"]), I(m["ldc"]),
+                     I(m["hw"])]
+        elif k == "conv":
+            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+            args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["Cin"]), I(m["H"]),
+                     I(m["W"]), I(m["OH"]), I(m["OW"])]
+        elif k == "im2col":
+            args = [P(l.inputs[0]), P(l.outputs[0])]
+            args += [I(m[f]) for f in ("C", "H", "W", "KH", "KW", "OH", "OW", "SH", "SW",
+                                       "PH", "PW", "DH", "DW", "batch", "ldc")]
+        elif k == "dwconv":
+            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+            args += [I(m[f]) for f in ("N", "C", "H", "W", "OC", "OH", "OW", "PT", "PL")]
+        elif k == "elementwise":
+            args = [P(e) for e in l.inputs] + [P(o) for o in l.outputs] + [I(m["N"])]
+        elif k == "maxpool":
+            args = [P(l.inputs[0]), P(l.outputs[0])]
+            args += [I(m[f]) for f in ("planes", "H", "W", "OH", "OW", "KH", "KW", "SH", "SW",
+                                       "PT", "PL", "DH", "DW")]
+        elif k == "gap":
+            args = [P(l.inputs[0]), P(l.outputs[0]), I(m["planes"]), I(m["HW"])]
+        elif k == "copy":
+            args = [P(l.inputs[0]), P(l.outputs[0]), Arg.i64(m["nbytes"])]
+        else:
+            raise HipError(f"launch kind {k!r} has no device implementation")
+        return (self.funcs[l.kernel_name].value, l.grid, l.block, 0, args)
+
+    # ---- execution ----------------------------------------------------------
+
+    def _upload_feeds(self, feeds: dict) -> None:
+        g = self.module.graph
+        for name in g.runtime_inputs:
+            if name not in feeds:
+                raise HipError(f"missing feed {name!r}")
+            arr = np.ascontiguousarray(feeds[name], dtype=self.dtypes[name])
+            if tuple(arr.shape) != tuple(self.shapes[name]):
+                raise HipError(f"feed {name!r} has shape {arr.shape}, compiled for {self.shapes[name]}")
+            self.ctx.htod(self.ptr(name), arr)
+
+    def read(self, name: str) -> np.ndarray:
+        return self.ctx.dtoh(self.ptr(name), self.shapes[name], self.dtypes[name])
+
+    def write(self, name: str, arr: np.ndarray) -> None:
+        arr = np.ascontiguousarray(arr, dtype=self.dtypes[name])
+        if tuple(arr.shape) != tuple(self.shapes[name]):
+            raise HipError(f"{name!r}: shape {arr.shape} != {self.shapes[name]}")
+        self.ctx.htod(self.ptr(name), arr)
+
+    def run(self, feeds: dict, *, timing: bool = False, warmup: int = 3, iters: int = 10) -> dict:
+        self._upload_feeds(feeds)
+        self.plan.run(1)
+        self.ctx.synchronize()
+        out = {"outputs": {o: self.read(o) for o in self.module.graph.outputs}}
+        if timing:
+            out["ms"] = self.plan.time_ms(warmup, iters)
+        return out
+
+    def _singles(self) -> list:
+        if self._single is None:
+            self._single = [Plan([r]) for r in self.launch_records]
+        return self._single
+
+    def run_all(self, feeds: dict) -> dict:
+        """Every tensor the plan writes (except scratch), read back right after
+        the launch that produced it, so pooled buffers can be reused safely."""
+        self._upload_feeds(feeds)
+        env = {}
+        for l, p in zip(self.module.plan, self._singles()):
+            p.run(1)
+            self.ctx.synchronize()
+            for o in l.outputs:
+                if o not in self.module.scratch_shapes:
+                    env[o] = self.read(o)
+        return env
+
+    def run_isolated(self, env: dict) -> dict:
+        """Run each launch group on the tensors in ``env`` (e.g. the oracle's
+        values of its inputs) and return what each group wrote."""
+        got = {}
+        groups: list = []
+        for i, l in enumerate(self.module.plan):
+            node = l.meta.get("node")
+            if groups and groups[-1][0] is node:
+                groups[-1][1].append(i)
+            else:
+                groups.append((node, [i]))
+        singles = self._singles()
+        consts = set(self.module.device_constants) | set(self.module.graph.initializers)
+        for node, idxs in groups:
+            for e in node.real_inputs():
+                if e in env and e not in consts:
+                    self.write(e, env[e])
+            for i in idxs:
+                singles[i].run(1)
+            self.ctx.synchronize()
+            for o in node.outputs:
+                if o:
+                    got[o] = self.read(o)
+        return got
+
+    def profile(self, iters: int = 3) -> list:
+        """[(launch, ms)] — each launch timed with its own event pair."""
+        return list(zip(self.module.plan, self.plan.profile(iters)))
+
+    def close(self) -> None:
+        if getattr(self, "arena", None) is not None:
+            self.plan.close()
+            for p in self._single or []:
+                p.close()
+            self.ctx.free(self.arena)
+            self.arena = None
+
+
+def run_on_gpu(module: HipModule, feeds: dict, *, timing: bool = False) -> dict:
+    ex = HipExecutor(module)
+    try:
+        return ex.run(feeds, timing=timing)
+    finally:
+        ex.close()

@@ -1,0 +1,287 @@
+"""HIP kernel generators for gfx950.
+
+Each fused-group kind has a hand-written HIP template under ``kernels/``
+(C++ templates in namespace ``mdlc``); this module writes the small
+``extern "C"`` wrappers that instantiate them for one group — tile schedule,
+epilogue (bias + activation baked in as code), convolution window, vector
+paths — plus the string-generated body of elementwise chains. Together they
+replace the CUDA string templates of mdlc/codegen/cuda/templates.py:
+``activation_expr`` (:24-51), ``gemm_kernel`` (:56-160), ``im2col_kernel``
+(:165-201) and ``elementwise_kernel`` (:209-269).
+
+Floating-point constants are emitted as exact hexadecimal literals so the
+kernel uses the same float32 bits as the NumPy oracle.
+"""
+
+from __future__ import annotations
+
+import os
+from typing import Optional
+
+from mdlc_amd.codegen.schedule import MfmaSchedule
+from mdlc_amd.ir import Node
+
+KERNEL_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "kernels")
+
+
+def library_source(part: str) -> str:
+    with open(os.path.join(KERNEL_DIR, part + ".hip")) as f:
+        return f.read()
+
+
+def flit(x: float) -> str:
+    """An exact float32 literal for ``x`` (``x`` is first rounded to float32)."""
+    import numpy as np
+
+    v = float(np.float32(x))
+    if v != v:
+        return "__builtin_nanf(\"\")"
+    if v in (float("inf"), float("-inf")):
+        return "__builtin_inff()" if v > 0 else "(-__builtin_inff())"
+    return f"{v.hex()}f"
+
+
+# ----- activation epilogue ------------------------------------------------
+
+def activation_expr(activation: Optional[str], var: str, attrs: dict) -> str:
+    """A HIP expression applying ``activation`` to float ``var``, with the
+    NumPy float32 semantics of the oracle (mdlc/runtime/ops.py:155-185)."""
+    v = var
+    if not activation or activation == "Identity":
+        return v
+    if activation == "Relu":
+        return f"fmaxf({v}, 0.0f)"
+    if activation == "Relu6":
+        return f"fminf(fmaxf({v}, 0.0f), 6.0f)"
+    if activation == "Clip":
+        lo, hi = attrs.get("clip_min"), attrs.get("clip_max")
+        e = v if lo is None else f"fmaxf({v}, {flit(lo)})"
+        return e if hi is None else f"fminf({e}, {flit(hi)})"
+    if activation == "Sigmoid":
+        return f"(1.0f / (1.0f + expf(-({v}))))"
+    if activation == "Tanh":
+        return f"tanhf({v})"
+    if activation == "LeakyRelu":
+        a = flit(attrs.get("alpha", 0.01))
+        return f"(({v}) >= 0.0f ? ({v}) : {a} * ({v}))"
+    if activation == "HardSigmoid":
+        a, b = flit(attrs.get("alpha", 0.2)), flit(attrs.get("beta", 0.5))
+        return f"fminf(fmaxf({a} * ({v}) + {b}, 0.0f), 1.0f)"
+    if activation == "HardSwish":
+        return f"(({v}) * fminf(fmaxf(({v}) / 6.0f + 0.5f, 0.0f), 1.0f))"
+    raise NotImplementedError(f"no HIP epilogue for activation {activation!r}")
+
+
+BIAS_CODE = {None: 0, "none": 0, "row": 1, "col": 2}
+
+
+def epilogue_struct(name: str, *, bias_mode: Optional[str], activation: Optional[str],
+                    attrs: dict, alpha: float = 1.0, beta: float = 1.0) -> str:
+    """``struct name { bias; apply(acc, b) }``: alpha*acc (+ beta*b), then the
+    activation — the order of mdlc/runtime/ops.py:84-92 followed by the act."""
+    code = BIAS_CODE[bias_mode]
+    lines = ["float v = acc;"]
+    if float(alpha) != 1.0:
+        lines.append(f"v = {flit(alpha)} * v;")
+    if code:
+        lines.append("v = v + b;" if float(beta) == 1.0 else f"v = v + {flit(beta)} * b;")
+    lines.append(f"return {activation_expr(activation, 'v', attrs)};")
+    body = " ".join(lines)
+    return (f"struct {name} {{\n  static constexpr int bias = {code};\n"
+            f"  __device__ __forceinline__ static float apply(float acc, float b) {{ {body} }}\n}};\n")
+
+
+# ----- GEMM / conv ----------------------------------------------------------
+
+def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: str = "col",
+                activation: Optional[str] = None, attrs: Optional[dict] = None,
+                alpha: float = 1.0, beta: float = 1.0, bmode: int = 0, out_nchw: bool = False,
+                vec_a: bool = True, win: Optional[tuple] = None) -> tuple:
+    """(name, source) of one GEMM instantiation.
+
+    Kernel ABI (the reference's gemm ABI plus trailing layout arguments):
+      dense  (bmode 0/1): (A, B, [bias], C, int M, int N, int K, int lda, int ldb, int ldc, int hw)
+      conv   (bmode 2)  : (W, x, [bias], y, int M, int N, int K, int lda,
+                           int Cin, int H, int W, int OH, int OW)
+    ``hw`` > 0 selects the NCHW output scatter for conv-as-GEMM.
+    """
+    attrs = attrs or {}
+    s = sched
+    epi = f"{name}_epi"
+    src = [epilogue_struct(epi, bias_mode=bias_mode if with_bias else None,
+                           activation=activation, attrs=attrs, alpha=alpha, beta=beta)]
+    winty = "mdlc::NoWin" if win is None else "mdlc::ConvWin<%d, %d, %d, %d, %d, %d, %d, %d>" % tuple(win)
+    bias_arg = "const float* __restrict__ bias, " if with_bias else ""
+    bias_val = "bias" if with_bias else "nullptr"
+    tmpl = (f"mdlc::gemm_f32_mfma<{s.BM}, {s.BN}, {s.BK}, {s.WGM}, {s.WGN}, {s.MS}, "
+            f"{'true' if s.DB else 'false'}, {'true' if vec_a else 'false'}, {bmode}, "
+            f"{1 if out_nchw else 0}, {epi}, {winty}>")
+    nt = s.threads_per_block()
+    if bmode == 2:
+        src.append(
+            f'extern "C" __global__ __launch_bounds__({nt}) void {name}(\n'
+            f"    const float* __restrict__ A, const float* __restrict__ x, {bias_arg}"
+            f"float* __restrict__ y,\n    int M, int N, int K, int lda, int Cin, int H, int W, "
+            f"int OH, int OW) {{\n"
+            f"  mdlc::GemmArgs g{{A, x, {bias_val}, y, M, N, K, lda, 0, 0, OH * OW, Cin, H, W, OH, OW}};\n"
+            f"  {tmpl}(g);\n}}\n")
+    else:
+        src.append(
+            f'extern "C" __global__ __launch_bounds__({nt}) void {name}(\n'
+            f"    const float* __restrict__ A, const float* __restrict__ B, {bias_arg}"
+            f"float* __restrict__ C,\n    int M, int N, int K, int lda, int ldb, int ldc, int hw) {{\n"
+            f"  mdlc::GemmArgs g{{A, B, {bias_val}, C, M, N, K, lda, ldb, ldc, hw, 0, 0, 0, 0, 0}};\n"
+            f"  {tmpl}(g);\n}}\n")
+    return name, "\n".join(src)
+
+
+def im2col_kernel(name: str = "im2col") -> tuple:
+    """ABI: the reference's (x, cols, C, H, W, KH, KW, OH, OW, SH, SW, PH, PW,
+    DH, DW) plus trailing (N, ldc) for the batched column matrix."""
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const float* __restrict__ x, float* __restrict__ cols, int C, int H, int W,\n"
+        "    int KH, int KW, int OH, int OW, int SH, int SW, int PH, int PW, int DH, int DW,\n"
+        "    int N, int ldc) {\n"
+        "  mdlc::im2col_f32(x, cols, C, H, W, KH, KW, OH, OW, SH, SW, PH, PW, DH, DW, N, ldc);\n}\n")
+
+
+def maxpool_kernel(name: str = "maxpool") -> tuple:
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const float* __restrict__ x, float* __restrict__ y, int planes, int H, int W,\n"
+        "    int OH, int OW, int KH, int KW, int SH, int SW, int PT, int PL, int DH, int DW) {\n"
+        "  mdlc::maxpool_f32(x, y, planes, H, W, OH, OW, KH, KW, SH, SW, PT, PL, DH, DW);\n}\n")
+
+
+def gap_kernel(name: str = "global_avg_pool") -> tuple:
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const float* __restrict__ x, float* __restrict__ y, int planes, int HW) {\n"
+        "  mdlc::gap_f32(x, y, planes, HW);\n}\n")
+
+
+def copy_kernel(name: str = "copy_bytes") -> tuple:
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const void* __restrict__ src, void* __restrict__ dst, long long nbytes) {\n"
+        "  mdlc::copy_bytes((const unsigned char*)src, (unsigned char*)dst, nbytes);\n}\n")
+
+
+def dwconv_kernel(name: str, win: tuple, *, with_bias: bool, activation: Optional[str],
+                  attrs: dict) -> tuple:
+    """Depthwise conv with epilogue. ``win`` = (KH, KW, SH, SW, DH, DW).
+    ABI: (x, w, [bias], y, N, C, H, W, OC, OH, OW, PT, PL)."""
+    epi = f"{name}_epi"
+    src = epilogue_struct(epi, bias_mode="row" if with_bias else None,
+                          activation=activation, attrs=attrs)
+    bias_arg = "const float* __restrict__ bias, " if with_bias else ""
+    return name, src + (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        f"    const float* __restrict__ x, const float* __restrict__ w, {bias_arg}"
+        "float* __restrict__ y,\n    int N, int C, int H, int W, int OC, int OH, int OW, int PT, int PL) {\n"
+        f"  mdlc::dwconv_f32<{', '.join(str(v) for v in win)}, {epi}>(x, w, "
+        f"{'bias' if with_bias else 'nullptr'}, y, N, C, H, W, OC, OH, OW, PT, PL);\n}}\n")
+
+
+# ----- fused elementwise ----------------------------------------------------
+
+_BINARY = {"Add": "+", "Sub": "-", "Mul": "*", "Div": "/"}
+
+
+def _cname(edge: str, table: dict) -> str:
+    if edge not in table:
+        table[edge] = f"v{len(table)}"
+    return table[edge]
+
+
+def elementwise_kernel(name: str, node: Node, *, scalar_consts: Optional[dict] = None) -> tuple:
+    """String-generate a fused pointwise kernel from a ``FusedElementwise``
+    (or a single pointwise node wrapped as a one-member group).
+
+    External non-constant inputs become pointer arguments in first-use order,
+    each member op one line of register arithmetic, and each group output one
+    store. Each thread handles 4 consecutive elements with 128-bit loads and
+    stores; the last N % 4 elements are handled one per thread.
+    ABI: (in_0, ..., in_k, out_0, ..., out_m, int N). Returns
+    ``(name, source, ordered_external_inputs)``.
+    """
+    consts = scalar_consts or {}
+    sub = node.attrs["subgraph"]
+    internal = {o for n in sub for o in n.outputs if o}
+    ext: list = []
+    for n in sub:
+        for e in n.real_inputs():
+            if e not in internal and e not in consts and e not in ext:
+                ext.append(e)
+    names: dict = {}
+
+    def ref(e: str) -> str:
+        return flit(consts[e]) if e in consts else _cname(e, names)
+
+    body = []
+    for n in sub:
+        out = _cname(n.outputs[0], names)
+        if n.op_type in _BINARY:
+            body.append(f"float {out} = {ref(n.inputs[0])} {_BINARY[n.op_type]} {ref(n.inputs[1])};")
+        elif n.op_type == "Clip":
+            attrs = dict(n.attrs)
+            lo = consts.get(n.inputs[1]) if len(n.inputs) > 1 and n.inputs[1] else n.attrs.get("min")
+            hi = consts.get(n.inputs[2]) if len(n.inputs) > 2 and n.inputs[2] else n.attrs.get("max")
+            attrs["clip_min"], attrs["clip_max"] = lo, hi
+            body.append(f"float {out} = {activation_expr('Clip', ref(n.inputs[0]), attrs)};")
+        else:
+            body.append(f"float {out} = {activation_expr(n.op_type, ref(n.inputs[0]), n.attrs)};")
+    in_vars = [_cname(e, names) for e in ext]
+    out_vars = [_cname(o, names) for o in node.outputs]
+    params = [f"const float* __restrict__ p_{v}" for v in in_vars] + \
+             [f"float* __restrict__ q_{v}" for v in out_vars] + ["int N"]
+
+    def lane(idx: str, comp: str = "") -> str:
+        loads = [f"float {v} = p_{v}[{idx}];" if not comp else f"float {v} = l_{v}.{comp};"
+                 for v in in_vars]
+        return " ".join(loads + body)
+
+    quad = []
+    for v in in_vars:
+        quad.append(f"    const float4 l_{v} = mdlc::ld4(p_{v} + 4 * (long long)i);")
+    comps = "xyzw"
+    for o in out_vars:
+        quad.append(f"    float4 s_{o};")
+    for c in comps:
+        stores = " ".join(f"s_{o}.{c} = {o};" for o in out_vars)
+        quad.append(f"    {{ {lane('', c)} {stores} }}")
+    for o in out_vars:
+        quad.append(f"    mdlc::st4(q_{o} + 4 * (long long)i, s_{o});")
+    tail_store = " ".join(f"q_{o}[j] = {o};" for o in out_vars)
+    src = (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}({", ".join(params)}) {{\n'
+        "  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;\n"
+        "  const long long nq = N >> 2;\n"
+        "  if (i < nq) {\n" + "\n".join(quad) + "\n"
+        "  } else {\n"
+        "    const long long j = nq * 4 + (i - nq);\n"
+        f"    if (j < N) {{ {lane('j')} {tail_store} }}\n"
+        "  }\n}\n")
+    return name, src, ext
+
+
+def elementwise_signature(node: Node, scalar_consts: dict) -> tuple:
+    """Structural identity of an elementwise group: two groups with the same
+    signature compile to the same kernel body, so one kernel serves both."""
+    sub = node.attrs["subgraph"]
+    internal = {o for n in sub for o in n.outputs if o}
+    table: dict = {}
+
+    def tag(e: str):
+        if e in scalar_consts:
+            return ("c", float(scalar_consts[e]))
+        if e not in table:
+            table[e] = len(table)
+        return ("v", table[e], e in internal)
+
+    ops = []
+    for n in sub:
+        extra = tuple(sorted((k, v) for k, v in n.attrs.items() if isinstance(v, (int, float, str))))
+        ops.append((n.op_type, tuple(tag(e) for e in n.inputs if e), tag(n.outputs[0]), extra))
+    return tuple(ops), tuple(tag(o) for o in node.outputs)

@@ -1,0 +1,102 @@
+"""GEMM schedules for the CDNA4 matrix-core kernel: the autotuner's knobs.
+
+The reference schedule is a CUDA thread-block tiling (BM, BN, BK, TM, TN;
+mdlc/codegen/schedule.py:16-69). On gfx950 the same role is played by:
+
+* the macro tile BM x BN x BK a workgroup owns,
+* the wave grid WGM x WGN (64-lane wavefronts; the workgroup has
+  64*WGM*WGN threads) and hence the wave tile (BM/WGM) x (BN/WGN),
+* the MFMA shape MS: 32 for v_mfma_f32_32x32x2_f32, 16 for
+  v_mfma_f32_16x16x4_f32 (int8 kernels use 32x32x32 / 16x16x64),
+* LDS double buffering DB (one barrier per K step, twice the LDS).
+
+Validity mirrors the kernel's static requirements; the space is the pruned
+cross product of a few proven values, as in the reference.
+"""
+
+from __future__ import annotations
+
+from dataclasses import asdict, dataclass
+from typing import Iterator
+
+LDS_LIMIT = 64 * 1024          # bytes one workgroup may allocate
+MAX_ACC_REGS = 128             # accumulator registers per lane we allow
+
+
+@dataclass(frozen=True)
+class MfmaSchedule:
+    BM: int = 128
+    BN: int = 128
+    BK: int = 16
+    WGM: int = 2
+    WGN: int = 2
+    MS: int = 32
+    DB: bool = True
+
+    def threads_per_block(self) -> int:
+        return 64 * self.WGM * self.WGN
+
+    def wave_tile(self) -> tuple:
+        return self.BM // self.WGM, self.BN // self.WGN
+
+    def acc_regs(self) -> int:
+        wm, wn = self.wave_tile()
+        per = 16 if self.MS == 32 else 4
+        return (wm // self.MS) * (wn // self.MS) * per
+
+    def lds_bytes(self, elem_bytes: int = 4) -> int:
+        one = self.BM * (self.BK + 4) + self.BK * (self.BN + 4)
+        return (2 if self.DB else 1) * one * elem_bytes
+
+    def is_valid(self) -> bool:
+        if min(self.BM, self.BN, self.BK, self.WGM, self.WGN) <= 0 or self.MS not in (16, 32):
+            return False
+        wm, wn = self.wave_tile()
+        if self.BM % self.WGM or self.BN % self.WGN:
+            return False
+        if wm % self.MS or wn % self.MS:
+            return False
+        kg = 64 // self.MS
+        if self.BK % kg or (self.BK // kg) % 4:
+            return False
+        nt = self.threads_per_block()
+        if nt > 1024 or self.BN % 4 or nt % (self.BN // 4):
+            return False
+        if self.lds_bytes() > LDS_LIMIT or self.acc_regs() > MAX_ACC_REGS:
+            return False
+        return True
+
+    def key(self) -> str:
+        return (f"BM{self.BM}_BN{self.BN}_BK{self.BK}_W{self.WGM}x{self.WGN}"
+                f"_M{self.MS}{'_DB' if self.DB else ''}")
+
+    def as_dict(self) -> dict:
+        return asdict(self)
+
+
+def gemm_search_space() -> Iterator[MfmaSchedule]:
+    for bm in (32, 64, 128, 256):
+        for bn in (32, 64, 128, 256):
+            for bk in (8, 16, 32):
+                for wgm, wgn in ((1, 1), (2, 1), (1, 2), (2, 2), (4, 1), (1, 4), (4, 2), (2, 4)):
+                    for ms in (32, 16):
+                        for db in (True, False):
+                            s = MfmaSchedule(bm, bn, bk, wgm, wgn, ms, db)
+                            if s.is_valid():
+                                yield s
+
+
+DEFAULT_GEMM = MfmaSchedule()
+GemmSchedule = MfmaSchedule
+
+
+def default_schedule(M: int, N: int, K: int) -> MfmaSchedule:
+    """A shape-aware default used when no tuner is supplied: shrink the tile
+    when a dimension is small so quantization waste stays bounded."""
+    bm = 128 if M > 64 else (64 if M > 32 else 32)
+    bn = 128 if N > 64 else (64 if N > 32 else 32)
+    wgm = 2 if bm >= 64 else 1
+    wgn = 2 if bn >= 64 else 1
+    ms = 32 if min(bm // wgm, bn // wgn) >= 32 else 16
+    s = MfmaSchedule(bm, bn, 16, wgm, wgn, ms, True)
+    return s if s.is_valid() else DEFAULT_GEMM

@@ -1,0 +1,79 @@
+"""Compiler driver: IR graph (or ONNX model) -> optimized, lowered HIP module.
+
+Same pipeline as mdlc/compiler.py:64-95 — passes (optionally verified after
+every change), static shapes, memory plan, codegen — with two differences:
+the frontend is optional (``onnx`` is not part of this stack, so an IR
+``Graph`` is accepted directly), and numerical pass verification is
+injected by the caller (``verify``) instead of running a CPU executor inside
+the compiler. Structural verification always runs.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Callable, Optional
+
+from mdlc_amd.codegen.hip.emit import HipModule, emit_hip_module
+from mdlc_amd.ir import Graph, verify_graph
+from mdlc_amd.passes import default_pipeline
+from mdlc_amd.passes.base import PassManager
+from mdlc_amd.passes.shape_inference import infer_shapes, make_dummy_feeds
+from mdlc_amd.runtime.memory_planner import MemoryPlan, plan_memory
+
+
+@dataclass
+class Compiled:
+    original: Graph
+    graph: Graph
+    module: HipModule
+    mem_plan: MemoryPlan
+    passes: PassManager
+    feeds: dict
+    checks: list = field(default_factory=list)
+
+    def report(self) -> str:
+        n_fused = sum(1 for n in self.graph.nodes if n.is_fused)
+        lines = ["== mdlc_amd compile report ==", self.original.summary(), "-> optimized:",
+                 self.graph.summary(), f"  fused groups: {n_fused}", self.passes.report(),
+                 self.module.report(), self.mem_plan.report()]
+        if self.checks:
+            ok = all(c.ok for c in self.checks)
+            lines.append(f"correctness vs golden: {'PASS' if ok else 'FAIL'}")
+            lines += [f"  {c}" for c in self.checks]
+        return "\n".join(lines)
+
+
+def _structural_verifier(extra: Optional[Callable]) -> Callable:
+    def verify(graph: Graph, pass_name: str) -> None:
+        verify_graph(graph, context=pass_name)
+        if extra is not None:
+            extra(graph, pass_name)
+    return verify
+
+
+def compile_graph(graph: Graph, *, batch: int = 1, feeds: Optional[dict] = None,
+                  schedule_fn=None, verify: Optional[Callable] = None,
+                  conv_mode: str = "implicit") -> Compiled:
+    original = graph.clone()
+    if feeds is None:
+        feeds = make_dummy_feeds(graph, batch=batch)
+    pm = default_pipeline(verify=_structural_verifier(verify))
+    graph = pm.run(graph)
+    infer_shapes(graph, feeds)
+    mem_plan = plan_memory(graph)
+    module = emit_hip_module(graph, schedule_fn, conv_mode=conv_mode)
+    return Compiled(original, graph, module, mem_plan, pm, feeds)
+
+
+def compile_onnx(source, **kw) -> Compiled:
+    """Compile an ONNX path/model, or an IR ``Graph``. ONNX input needs the
+    optional ``onnx`` package and an importer; without them pass a Graph."""
+    if isinstance(source, Graph):
+        return compile_graph(source, **kw)
+    try:
+        import onnx  # noqa: F401
+    except ImportError as exc:
+        raise NotImplementedError(
+            "ONNX input needs the `onnx` package, which is not installed; "
+            "build the model as an mdlc_amd.ir.Graph instead") from exc
+    raise NotImplementedError("ONNX import is not part of this backend; pass an IR Graph")

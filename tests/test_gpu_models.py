@@ -1,0 +1,125 @@
+"""Whole-graph device parity: every tensor of every fused group against the
+NumPy oracle.
+
+Two views of each network (the reference compares the whole module against
+its executor, tests/test_end_to_end_sim.py:13-38):
+
+* isolated — every launch group runs on the oracle's values of its inputs,
+  so each group's output is held to rtol 1e-4 / atol 1e-5 by itself;
+* chained — the plan runs end to end on the device; its outputs then carry
+  drift accumulated over ~20 reductions and are held to the network tier.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import build_graph
+from gpu_util import assert_close, device_run
+from mdlc_amd.codegen.hip.hip_executor import HipExecutor
+from mdlc_amd.compiler import compile_graph
+from mdlc_amd.testing import DEVICE_TENSOR, FP32_NETWORK
+from mdlc_amd.tools.build_mobilenetv2 import build_mobilenetv2
+from mdlc_amd.tools.build_resnet18 import build_resnet18, make_input
+from oracle.reference import run_reference
+
+pytestmark = pytest.mark.gpu
+
+
+def test_tiny_models_every_tensor(model_case, hip_ctx):
+    name, kw = model_case
+    g, feeds = build_graph(name, **kw)
+    c, got, want = device_run(g, feeds, ctx=hip_ctx, all_tensors=True)
+    assert c.module.fallbacks() == []
+    for t, v in got.items():
+        assert_close(t, v, want[t], DEVICE_TENSOR, vacuous_ok=True)
+
+
+def _report_ratios(got, want):
+    from mdlc_amd.testing import tolerance_ratio
+
+    worst = sorted(((tolerance_ratio(v, want[t], rtol=DEVICE_TENSOR.rtol, atol=DEVICE_TENSOR.atol), t)
+                    for t, v in got.items()), reverse=True)[:3]
+    print("worst tolerance ratios:", ", ".join(f"{t}={r:.3f}" for r, t in worst))
+
+
+def _isolated(c, feeds, ctx):
+    want = run_reference(c.graph, feeds, return_all=True)
+    ex = HipExecutor(c.module, ctx)
+    try:
+        ex._upload_feeds(feeds)
+        got = ex.run_isolated(want)
+        chained = ex.run(feeds)["outputs"]
+    finally:
+        ex.close()
+    return got, want, chained
+
+
+@pytest.mark.parametrize("batch", [1, 2])
+@pytest.mark.parametrize("mode", ["implicit", "im2col"])
+def test_resnet18_every_group(batch, mode, hip_ctx):
+    g = build_resnet18(batch=batch)
+    feeds = {"input": make_input(batch)}
+    c = compile_graph(g, feeds=feeds, conv_mode=mode)
+    assert c.module.fallbacks() == []
+    got, want, chained = _isolated(c, feeds, hip_ctx)
+    assert len(got) == 32
+    _report_ratios(got, want)
+    for t, v in got.items():
+        assert_close(t, v, want[t], DEVICE_TENSOR)
+    assert_close("logits", chained["logits"], want["logits"], FP32_NETWORK)
+
+
+def test_resnet18_batch32_rows_match_single_images(hip_ctx):
+    """At the benchmark batch the oracle is too slow for every image, so the
+    device's batch-32 logits are checked against the oracle on two images
+    and against the device's own batch-1 runs of every image, a property
+    that holds at any size."""
+    x = make_input(32)
+    c32 = compile_graph(build_resnet18(batch=32), feeds={"input": x})
+    ex = HipExecutor(c32.module, hip_ctx)
+    try:
+        y32 = ex.run({"input": x})["outputs"]["logits"]
+    finally:
+        ex.close()
+    c1 = compile_graph(build_resnet18(batch=1), feeds={"input": x[:1]})
+    ex1 = HipExecutor(c1.module, hip_ctx)
+    try:
+        for i in range(32):
+            yi = ex1.run({"input": x[i:i + 1]})["outputs"]["logits"]
+            assert_close(f"logits[{i}]", y32[i:i + 1], yi, FP32_NETWORK)
+    finally:
+        ex1.close()
+    for i in (0, 31):
+        want = run_reference(c1.graph, {"input": x[i:i + 1]})["logits"]
+        assert_close(f"oracle logits[{i}]", y32[i:i + 1], want, FP32_NETWORK)
+
+
+def test_mobilenetv2_every_group(hip_ctx):
+    g = build_mobilenetv2(batch=1)
+    feeds = {"input": make_input(1, seed=3)}
+    c = compile_graph(g, feeds=feeds)
+    assert c.module.fallbacks() == []
+    got, want, chained = _isolated(c, feeds, hip_ctx)
+    _report_ratios(got, want)
+    for t, v in got.items():
+        assert_close(t, v, want[t], DEVICE_TENSOR)
+    assert_close("logits", chained["logits"], want["logits"], FP32_NETWORK)
+
+
+def test_plan_graph_replay_matches_eager(hip_ctx):
+    """The plan captured as a hipGraph replays to the same result as direct
+    launches, several times with host work in between."""
+    g = build_resnet18(batch=1)
+    x = make_input(1)
+    c = compile_graph(g, feeds={"input": x})
+    ex = HipExecutor(c.module, hip_ctx)
+    try:
+        ref = ex.run({"input": x})["outputs"]["logits"]
+        ex.plan.use_graph(True)
+        for _ in range(3):
+            got = ex.run({"input": x})["outputs"]["logits"]
+            np.testing.assert_array_equal(got, ref)
+    finally:
+        ex.close()
