@@ -1,0 +1,276 @@
+"""Autotuner over MFMA schedules (macro tile, wave grid, MFMA shape, LDS
+double buffering, split-K).
+
+Same roles as the reference tuner (mdlc/autotuner/tuner.py:31-174): an
+analytical cost model ranks candidates without a device; on a device each
+candidate is compiled and timed with HIP events; the best schedule per
+problem is kept in a JSON cache (same entry format: ``{"sched": {...},
+"metric": ..., "measured": ...}``). Two differences:
+
+* Candidates are chosen model-first: the whole valid space is ranked by the
+  cost model and the best ``budget`` are measured, plus a seeded random few
+  and the default, instead of a blind random sample.
+* Convolutions are tuned as the implicit-GEMM kernel they lower to, keyed by
+  their full problem (window, batch, channels), not only by (M, N, K).
+"""
+
+from __future__ import annotations
+
+import json
+import os
+import random
+from dataclasses import dataclass, field
+from typing import Optional
+
+from mdlc_amd.codegen.schedule import (
+    CUS, DEFAULT_GEMM, MfmaSchedule, default_schedule, gemm_search_space, split_slices,
+)
+
+LDS_PER_CU = 160 * 1024
+MFMA_FLOPS_PER_CU_CLK = 256          # fp32 MFMA, dense
+CLOCK_GHZ = 2.4
+HBM_GBS = 8000.0
+LAUNCH_US = 2.0
+SPLITS = (1, 2, 4, 8)
+
+
+def analytical_cost(sched: MfmaSchedule, M: int, N: int, K: int) -> float:
+    """Estimated microseconds (lower is better) for one GEMM with this schedule.
+
+    * Occupancy: workgroups resident per CU, limited by LDS, by 8 waves per
+      SIMD, and by the accumulator registers; the grid runs in rounds of
+      (CUs x resident) workgroups — tile quantization shows up as a partial
+      last round.
+    * Compute per round: the tile's MFMA flops at the per-CU rate, derated
+      when fewer than 2 waves per SIMD are resident (no one to hide latency).
+    * Memory: A re-read once per column tile and B once per row tile, at
+      HBM bandwidth, overlapped with compute.
+    * Split-K adds the workspace round trip and a second launch.
+    """
+    slices, chunk = split_slices(K, sched)
+    tiles = -(-M // sched.BM) * -(-N // sched.BN)
+    wgs = tiles * slices
+    waves = sched.WGM * sched.WGN
+    by_lds = max(1, LDS_PER_CU // sched.lds_bytes())
+    vgprs = 64 + sched.acc_regs() + 32
+    by_regs = max(1, (512 // vgprs) * 4 // waves)
+    resident = max(1, min(by_lds, by_regs, 32 // waves))
+    rounds = -(-wgs // (CUS * resident))
+    per_cu = min(resident, -(-wgs // CUS))
+    waves_per_simd = per_cu * waves / 4.0
+    eff = min(1.0, 0.35 + 0.3 * waves_per_simd)
+    kp = -(-chunk // sched.BK) * sched.BK
+    wg_flops = 2.0 * sched.BM * sched.BN * kp
+    round_us = wg_flops * per_cu / (MFMA_FLOPS_PER_CU_CLK * CLOCK_GHZ * 1e3) / eff
+    compute = rounds * round_us
+    traffic = 4.0 * (-(-N // sched.BN) * M * K + -(-M // sched.BM) * K * N)
+    memory = traffic / (HBM_GBS * 1e3)
+    t = max(compute, memory) + LAUNCH_US
+    if slices > 1:
+        t += 4.0 * (slices + 1) * M * N / (HBM_GBS * 1e3) + LAUNCH_US
+    return t
+
+
+def problem_key(problem: dict) -> str:
+    M, N, K = problem["M"], problem["N"], problem["K"]
+    if problem.get("kind") == "conv":
+        return (f"conv:{M}x{N}x{K}:{problem['KH']}x{problem['KW']}s{problem['SH']}"
+                f":{problem['C']}x{problem['H']}x{problem['W']}:{problem.get('mode', 'implicit')}")
+    return f"{M}x{N}x{K}"
+
+
+@dataclass
+class TuneResult:
+    key: str
+    best: MfmaSchedule
+    best_metric: float
+    measured: bool
+    n_evaluated: int
+    ranking: list = field(default_factory=list)
+
+
+class AutotuneCache:
+    """Best schedule per problem, persisted as JSON."""
+
+    def __init__(self, path: Optional[str] = None) -> None:
+        self.path = path
+        self.entries: dict = {}
+        if path and os.path.exists(path):
+            with open(path) as f:
+                self.entries = json.load(f)
+
+    @staticmethod
+    def key(M, N, K) -> str:
+        return f"{M}x{N}x{K}"
+
+    def get_key(self, key: str) -> Optional[MfmaSchedule]:
+        e = self.entries.get(key)
+        return None if not e else MfmaSchedule(**e["sched"])
+
+    def get(self, M, N, K) -> Optional[MfmaSchedule]:
+        return self.get_key(self.key(M, N, K))
+
+    def put_key(self, key: str, sched: MfmaSchedule, metric: float, measured: bool) -> None:
+        self.entries[key] = {"sched": sched.as_dict(), "metric": metric, "measured": measured}
+
+    def put(self, M, N, K, sched: MfmaSchedule, metric: float, measured: bool) -> None:
+        self.put_key(self.key(M, N, K), sched, metric, measured)
+
+    def save(self, path: Optional[str] = None) -> None:
+        path = path or self.path
+        os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+        with open(path, "w") as f:
+            json.dump(self.entries, f, indent=1, sort_keys=True)
+
+
+def candidates(M: int, N: int, K: int, *, budget: int = 24, seed: int = 0, extra_random: int = 4) -> list:
+    """The ``budget`` best schedules by the cost model, a seeded random few
+    more, and the shape-aware default."""
+    space = list(gemm_search_space(SPLITS))
+    space = [s for s in space if split_slices(K, s)[0] == s.SK or s.SK == 1]
+    ranked = sorted(space, key=lambda s: analytical_cost(s, M, N, K))
+    pick = ranked[:budget]
+    rest = ranked[budget:]
+    rng = random.Random(seed)
+    pick += rng.sample(rest, min(extra_random, len(rest)))
+    d = default_schedule(M, N, K)
+    if d not in pick:
+        pick.append(d)
+    return pick
+
+
+def _problem_graph(problem: dict, sched_seed: int = 0):
+    """A one-group graph (and feeds) that lowers to exactly this problem."""
+    import numpy as np
+
+    from mdlc_amd.tools.graph_builder import GraphBuilder
+
+    rng = np.random.default_rng(sched_seed)
+    b = GraphBuilder("tune")
+    if problem["kind"] == "conv":
+        n, c, h, w = problem["batch"], problem["C"], problem["H"], problem["W"]
+        oc, kh, kw = problem["M"], problem["KH"], problem["KW"]
+        b.input("x", (n, c, h, w))
+        b.const("w", (rng.standard_normal((oc, c, kh, kw)) / np.sqrt(c * kh * kw)).astype(np.float32))
+        ins = ["x", "w"]
+        if problem.get("bias"):
+            b.const("b", rng.standard_normal(oc).astype(np.float32))
+            ins.append("b")
+        out = "y" if not problem.get("act") else "pre"
+        b.node("Conv", ins, out, kernel_shape=[kh, kw], strides=[problem["SH"], problem["SW"]],
+               dilations=[problem["DH"], problem["DW"]],
+               pads=[problem["PT"], problem["PL"], problem["PB"], problem["PR"]])
+        if problem.get("act"):
+            b.node(problem["act"], [out], "y")
+        b.output("y")
+        feeds = {"x": rng.standard_normal((n, c, h, w)).astype(np.float32)}
+    else:
+        M, N, K = problem["M"], problem["N"], problem["K"]
+        b.input("A", (M, K))
+        b.const("B", rng.standard_normal((K, N)).astype(np.float32))
+        b.node("Gemm", ["A", "B"], "y")
+        b.output("y")
+        feeds = {"A": rng.standard_normal((M, K)).astype(np.float32)}
+    return b.graph(), feeds
+
+
+def _compile_for(problem: dict, sched: MfmaSchedule):
+    from mdlc_amd.compiler import compile_graph
+
+    g, feeds = _problem_graph(problem)
+    c = compile_graph(g, feeds=feeds, schedule_fn=lambda node, mnk: sched,
+                      conv_mode=problem.get("mode", "implicit"))
+    return c, feeds
+
+
+def precompile(problem: dict, sched: MfmaSchedule) -> None:
+    """Compile the candidate's module into the code-object cache (no device)."""
+    from mdlc_amd.codegen.hip.hiprtc_runtime import compile_code_object
+
+    c, _ = _compile_for(problem, sched)
+    compile_code_object(c.module.sources())
+
+
+def measure(problem: dict, sched: MfmaSchedule, ctx, *, iters: int = 20, warmup: int = 3) -> float:
+    """Device time (ms) of one run of the problem's launches with ``sched``."""
+    from mdlc_amd.codegen.hip.hip_executor import HipExecutor
+
+    c, feeds = _compile_for(problem, sched)
+    ex = HipExecutor(c.module, ctx)
+    try:
+        ex._upload_feeds(feeds)
+        return ex.plan.time_ms(warmup, iters)
+    finally:
+        ex.close()
+
+
+def tune_problem(problem: dict, *, budget: int = 24, ctx=None, seed: int = 0) -> TuneResult:
+    M, N, K = problem["M"], problem["N"], problem["K"]
+    cands = candidates(M, N, K, budget=budget, seed=seed)
+    scored = []
+    for s in cands:
+        if ctx is not None:
+            try:
+                metric = measure(problem, s, ctx)
+            except Exception:
+                continue
+        else:
+            metric = analytical_cost(s, M, N, K)
+        scored.append((s, metric))
+    scored.sort(key=lambda t: t[1])
+    best, best_metric = scored[0]
+    return TuneResult(problem_key(problem), best, best_metric, ctx is not None, len(scored),
+                      [(s.key_full(), m) for s, m in scored])
+
+
+def tune_gemm(M: int, N: int, K: int, *, budget: int = 24, ctx=None, seed: int = 0) -> TuneResult:
+    """Tune a plain GEMM (activation A, constant B) of shape (M, N, K)."""
+    return tune_problem({"kind": "gemm", "M": M, "N": N, "K": K}, budget=budget, ctx=ctx, seed=seed)
+
+
+class Tuner:
+    """A cache-backed schedule source usable as the codegen's ``schedule_fn``.
+
+    A cache hit is returned as is; a miss is tuned (measured when ``ctx`` is
+    given, else by the cost model) and recorded.
+    """
+
+    def __init__(self, cache: Optional[AutotuneCache] = None, ctx=None, budget: int = 24,
+                 tune_misses: bool = True) -> None:
+        self.cache = cache or AutotuneCache()
+        self.ctx = ctx
+        self.budget = budget
+        self.tune_misses = tune_misses
+
+    def schedule_problem(self, problem: dict) -> MfmaSchedule:
+        key = problem_key(problem)
+        hit = self.cache.get_key(key)
+        if hit is not None and hit.is_valid():
+            return hit
+        if not self.tune_misses:
+            return default_schedule(problem["M"], problem["N"], problem["K"])
+        res = tune_problem(problem, budget=self.budget, ctx=self.ctx)
+        self.cache.put_key(key, res.best, res.best_metric, res.measured)
+        return res.best
+
+    def schedule_for(self, node, mnk) -> MfmaSchedule:
+        M, N, K = mnk
+        return self.schedule_problem({"kind": "gemm", "M": M, "N": N, "K": K})
+
+    def __call__(self, node, mnk) -> MfmaSchedule:
+        return self.schedule_for(node, mnk)
+
+
+TUNED_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tuned_gfx950.json")
+
+
+def tuned_schedules() -> Tuner:
+    """The shipped measured schedules for gfx950 (cache misses fall back to
+    the shape-aware default without tuning)."""
+    return Tuner(AutotuneCache(TUNED_PATH if os.path.exists(TUNED_PATH) else None),
+                 tune_misses=False)
+
+
+__all__ = ["AutotuneCache", "Tuner", "TuneResult", "analytical_cost", "candidates", "measure",
+           "precompile", "problem_key", "tune_gemm", "tune_problem", "tuned_schedules",
+           "DEFAULT_GEMM"]

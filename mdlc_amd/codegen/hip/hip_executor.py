@@ -75,11 +75,17 @@ class HipExecutor:
             self.shapes[t] = tuple(info.shape)
             self.dtypes[t] = DType.to_numpy(info.dtype)
         cur = act_base + self.mem_plan.arena_bytes
-        scratch = max([r * ld * 4 for r, ld in module.scratch_shapes.values()] + [0])
+        regions: dict = {}
         for name, (r, ld) in module.scratch_shapes.items():
-            self.offsets[name] = cur
+            cls = module.scratch_class.get(name, "cols")
+            regions[cls] = max(regions.get(cls, 0), r * ld * 4)
+        region_at: dict = {}
+        for cls in sorted(regions):
+            region_at[cls] = cur
+            cur += align_up(regions[cls])
+        for name, (r, ld) in module.scratch_shapes.items():
+            self.offsets[name] = region_at[module.scratch_class.get(name, "cols")]
             self.shapes[name], self.dtypes[name] = (r, ld), np.dtype(np.float32)
-        cur += align_up(scratch)
         self.arena_bytes = cur
         self.arena = self.ctx.malloc(max(cur, 256))
         self.base = int(self.arena.value)
@@ -107,11 +113,14 @@ class HipExecutor:
         if k == "gemm":
             args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
             args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["ldb"]), I(m["ldc"]),
-                     I(m["hw"])]
+                     I(m["hw"]), I(m["ksplit"]), I(m["kchunk"])]
         elif k == "conv":
             args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
             args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["Cin"]), I(m["H"]),
-                     I(m["W"]), I(m["OH"]), I(m["OW"])]
+                     I(m["W"]), I(m["OH"]), I(m["OW"]), I(m["ksplit"]), I(m["kchunk"])]
+        elif k == "splitk_reduce":
+            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+            args += [I(m["S"]), I(m["M"]), I(m["N"]), I(m["ldc"]), I(m["hw"])]
         elif k == "im2col":
             args = [P(l.inputs[0]), P(l.outputs[0])]
             args += [I(m[f]) for f in ("C", "H", "W", "KH", "KW", "OH", "OW", "SH", "SW",

@@ -8,7 +8,10 @@
 // (B[k][p] = x[n][c][oh*SH-PT+kh*DH][ow*SW-PL+kw*DW], zero outside), so a
 // convolution needs no column buffer. The output is row-major C[M][ldc]
 // (OUT = 0) or, for convolutions, NCHW: column p = n*hw + s goes to
-// C[(n*M + row)*hw + s] (OUT = 1).
+// C[(n*M + row)*hw + s] (OUT = 1). With split-K (OUT = 2) the grid holds
+// ksplit slices of K; slice s writes its raw partial sums to the workspace
+// C[(s*M + row)*N + col] and splitk_reduce_f32 adds the slices in order and
+// applies the epilogue.
 //
 // Tiling: a workgroup of WGM x WGN waves (64 lanes each) owns a BM x BN tile;
 // each wave owns (BM/WGM) x (BN/WGN) as a grid of MS x MS MFMA blocks
@@ -56,6 +59,7 @@ struct GemmArgs {
   float* __restrict__ C;
   int M, N, K, lda, ldb, ldc, hw;
   int Cin, H, W, OH, OW;         // conv input / output geometry (BMODE == 2)
+  int ksplit, kchunk;            // K slices (grid = tiles * ksplit) and slice depth
 };
 
 template <int BM, int BN, int BK, int WGM, int WGN, int MS, bool DB, bool VA, int BMODE, int OUT,
@@ -86,9 +90,16 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
 
   const int tiles_m = (g.M + BM - 1) / BM;
   const int tiles_n = (g.N + BN - 1) / BN;
-  const int t = xcd_remap(blockIdx.x, tiles_m * tiles_n);
-  const int m0 = (t % tiles_m) * BM;
-  const int n0 = (t / tiles_m) * BN;
+  const int tiles = tiles_m * tiles_n;
+  // Logical order (slice, n-block, m-block), m fastest: workgroups sharing a
+  // B slab are consecutive and land on the same XCD.
+  const int t = xcd_remap(blockIdx.x, tiles * g.ksplit);
+  const int ks = t / tiles;
+  const int tt = t - ks * tiles;
+  const int m0 = (tt % tiles_m) * BM;
+  const int n0 = (tt / tiles_m) * BN;
+  const int kbeg = ks * g.kchunk;
+  const int kend = min(g.K, kbeg + g.kchunk);
 
   // ---- A tile staging ----------------------------------------------------
   constexpr int A_ELEMS = VA ? BM * BK / 4 : BM * BK;
@@ -137,7 +148,7 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
         if (idx < A_ELEMS) {
           int r = idx / (BK / 4), kq = idx % (BK / 4);
           int gm = m0 + r, gk = k0 + kq * 4;
-          if (gm < g.M && gk < g.K) v = ld4(g.A + (size_t)gm * g.lda + gk);
+          if (gm < g.M && gk < kend) v = ld4(g.A + (size_t)gm * g.lda + gk);
         }
         ra[i] = v;
       }
@@ -149,7 +160,7 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
         if (idx < A_ELEMS) {
           int r = idx / BK, kk = idx % BK;
           int gm = m0 + r, gk = k0 + kk;
-          if (gm < g.M && gk < g.K) v = g.A[(size_t)gm * g.lda + gk];
+          if (gm < g.M && gk < kend) v = g.A[(size_t)gm * g.lda + gk];
         }
         rs[i] = v;
       }
@@ -162,7 +173,7 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
         if (idx < B_ELEMS) {
           int kr = idx / (BN / 4), nq = idx % (BN / 4);
           int gk = k0 + kr, gn = n0 + nq * 4;
-          if (gk < g.K && gn < g.N) v = ld4(g.B + (size_t)gk * g.ldb + gn);
+          if (gk < kend && gn < g.N) v = ld4(g.B + (size_t)gk * g.ldb + gn);
         }
         rb[i] = v;
       }
@@ -174,7 +185,7 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
         if (idx < B_ELEMS) {
           int kr = idx / BN, nn = idx % BN;
           int gk = k0 + kr, gn = n0 + nn;
-          if (gk < g.K && gn < g.N) v = g.B[(size_t)gk * g.ldb + gn];
+          if (gk < kend && gn < g.N) v = g.B[(size_t)gk * g.ldb + gn];
         }
         rbs[i] = v;
       }
@@ -188,7 +199,7 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
         if (idx < B_ELEMS) {
           int kr = idx / (BN / 4);
           int k = k0 + kr;
-          if (k < g.K) {
+          if (k < kend) {
             int c = k / KHW;
             int rr = k - c * KHW;
             int kh = rr / Win::KW;
@@ -277,21 +288,21 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
     }
   };
 
-  const int nk = (g.K + BK - 1) / BK;
+  const int nk = (kend - kbeg + BK - 1) / BK;
   if (DB) {
-    load_tiles(0);
+    load_tiles(kbeg);
     store_tiles(0);
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
       const int cur = kt & 1;
-      if (kt + 1 < nk) load_tiles((kt + 1) * BK);
+      if (kt + 1 < nk) load_tiles(kbeg + (kt + 1) * BK);
       compute(cur);
       if (kt + 1 < nk) store_tiles(cur ^ 1);
       __syncthreads();
     }
   } else {
     for (int kt = 0; kt < nk; ++kt) {
-      load_tiles(kt * BK);
+      load_tiles(kbeg + kt * BK);
       store_tiles(0);
       __syncthreads();
       compute(0);
@@ -306,7 +317,10 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
     if (col >= g.N) continue;
     size_t cofs;
     int rstride;
-    if (OUT == 1) {
+    if (OUT == 2) {
+      cofs = (size_t)ks * g.M * g.N + col;
+      rstride = g.N;
+    } else if (OUT == 1) {
       int n = col / g.hw;
       int s = col - n * g.hw;
       cofs = (size_t)n * g.M * g.hw + s;
@@ -315,17 +329,46 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
       cofs = col;
       rstride = g.ldc;
     }
-    const float bcol = (Epi::bias == 2) ? g.bias[col] : 0.f;
+    const float bcol = (OUT != 2 && Epi::bias == 2) ? g.bias[col] : 0.f;
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
       for (int r = 0; r < Mfma<MS>::kAcc; ++r) {
         const int row = m0 + wm0 + mi * MS + (r / 4) * 8 + lk * 4 + (r % 4);
         if (row < g.M) {
-          const float bv = (Epi::bias == 1) ? g.bias[row] : bcol;
-          g.C[cofs + (size_t)row * rstride] = Epi::apply(acc[mi][ni][r], bv);
+          if (OUT == 2) {
+            g.C[cofs + (size_t)row * rstride] = acc[mi][ni][r];
+          } else {
+            const float bv = (Epi::bias == 1) ? g.bias[row] : bcol;
+            g.C[cofs + (size_t)row * rstride] = Epi::apply(acc[mi][ni][r], bv);
+          }
         }
       }
+  }
+}
+
+// Split-K epilogue: out = epi(sum_s ws[s][row][col], bias) with the slices
+// added in slice order, written row-major (ldc) or NCHW (hw > 0). One thread
+// per output element, consecutive threads on consecutive columns.
+template <class Epi>
+__device__ __forceinline__ void splitk_reduce_f32(const float* __restrict__ ws,
+                                                  const float* __restrict__ bias,
+                                                  float* __restrict__ C, int S, int M, int N,
+                                                  int ldc, int hw) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)M * N) return;
+  const int row = (int)(i / N);
+  const int col = (int)(i - (long long)row * N);
+  float v = ws[i];
+  for (int s = 1; s < S; ++s) v = v + ws[(size_t)s * M * N + i];
+  const float b = Epi::bias == 1 ? bias[row] : (Epi::bias == 2 ? bias[col] : 0.f);
+  v = Epi::apply(v, b);
+  if (hw > 0) {
+    const int n = col / hw;
+    const int sidx = col - n * hw;
+    C[((size_t)n * M + row) * hw + sidx] = v;
+  } else {
+    C[(size_t)row * ldc + col] = v;
   }
 }
 

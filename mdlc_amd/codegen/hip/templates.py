@@ -100,39 +100,67 @@ def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: s
     """(name, source) of one GEMM instantiation.
 
     Kernel ABI (the reference's gemm ABI plus trailing layout arguments):
-      dense  (bmode 0/1): (A, B, [bias], C, int M, int N, int K, int lda, int ldb, int ldc, int hw)
+      dense  (bmode 0/1): (A, B, [bias], C, int M, int N, int K, int lda, int ldb, int ldc,
+                           int hw, int ksplit, int kchunk)
       conv   (bmode 2)  : (W, x, [bias], y, int M, int N, int K, int lda,
-                           int Cin, int H, int W, int OH, int OW)
-    ``hw`` > 0 selects the NCHW output scatter for conv-as-GEMM.
+                           int Cin, int H, int W, int OH, int OW, int ksplit, int kchunk)
+    ``hw`` > 0 selects the NCHW output scatter for conv-as-GEMM. With
+    ``sched.SK > 1`` the kernel writes raw partial sums of each K slice to
+    its C argument (the split-K workspace) and takes no bias argument; the
+    epilogue then lives in ``splitk_reduce_kernel``.
     """
     attrs = attrs or {}
     s = sched
+    split = s.SK > 1
+    if split:
+        with_bias = False
     epi = f"{name}_epi"
     src = [epilogue_struct(epi, bias_mode=bias_mode if with_bias else None,
-                           activation=activation, attrs=attrs, alpha=alpha, beta=beta)]
+                           activation=None if split else activation, attrs=attrs,
+                           alpha=1.0 if split else alpha, beta=beta)]
     winty = "mdlc::NoWin" if win is None else "mdlc::ConvWin<%d, %d, %d, %d, %d, %d, %d, %d>" % tuple(win)
     bias_arg = "const float* __restrict__ bias, " if with_bias else ""
     bias_val = "bias" if with_bias else "nullptr"
+    out = 2 if split else (1 if out_nchw else 0)
     tmpl = (f"mdlc::gemm_f32_mfma<{s.BM}, {s.BN}, {s.BK}, {s.WGM}, {s.WGN}, {s.MS}, "
             f"{'true' if s.DB else 'false'}, {'true' if vec_a else 'false'}, {bmode}, "
-            f"{1 if out_nchw else 0}, {epi}, {winty}>")
+            f"{out}, {epi}, {winty}>")
     nt = s.threads_per_block()
     if bmode == 2:
         src.append(
             f'extern "C" __global__ __launch_bounds__({nt}) void {name}(\n'
             f"    const float* __restrict__ A, const float* __restrict__ x, {bias_arg}"
             f"float* __restrict__ y,\n    int M, int N, int K, int lda, int Cin, int H, int W, "
-            f"int OH, int OW) {{\n"
-            f"  mdlc::GemmArgs g{{A, x, {bias_val}, y, M, N, K, lda, 0, 0, OH * OW, Cin, H, W, OH, OW}};\n"
+            f"int OH, int OW, int ksplit, int kchunk) {{\n"
+            f"  mdlc::GemmArgs g{{A, x, {bias_val}, y, M, N, K, lda, 0, 0, OH * OW, Cin, H, W, OH, OW, "
+            f"ksplit, kchunk}};\n"
             f"  {tmpl}(g);\n}}\n")
     else:
         src.append(
             f'extern "C" __global__ __launch_bounds__({nt}) void {name}(\n'
             f"    const float* __restrict__ A, const float* __restrict__ B, {bias_arg}"
-            f"float* __restrict__ C,\n    int M, int N, int K, int lda, int ldb, int ldc, int hw) {{\n"
-            f"  mdlc::GemmArgs g{{A, B, {bias_val}, C, M, N, K, lda, ldb, ldc, hw, 0, 0, 0, 0, 0}};\n"
+            f"float* __restrict__ C,\n    int M, int N, int K, int lda, int ldb, int ldc, int hw, "
+            f"int ksplit, int kchunk) {{\n"
+            f"  mdlc::GemmArgs g{{A, B, {bias_val}, C, M, N, K, lda, ldb, ldc, hw, 0, 0, 0, 0, 0, "
+            f"ksplit, kchunk}};\n"
             f"  {tmpl}(g);\n}}\n")
     return name, "\n".join(src)
+
+
+def splitk_reduce_kernel(name: str, *, with_bias: bool, bias_mode: str,
+                         activation: Optional[str], attrs: dict, alpha: float = 1.0,
+                         beta: float = 1.0) -> tuple:
+    """Split-K epilogue. ABI: (ws, [bias], C, int S, int M, int N, int ldc, int hw)."""
+    epi = f"{name}_epi"
+    src = epilogue_struct(epi, bias_mode=bias_mode if with_bias else None, activation=activation,
+                          attrs=attrs, alpha=alpha, beta=beta)
+    bias_arg = "const float* __restrict__ bias, " if with_bias else ""
+    return name, src + (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        f"    const float* __restrict__ ws, {bias_arg}float* __restrict__ C, int S, int M, int N,\n"
+        "    int ldc, int hw) {\n"
+        f"  mdlc::splitk_reduce_f32<{epi}>(ws, {'bias' if with_bias else 'nullptr'}, C, S, M, N, "
+        "ldc, hw);\n}\n")
 
 
 def im2col_kernel(name: str = "im2col") -> tuple:

@@ -8,7 +8,11 @@ mdlc/codegen/schedule.py:16-69). On gfx950 the same role is played by:
   64*WGM*WGN threads) and hence the wave tile (BM/WGM) x (BN/WGN),
 * the MFMA shape MS: 32 for v_mfma_f32_32x32x2_f32, 16 for
   v_mfma_f32_16x16x4_f32 (int8 kernels use 32x32x32 / 16x16x64),
-* LDS double buffering DB (one barrier per K step, twice the LDS).
+* LDS double buffering DB (one barrier per K step, twice the LDS),
+* split-K SK: the K range is cut into SK slices computed by separate
+  workgroups into a workspace, then reduced in slice order by an epilogue
+  kernel — for deep layers whose M x N alone gives too few workgroups to
+  fill 256 CUs.
 
 Validity mirrors the kernel's static requirements; the space is the pruned
 cross product of a few proven values, as in the reference.
@@ -32,6 +36,7 @@ class MfmaSchedule:
     WGN: int = 2
     MS: int = 32
     DB: bool = True
+    SK: int = 1
 
     def threads_per_block(self) -> int:
         return 64 * self.WGM * self.WGN
@@ -49,7 +54,7 @@ class MfmaSchedule:
         return (2 if self.DB else 1) * one * elem_bytes
 
     def is_valid(self) -> bool:
-        if min(self.BM, self.BN, self.BK, self.WGM, self.WGN) <= 0 or self.MS not in (16, 32):
+        if min(self.BM, self.BN, self.BK, self.WGM, self.WGN, self.SK) <= 0 or self.MS not in (16, 32):
             return False
         wm, wn = self.wave_tile()
         if self.BM % self.WGM or self.BN % self.WGN:
@@ -70,33 +75,66 @@ class MfmaSchedule:
         return (f"BM{self.BM}_BN{self.BN}_BK{self.BK}_W{self.WGM}x{self.WGN}"
                 f"_M{self.MS}{'_DB' if self.DB else ''}")
 
+    def key_full(self) -> str:
+        return self.key() + (f"_SK{self.SK}" if self.SK > 1 else "")
+
+    def with_split(self, sk: int) -> "MfmaSchedule":
+        return MfmaSchedule(self.BM, self.BN, self.BK, self.WGM, self.WGN, self.MS, self.DB, sk)
+
     def as_dict(self) -> dict:
         return asdict(self)
 
 
-def gemm_search_space() -> Iterator[MfmaSchedule]:
+def gemm_search_space(splits=(1,)) -> Iterator[MfmaSchedule]:
     for bm in (32, 64, 128, 256):
         for bn in (32, 64, 128, 256):
             for bk in (8, 16, 32):
                 for wgm, wgn in ((1, 1), (2, 1), (1, 2), (2, 2), (4, 1), (1, 4), (4, 2), (2, 4)):
                     for ms in (32, 16):
                         for db in (True, False):
-                            s = MfmaSchedule(bm, bn, bk, wgm, wgn, ms, db)
-                            if s.is_valid():
-                                yield s
+                            for sk in splits:
+                                s = MfmaSchedule(bm, bn, bk, wgm, wgn, ms, db, sk)
+                                if s.is_valid():
+                                    yield s
+
+
+def split_slices(K: int, sched: MfmaSchedule) -> tuple:
+    """(slices, chunk): K cut into chunks that are multiples of BK, with no
+    empty slice."""
+    if sched.SK <= 1:
+        return 1, K
+    chunk = -(-K // sched.SK)
+    chunk = -(-chunk // sched.BK) * sched.BK
+    return -(-K // chunk), chunk
 
 
 DEFAULT_GEMM = MfmaSchedule()
 GemmSchedule = MfmaSchedule
 
 
+CUS = 256
+
+
 def default_schedule(M: int, N: int, K: int) -> MfmaSchedule:
-    """A shape-aware default used when no tuner is supplied: shrink the tile
-    when a dimension is small so quantization waste stays bounded."""
+    """A shape-aware default used when no tuned entry exists: shrink the
+    tile until the grid covers the chip twice (or the tile is 64x64), then
+    split K while slices stay at least 256 deep and the grid is short of
+    two workgroups per CU."""
     bm = 128 if M > 64 else (64 if M > 32 else 32)
     bn = 128 if N > 64 else (64 if N > 32 else 32)
+    tiles = lambda: -(-M // bm) * -(-N // bn)  # noqa: E731
+    while tiles() < 2 * CUS and (bm > 64 or bn > 64):
+        if bm >= bn and bm > 64:
+            bm //= 2
+        elif bn > 64:
+            bn //= 2
+        else:
+            bm //= 2
+    sk = 1
+    while tiles() * sk < 2 * CUS and K // (2 * sk) >= 256 and sk < 8:
+        sk *= 2
     wgm = 2 if bm >= 64 else 1
     wgn = 2 if bn >= 64 else 1
     ms = 32 if min(bm // wgm, bn // wgn) >= 32 else 16
-    s = MfmaSchedule(bm, bn, 16, wgm, wgn, ms, True)
+    s = MfmaSchedule(bm, bn, 16, wgm, wgn, ms, True, sk)
     return s if s.is_valid() else DEFAULT_GEMM

@@ -1,0 +1,102 @@
+"""Tune the MFMA schedules of every GEMM/conv problem in a model.
+
+    python -m mdlc_amd.tools.tune --model resnet18 --batch 32 --precompile   # CPU: fill the code-object cache
+    python -m mdlc_amd.tools.tune --model resnet18 --batch 32                # device: measure, write JSON
+
+The first form needs no GPU: hipRTC compiles every candidate module into the
+on-disk code-object cache, so the measuring run on the device spends its
+time timing rather than compiling. Results merge into
+``mdlc_amd/autotuner/tuned_gfx950.json`` (or ``--out``).
+"""
+
+from __future__ import annotations
+
+import argparse
+import sys
+import time
+from concurrent.futures import ProcessPoolExecutor
+
+from mdlc_amd.autotuner.tuner import (
+    TUNED_PATH, AutotuneCache, candidates, precompile, problem_key, tune_problem,
+)
+from mdlc_amd.codegen.schedule import default_schedule
+
+
+class _Recorder:
+    def __init__(self) -> None:
+        self.problems: dict = {}
+
+    def schedule_problem(self, problem: dict):
+        self.problems.setdefault(problem_key(problem), dict(problem))
+        return default_schedule(problem["M"], problem["N"], problem["K"])
+
+    def __call__(self, node, mnk):
+        return default_schedule(*mnk)
+
+
+def model_problems(model: str, batch: int, conv_mode: str) -> list:
+    from mdlc_amd.compiler import compile_graph
+
+    if model == "resnet18":
+        from mdlc_amd.tools.build_resnet18 import build_resnet18 as build
+    elif model == "mobilenetv2":
+        from mdlc_amd.tools.build_mobilenetv2 import build_mobilenetv2 as build
+    else:
+        raise SystemExit(f"unknown model {model!r}")
+    rec = _Recorder()
+    compile_graph(build(batch=batch, calibrate=False), batch=batch, schedule_fn=rec,
+                  conv_mode=conv_mode)
+    return list(rec.problems.values())
+
+
+def _precompile_one(args):
+    problem, sched = args
+    precompile(problem, sched)
+    return 1
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--model", default="resnet18")
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--conv-mode", default="implicit")
+    ap.add_argument("--budget", type=int, default=24)
+    ap.add_argument("--precompile", action="store_true")
+    ap.add_argument("--jobs", type=int, default=8)
+    ap.add_argument("--out", default=TUNED_PATH)
+    ap.add_argument("--only", default="", help="substring filter on problem keys")
+    args = ap.parse_args(argv)
+
+    probs = [p for p in model_problems(args.model, args.batch, args.conv_mode)
+             if args.only in problem_key(p)]
+    print(f"{len(probs)} problems", flush=True)
+    if args.precompile:
+        work = [(p, s) for p in probs for s in candidates(p["M"], p["N"], p["K"], budget=args.budget)]
+        t0 = time.time()
+        with ProcessPoolExecutor(args.jobs) as pool:
+            for i, _ in enumerate(pool.map(_precompile_one, work, chunksize=2), 1):
+                if i % 25 == 0:
+                    print(f"  compiled {i}/{len(work)} ({time.time() - t0:.0f} s)", flush=True)
+        print(f"precompiled {len(work)} candidate modules in {time.time() - t0:.0f} s")
+        return 0
+
+    from mdlc_amd.codegen.hip.hiprtc_runtime import HipContext
+
+    ctx = HipContext(0)
+    cache = AutotuneCache(args.out)
+    for p in probs:
+        t0 = time.time()
+        res = tune_problem(p, budget=args.budget, ctx=ctx)
+        d = default_schedule(p["M"], p["N"], p["K"]).key_full()
+        dflt = next((m for k, m in res.ranking if k == d), float("nan"))
+        cache.put_key(res.key, res.best, res.best_metric, True)
+        cache.save()
+        flops = 2.0 * p["M"] * p["N"] * p["K"]
+        print(f"{res.key:48s} best {res.best.key_full():40s} {res.best_metric * 1e3:9.1f} us "
+              f"({flops / res.best_metric / 1e9:6.1f} TFLOP/s; default {dflt * 1e3:9.1f} us) "
+              f"[{res.n_evaluated} cands, {time.time() - t0:.1f} s]", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

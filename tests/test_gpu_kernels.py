@@ -29,6 +29,8 @@ SCHEDULES = [
     MfmaSchedule(64, 64, 16, 2, 2, 16, True),         # 16x16x4 MFMA
     MfmaSchedule(128, 64, 32, 2, 2, 16, False),       # single buffered
     MfmaSchedule(256, 128, 16, 4, 2, 32, True),
+    MfmaSchedule(64, 64, 16, 2, 2, 32, True, 3),       # split-K, ragged last slice
+    MfmaSchedule(32, 32, 16, 1, 1, 16, True, 2),       # split-K with 16x16x4
 ]
 
 
@@ -118,6 +120,19 @@ def test_conv_matches_oracle(case, mode, hip_ctx):
     g, feeds = _conv_graph(*case)
     c, got, want = device_run(g, feeds, conv_mode=mode, ctx=hip_ctx)
     assert [n.op_type for n in c.graph.nodes] == ["FusedConvAct"]
+    assert_close("y", got["y"], want["y"])
+
+
+@pytest.mark.parametrize("mode", ["implicit", "im2col"])
+@pytest.mark.parametrize("sk", [2, 4])
+@pytest.mark.parametrize("case", [CONV_CASES[2], CONV_CASES[4], CONV_CASES[6]],
+                         ids=lambda c: "x".join(map(str, c)))
+def test_conv_split_k(case, sk, mode, hip_ctx):
+    sched = MfmaSchedule(64, 64, 16, 2, 2, 32, True, sk)
+    g, feeds = _conv_graph(*case)
+    c, got, want = device_run(g, feeds, conv_mode=mode, ctx=hip_ctx,
+                              schedule_fn=lambda n, mnk: sched)
+    assert any(l.kind == "splitk_reduce" for l in c.module.plan)
     assert_close("y", got["y"], want["y"])
 
 
