@@ -2,10 +2,14 @@
 //
 //   C = epi(A[M x K] * B[K x N], bias)
 //
-// A is row-major with leading dimension lda. B comes from one of three
+// A is row-major with leading dimension lda. B comes from one of four
 // sources (BMODE): 0 = dense row-major B[K][ldb] read as float4 (ldb % 4 == 0),
 // 1 = dense row-major read as scalars, 2 = implicit im2col of an NCHW input x
-// (B[k][p] = x[n][c][oh*SH-PT+kh*DH][ow*SW-PL+kw*DW], zero outside), so a
+// (B[k][p] = x[n][c][oh*SH-PT+kh*DH][ow*SW-PL+kw*DW], zero outside) with k
+// ordered (c, kh, kw), 3 = the same gather with k ordered (kh, kw, c) — the
+// weights are packed to match — for Cin % BK == 0: every K tile is then one
+// filter tap, so a column's bounds check and pixel address are computed once
+// per tile and each element costs one add and one load. Either way a
 // convolution needs no column buffer. The output is row-major C[M][ldc]
 // (OUT = 0) or, for convolutions, NCHW: column p = n*hw + s goes to
 // C[(n*M + row)*hw + s] (OUT = 1). With split-K (OUT = 2) the grid holds
@@ -45,7 +49,7 @@ template <> struct Mfma<16> {
   }
 };
 
-// Compile-time convolution window (used when BMODE == 2).
+// Compile-time convolution window (used when BMODE >= 2).
 template <int KH_, int KW_, int SH_, int SW_, int DH_, int DW_, int PT_, int PL_>
 struct ConvWin {
   static constexpr int KH = KH_, KW = KW_, SH = SH_, SW = SW_, DH = DH_, DW = DW_, PT = PT_, PL = PL_;
@@ -58,7 +62,7 @@ struct GemmArgs {
   const float* __restrict__ bias;
   float* __restrict__ C;
   int M, N, K, lda, ldb, ldc, hw;
-  int Cin, H, W, OH, OW;         // conv input / output geometry (BMODE == 2)
+  int Cin, H, W, OH, OW;         // conv input / output geometry (BMODE >= 2)
   int ksplit, kchunk;            // K slices (grid = tiles * ksplit) and slice depth
 };
 
@@ -117,7 +121,7 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
 
   // Implicit-im2col state: the column quad each thread gathers is fixed.
   int cbase[4], cih[4], ciw[4];
-  if (BMODE == 2) {
+  if (BMODE >= 2) {
     const int nq = tid % (BN / 4);
     const int ohw = g.OH * g.OW;
 #pragma unroll
@@ -188,6 +192,34 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
           if (gk < kend && gn < g.N) v = g.B[(size_t)gk * g.ldb + gn];
         }
         rbs[i] = v;
+      }
+    } else if (BMODE == 3) {
+      // One filter tap per tile: k0 = tap * Cin + c0 with c0 % BK == 0.
+      const int HW = g.H * g.W;
+      const int tap = k0 / g.Cin;
+      const int c0 = k0 - tap * g.Cin;
+      const int kh = tap / Win::KW;
+      const int kw = tap - kh * Win::KW;
+      int pix[4];
+      bool ok[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int ih = cih[j] + kh * Win::DH;
+        const int iw = ciw[j] + kw * Win::DW;
+        ok[j] = (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W && k0 < kend;
+        pix[j] = cbase[j] + ih * g.W + iw;
+      }
+#pragma unroll
+      for (int i = 0; i < B_PT; ++i) {
+        int idx = tid + i * NT;
+        float e[4] = {0.f, 0.f, 0.f, 0.f};
+        if (idx < B_ELEMS) {
+          const int cofs = (c0 + idx / (BN / 4)) * HW;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (ok[j]) e[j] = g.B[pix[j] + cofs];
+        }
+        rb[i] = make_float4(e[0], e[1], e[2], e[3]);
       }
     } else {
       constexpr int KHW = Win::KH * Win::KW;

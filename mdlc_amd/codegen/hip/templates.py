@@ -102,7 +102,7 @@ def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: s
     Kernel ABI (the reference's gemm ABI plus trailing layout arguments):
       dense  (bmode 0/1): (A, B, [bias], C, int M, int N, int K, int lda, int ldb, int ldc,
                            int hw, int ksplit, int kchunk)
-      conv   (bmode 2)  : (W, x, [bias], y, int M, int N, int K, int lda,
+      conv   (bmode 2/3): (W, x, [bias], y, int M, int N, int K, int lda,
                            int Cin, int H, int W, int OH, int OW, int ksplit, int kchunk)
     ``hw`` > 0 selects the NCHW output scatter for conv-as-GEMM. With
     ``sched.SK > 1`` the kernel writes raw partial sums of each K slice to
@@ -126,7 +126,7 @@ def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: s
             f"{'true' if s.DB else 'false'}, {'true' if vec_a else 'false'}, {bmode}, "
             f"{out}, {epi}, {winty}>")
     nt = s.threads_per_block()
-    if bmode == 2:
+    if bmode >= 2:
         src.append(
             f'extern "C" __global__ __launch_bounds__({nt}) void {name}(\n'
             f"    const float* __restrict__ A, const float* __restrict__ x, {bias_arg}"

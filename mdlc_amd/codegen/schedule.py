@@ -23,7 +23,7 @@ from __future__ import annotations
 from dataclasses import asdict, dataclass
 from typing import Iterator
 
-LDS_LIMIT = 64 * 1024          # bytes one workgroup may allocate
+LDS_LIMIT = 160 * 1024         # bytes one workgroup may allocate (gfx950: 160 KB per CU)
 MAX_ACC_REGS = 128             # accumulator registers per lane we allow
 
 

@@ -60,7 +60,7 @@ def main(argv=None) -> int:
     ap.add_argument("--model", default="resnet18")
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--conv-mode", default="implicit")
-    ap.add_argument("--budget", type=int, default=24)
+    ap.add_argument("--budget", type=int, default=48)
     ap.add_argument("--precompile", action="store_true")
     ap.add_argument("--jobs", type=int, default=8)
     ap.add_argument("--out", default=TUNED_PATH)
