@@ -24,6 +24,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 METRIC = "ResNet-18 b=32 fp32 images/sec; fused GEMM/conv TFLOP/s & % MFMA peak"
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "resnet18_b32_traffic.json")
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 
@@ -87,6 +88,12 @@ def main(argv=None) -> int:
     ms_per_step = ex.plan.time_ms(0, args.steps)
     value = B * 1000.0 / ms_per_step
     print(f"[bench] {ms_per_step:.3f} ms/step, {value:.1f} images/s", file=sys.stderr, flush=True)
+    # The same forward through the host-buffer boundary (input H2D, logits
+    # D2H, both synchronous): reported beside the value, never as it.
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        ex.run({"input": x})
+    pcie_value = B * args.steps / (time.perf_counter() - t1)
 
     # Per-launch timing -> per-kernel totals; the dominant kernel is the one
     # with the most device time per step.
@@ -115,6 +122,14 @@ def main(argv=None) -> int:
         achieved = dom["bytes"] / dom["launches"] / (avg_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": achieved / PEAK_HBM_GBS, "traffic": None}
+    if os.path.exists(TRAFFIC_JSON):
+        # HBM bytes per dispatch from the committed rocprofv3 FETCH_SIZE /
+        # WRITE_SIZE runs of this workload (copy-calibrated); only valid for
+        # the kernel those runs measured.
+        with open(TRAFFIC_JSON) as f:
+            measured = json.load(f)["kernels"].get(dom_name)
+        if measured:
+            roof["traffic"] = measured["traffic_bytes"]
     roof.update({"kernel": dom_name, "launches_per_step": dom["launches"],
                  "avg_launch_ms": avg_ms, "share_of_step": dom["ms"] / total_ms})
     all_flops = sum(l.meta.get("flops", 0) for l in c.module.plan)
@@ -126,12 +141,14 @@ def main(argv=None) -> int:
         "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic N(0,1) images, random-init weights (Kaiming-normal conv/FC, "
-                "BN gamma U(0.5,1.5) beta N(0,0.1) mean N(0,0.1) var U(0.5,1.5))",
+                "BN gamma U(0.5,1.5) beta N(0,0.1) mean N(0,0.1) var U(0.5,1.5); each "
+                "Conv/Gemm LSUV-rescaled to unit output std as the reference exporters do)",
         "config": {"workload": f"resnet18_fp32_b{B}", "batch": B, "image": [3, 224, 224],
                    "conv_mode": args.conv_mode, "launches": len(c.module.plan),
                    "gflop_per_step": all_flops / 1e9,
                    "conv_gemm_tflops": all_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms else None,
-                   "network_tflops": all_flops / (ms_per_step * 1e-3) / 1e12},
+                   "network_tflops": all_flops / (ms_per_step * 1e-3) / 1e12,
+                   "host_buffer_images_per_s": pcie_value},
         "roofline": roof,
     }
     if not args.no_cpu_baseline:

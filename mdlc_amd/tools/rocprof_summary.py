@@ -1,0 +1,92 @@
+"""Summarise rocprofv3 SQLite output (``*_results.db``) as text.
+
+    python -m mdlc_amd.tools.rocprof_summary trace.db                 # per-kernel durations
+    python -m mdlc_amd.tools.rocprof_summary pmc.db --counter FETCH_SIZE
+    python -m mdlc_amd.tools.rocprof_summary --traffic fetch.db write.db \
+        copy_fetch.db copy_write.db --copy-mib 256 --out traffic.json
+
+The first form lists, per kernel name, the dispatch count, total and average
+duration and share of device time (the ``--kernel-trace --stats`` view). The
+second lists the average value of one PMC counter per dispatch of each
+kernel (``--pmc`` runs). The third turns a FETCH_SIZE run and a WRITE_SIZE
+run of a workload, plus the same two counters read for a plain copy of
+``--copy-mib`` MiB, into HBM bytes per dispatch for every kernel: each
+counter is scaled by (true copy bytes / counter reading for the copy).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import sqlite3
+
+
+def kernel_stats(path: str) -> list:
+    con = sqlite3.connect(path)
+    rows = con.execute(
+        "select name, count(*), sum(duration), avg(duration), min(duration), max(duration) "
+        "from kernels group by name order by sum(duration) desc").fetchall()
+    con.close()
+    return rows
+
+
+def counter_stats(path: str, counter: str) -> list:
+    con = sqlite3.connect(path)
+    rows = con.execute(
+        "select k.name, count(*), avg(p.counter_value) from pmc_events p "
+        "join kernels k on k.dispatch_id = p.dispatch_id "
+        "where p.counter_name = ? group by k.name order by avg(p.counter_value) desc",
+        (counter,)).fetchall()
+    con.close()
+    return rows
+
+
+def traffic(fetch_db, write_db, copy_fetch_db, copy_write_db, copy_mib) -> dict:
+    true_kib = copy_mib * 1024.0
+    cf = dict((n, v) for n, _, v in counter_stats(copy_fetch_db, "FETCH_SIZE"))["copy_bytes"]
+    cw = dict((n, v) for n, _, v in counter_stats(copy_write_db, "WRITE_SIZE"))["copy_bytes"]
+    fs, ws = true_kib / cf, true_kib / cw
+    fetch = {n: v for n, _, v in counter_stats(fetch_db, "FETCH_SIZE")}
+    write = {n: v for n, _, v in counter_stats(write_db, "WRITE_SIZE")}
+    kernels = {n: {"fetch_bytes": fetch[n] * fs * 1024, "write_bytes": write.get(n, 0.0) * ws * 1024,
+                   "traffic_bytes": (fetch[n] * fs + write.get(n, 0.0) * ws) * 1024}
+               for n in fetch}
+    return {"fetch_scale": fs, "write_scale": ws, "copy_mib": copy_mib, "kernels": kernels}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("db", nargs="?")
+    ap.add_argument("--counter", default="")
+    ap.add_argument("--traffic", nargs=4, metavar=("FETCH_DB", "WRITE_DB", "COPY_FETCH_DB", "COPY_WRITE_DB"))
+    ap.add_argument("--copy-mib", type=int, default=256)
+    ap.add_argument("--out", default="")
+    args = ap.parse_args(argv)
+    if args.traffic:
+        t = traffic(*args.traffic, args.copy_mib)
+        text = json.dumps(t, indent=1, sort_keys=True)
+        if args.out:
+            with open(args.out, "w") as f:
+                f.write(text + "\n")
+        print(f"scale: FETCH_SIZE x{t['fetch_scale']:.4f}, WRITE_SIZE x{t['write_scale']:.4f}")
+        for n, d in sorted(t["kernels"].items(), key=lambda kv: -kv[1]["traffic_bytes"]):
+            print(f"{n[:64]:64s} fetch {d['fetch_bytes'] / 1e6:9.2f} MB  write "
+                  f"{d['write_bytes'] / 1e6:9.2f} MB")
+        return 0
+    if args.counter:
+        print(f"{'kernel':64s} {'dispatches':>10s} {'avg ' + args.counter:>18s}")
+        for name, n, avg in counter_stats(args.db, args.counter):
+            print(f"{name[:64]:64s} {n:10d} {avg:18.1f}")
+        return 0
+    rows = kernel_stats(args.db)
+    total = sum(r[2] for r in rows) or 1
+    print(f"{'kernel':64s} {'calls':>6s} {'total_us':>10s} {'avg_us':>9s} {'min_us':>9s} "
+          f"{'max_us':>9s} {'pct':>6s}")
+    for name, n, tot, avg, mn, mx in rows:
+        print(f"{name[:64]:64s} {n:6d} {tot / 1e3:10.1f} {avg / 1e3:9.2f} {mn / 1e3:9.2f} "
+              f"{mx / 1e3:9.2f} {100.0 * tot / total:6.2f}")
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,99 @@
+"""Autotuner: schedule-space validity, cost-model ranking, cache round trip
+(reference tests/test_autotuner.py:9-42, re-parameterised for MFMA)."""
+
+from __future__ import annotations
+
+import os
+
+from mdlc_amd.autotuner import AutotuneCache, Tuner, analytical_cost, tune_gemm
+from mdlc_amd.autotuner.tuner import TUNED_PATH, candidates, problem_key
+from mdlc_amd.codegen.schedule import (
+    DEFAULT_GEMM, MfmaSchedule, default_schedule, gemm_search_space, split_slices,
+)
+
+
+def test_schedule_validity_and_pruning():
+    space = list(gemm_search_space((1, 2, 4)))
+    assert space
+    for s in space:
+        assert s.is_valid()
+        assert s.lds_bytes() <= 160 * 1024
+        assert 64 <= s.threads_per_block() <= 1024
+        wm, wn = s.wave_tile()
+        assert wm % s.MS == 0 and wn % s.MS == 0
+    assert not MfmaSchedule(32, 32, 8, 1, 1, 16).is_valid()       # BK too shallow for 16x16x4
+    assert not MfmaSchedule(64, 48, 16, 2, 2, 32).is_valid()      # wave tile not MFMA multiple
+
+
+def test_split_slices_cover_k_without_empty_slices():
+    for K in (33, 147, 576, 4608):
+        for sk in (1, 2, 3, 4, 8):
+            s = MfmaSchedule(64, 64, 16, 2, 2, 32, True, sk)
+            n, chunk = split_slices(K, s)
+            assert chunk % s.BK == 0 or n == 1
+            assert (n - 1) * chunk < K <= n * chunk
+
+
+def test_cost_model_prefers_no_quant_waste_on_small_gemm():
+    perfect = MfmaSchedule(64, 64, 16, 2, 2, 32)
+    oversized = MfmaSchedule(256, 256, 16, 2, 4, 32)
+    assert analytical_cost(perfect, 64, 64, 64) < analytical_cost(oversized, 64, 64, 64)
+
+
+def test_cost_model_prefers_split_k_for_deep_small_grids():
+    base = MfmaSchedule(64, 64, 16, 2, 2, 32)
+    assert analytical_cost(base.with_split(8), 512, 49, 4608) < analytical_cost(base, 512, 49, 4608)
+
+
+def test_default_schedule_fills_the_chip():
+    for M, N, K in [(64, 100352, 576), (512, 1568, 4608), (256, 6272, 2304)]:
+        s = default_schedule(M, N, K)
+        n, _ = split_slices(K, s)
+        assert s.is_valid()
+        assert -(-M // s.BM) * -(-N // s.BN) * n >= 256
+
+
+def test_tune_gemm_returns_valid_best():
+    res = tune_gemm(512, 512, 512, budget=16)
+    assert res.best.is_valid() and res.n_evaluated >= 16
+    metrics = [m for _, m in res.ranking]
+    assert metrics == sorted(metrics)
+    assert not res.measured
+
+
+def test_candidates_include_default_and_are_valid():
+    c = candidates(256, 6272, 2304, budget=8)
+    assert default_schedule(256, 6272, 2304) in c
+    assert all(s.is_valid() for s in c)
+
+
+def test_cache_roundtrip(tmp_path):
+    path = os.path.join(tmp_path, "cache.json")
+    c = AutotuneCache(path)
+    s = MfmaSchedule(64, 64, 16, 2, 2, 32, False, 2)
+    c.put(128, 256, 64, s, 1.23, measured=False)
+    c.save()
+    assert AutotuneCache(path).get(128, 256, 64) == s
+
+
+def test_tuner_caches_per_shape(tmp_path):
+    cache = AutotuneCache(os.path.join(tmp_path, "c.json"))
+    tuner = Tuner(cache=cache, budget=8)
+    s1 = tuner.schedule_for(None, (256, 256, 256))
+    s2 = tuner.schedule_for(None, (256, 256, 256))
+    assert s1 == s2 and cache.get(256, 256, 256) is not None
+
+
+def test_shipped_tuned_schedules_are_valid():
+    """The measured gfx950 schedules shipped with the backend parse and are
+    valid, and cover every conv/GEMM problem of ResNet-18 at batch 32."""
+    from mdlc_amd.tools.tune import model_problems
+
+    cache = AutotuneCache(TUNED_PATH)
+    assert cache.entries
+    for key, e in cache.entries.items():
+        assert MfmaSchedule(**e["sched"]).is_valid(), key
+        assert e["measured"]
+    for p in model_problems("resnet18", 32, "implicit"):
+        assert problem_key(p) in cache.entries, problem_key(p)
+    assert DEFAULT_GEMM.is_valid()

