@@ -23,7 +23,8 @@ from dataclasses import dataclass, field
 from typing import Optional
 
 from mdlc_amd.codegen.schedule import (
-    CUS, DEFAULT_GEMM, MfmaSchedule, default_schedule, gemm_search_space, split_slices,
+    CUS, DEFAULT_GEMM, MfmaSchedule, default_qschedule, default_schedule, gemm_search_space,
+    split_slices,
 )
 
 LDS_PER_CU = 160 * 1024
@@ -73,6 +74,8 @@ def analytical_cost(sched: MfmaSchedule, M: int, N: int, K: int) -> float:
 
 def problem_key(problem: dict) -> str:
     M, N, K = problem["M"], problem["N"], problem["K"]
+    if problem.get("kind") in ("qconv", "qgemm"):
+        return f"i8:{problem['kind']}:{M}x{N}x{K}:a{problem.get('amode', 0)}"
     if problem.get("kind") == "conv":
         return (f"conv:{M}x{N}x{K}:{problem['KH']}x{problem['KW']}s{problem['SH']}"
                 f":{problem['C']}x{problem['H']}x{problem['W']}:{problem.get('mode', 'implicit')}")
@@ -247,6 +250,8 @@ class Tuner:
         hit = self.cache.get_key(key)
         if hit is not None and hit.is_valid():
             return hit
+        if problem.get("kind") in ("qconv", "qgemm"):
+            return default_qschedule(problem["M"], problem["N"], problem["K"])
         if not self.tune_misses:
             return default_schedule(problem["M"], problem["N"], problem["K"])
         res = tune_problem(problem, budget=self.budget, ctx=self.ctx)

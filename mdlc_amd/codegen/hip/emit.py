@@ -13,6 +13,8 @@ extended because nothing runs on the host here:
   im2col      batched column matrix for the explicit conv path
   dwconv      direct depthwise convolution + epilogue
   splitk_reduce  sums split-K partial slices in order + epilogue
+  quantize, qgemm, qconv, qdwconv, qadd, qlut, qgap, dequantize  (INT8 path,
+              int8 activations channels-last on the device)
   elementwise fused pointwise chain (also single pointwise ops)
   maxpool, gap, copy (reshaping views: Flatten/Reshape/Identity/...)
 
@@ -29,12 +31,13 @@ epilogue, which also fixes the reference's batch>1 bug (emit.py:187-188).
 
 from __future__ import annotations
 
-from dataclasses import dataclass, field
 from typing import Callable, Optional
 
 import numpy as np
 
 from mdlc_amd.codegen.hip import templates as T
+from mdlc_amd.codegen.hip.emit_int8 import Int8LoweringMixin
+from mdlc_amd.codegen.hip.plan import LIBRARY_PARTS, QUANT_OPS, HipModule, Launch, round4, round16  # noqa: F401
 from mdlc_amd.codegen.schedule import MfmaSchedule, default_schedule, split_slices
 from mdlc_amd.ir import Graph, Node
 from mdlc_amd.passes.fuse_elementwise import ELEMENTWISE
@@ -43,60 +46,9 @@ from mdlc_amd.passes.shape_inference import conv_geometry
 ScheduleFn = Callable[[Optional[Node], tuple], MfmaSchedule]
 
 VIEW_OPS = {"Flatten", "Reshape", "Identity", "Squeeze", "Unsqueeze"}
-LIBRARY_PARTS = ("common", "gemm_f32", "im2col", "pool", "dwconv", "copy")
 
 
-def round4(n: int) -> int:
-    return (int(n) + 3) // 4 * 4
-
-
-@dataclass
-class Launch:
-    """One kernel invocation of the plan (contract of emit.py:38-47)."""
-    kind: str
-    kernel_name: str
-    inputs: list
-    outputs: list
-    grid: tuple
-    block: tuple
-    meta: dict = field(default_factory=dict)
-
-
-@dataclass
-class HipModule:
-    graph: Graph
-    kernels: dict                  # kernel name -> wrapper source
-    plan: list                     # [Launch]
-    scratch_shapes: dict           # scratch tensor -> (rows, ld) float32
-    device_constants: dict = field(default_factory=dict)   # packed constant -> ndarray
-    library: tuple = LIBRARY_PARTS
-    # scratch tensor -> region class; tensors of one class share one region
-    # (they are used strictly one after another on the stream)
-    scratch_class: dict = field(default_factory=dict)
-
-    def sources(self) -> str:
-        """One hipRTC translation unit: the templates, then every wrapper."""
-        head = "// Generated by mdlc_amd for gfx950.\n"
-        lib = "\n".join(T.library_source(p) for p in self.library)
-        return head + lib + "\n" + "\n".join(self.kernels[k] for k in sorted(self.kernels))
-
-    def fallbacks(self) -> list:
-        """Host-executed launches: always empty — every op runs on the device."""
-        return [l.kernel_name for l in self.plan if l.kind == "host"]
-
-    def report(self) -> str:
-        kinds: dict = {}
-        for l in self.plan:
-            kinds[l.kind] = kinds.get(l.kind, 0) + 1
-        fb = self.fallbacks()
-        return "\n".join([
-            f"HIP module: {len(self.kernels)} distinct kernels, {len(self.plan)} launches",
-            "  launches by kind: " + ", ".join(f"{k}x{v}" for k, v in sorted(kinds.items())),
-            "  host fallbacks: " + (", ".join(fb) if fb else "none"),
-        ])
-
-
-class HipCodegen:
+class HipCodegen(Int8LoweringMixin):
     def __init__(self, schedule_fn: Optional[ScheduleFn] = None, *, conv_mode: str = "implicit") -> None:
         if conv_mode not in ("implicit", "im2col"):
             raise ValueError(f"conv_mode must be 'implicit' or 'im2col', not {conv_mode!r}")
@@ -111,6 +63,7 @@ class HipCodegen:
         self.scratch: dict = {}
         self.scratch_class: dict = {}
         self.consts: dict = {}
+        self.layout: dict = {}
         self._dedup: dict = {}
 
     # -- helpers ------------------------------------------------------------
@@ -173,6 +126,7 @@ class HipCodegen:
     # -- lowering -------------------------------------------------------------
 
     def lower(self, g: Graph) -> HipModule:
+        self._graph = g
         for node in g.topo_sort():
             op = node.op_type
             if op in ("Conv", "FusedConvAct", "FusedConvBNAct"):
@@ -191,10 +145,13 @@ class HipCodegen:
                 self._lower_gap(g, node)
             elif op in VIEW_OPS:
                 self._lower_view(g, node)
+            elif op in QUANT_OPS:
+                getattr(self, "_lower_" + op.lower())(g, node)
             else:
                 raise NotImplementedError(f"HIP codegen: no device lowering for {op!r}")
-        return HipModule(g, self.kernels, self.plan, self.scratch, self.consts,
-                         scratch_class=self.scratch_class)
+        lib = LIBRARY_PARTS + (("int8",) if any(n.op_type in QUANT_OPS for n in g.nodes) else ())
+        return HipModule(g, self.kernels, self.plan, self.scratch, self.consts, lib,
+                         scratch_class=self.scratch_class, device_layout=dict(self.layout))
 
     def _lower_conv(self, g: Graph, node: Node) -> None:
         x, w = node.inputs[0], node.inputs[1]
@@ -443,6 +400,11 @@ class HipCodegen:
 
     def _lower_view(self, g: Graph, node: Node) -> None:
         src = node.inputs[0]
+        if self.layout.get(src) == "NHWC":
+            shp = self._shape(g, src)
+            if len(shp) == 4 and shp[2] * shp[3] != 1 and shp[1] != 1:
+                raise NotImplementedError(
+                    f"HIP codegen: {node.op_type} of a channels-last int8 tensor {shp}")
         info = g.info(node.outputs[0])
         nbytes = int(info.nbytes())
         self._kernel("copy", lambda i: T.copy_kernel("copy_bytes"))

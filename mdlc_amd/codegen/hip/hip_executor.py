@@ -138,6 +138,26 @@ class HipExecutor:
             args = [P(l.inputs[0]), P(l.outputs[0]), I(m["planes"]), I(m["HW"])]
         elif k == "copy":
             args = [P(l.inputs[0]), P(l.outputs[0]), Arg.i64(m["nbytes"])]
+        elif k == "quantize":
+            args = [P(l.inputs[0]), P(l.outputs[0]), I(m["N"]), I(m["C"]), I(m["HW"]),
+                    Arg.f32(m["inv_s"])]
+        elif k == "qgemm":
+            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+            args += [I(m[f]) for f in ("M", "N", "K", "lda", "ldb", "ldc", "Cin", "H", "W", "OH", "OW")]
+        elif k == "qdwconv":
+            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+            args += [I(m[f]) for f in ("N", "C", "H", "W", "OH", "OW", "PT", "PL")]
+        elif k == "qadd":
+            args = [P(l.inputs[0]), P(l.inputs[1]), P(l.outputs[0]), Arg.i64(m["n"]),
+                    Arg.f32(m["ma"]), Arg.f32(m["mb"])]
+        elif k == "qlut":
+            args = [P(l.inputs[0]), P(l.inputs[1]), P(l.outputs[0]), Arg.i64(m["n"])]
+        elif k == "qgap":
+            args = [P(l.inputs[0]), P(l.outputs[0]), I(m["N"]), I(m["C"]), I(m["HW"]),
+                    Arg.f32(m["m"])]
+        elif k == "dequantize":
+            args = [P(l.inputs[0]), P(l.outputs[0]), Arg.i64(m["n"]), I(m["C"]), I(m["HW"]),
+                    Arg.f32(m["s"])]
         else:
             raise HipError(f"launch kind {k!r} has no device implementation")
         return (self.funcs[l.kernel_name].value, l.grid, l.block, 0, args)
@@ -154,13 +174,25 @@ class HipExecutor:
                 raise HipError(f"feed {name!r} has shape {arr.shape}, compiled for {self.shapes[name]}")
             self.ctx.htod(self.ptr(name), arr)
 
+    def _nhwc(self, name: str) -> bool:
+        return (self.module.device_layout.get(name) == "NHWC" and len(self.shapes[name]) == 4)
+
     def read(self, name: str) -> np.ndarray:
-        return self.ctx.dtoh(self.ptr(name), self.shapes[name], self.dtypes[name])
+        """A tensor's value in the IR's layout (channels-last device tensors
+        are transposed back to NCHW)."""
+        shp = tuple(self.shapes[name])
+        if self._nhwc(name):
+            n, c, h, w = shp
+            dev = self.ctx.dtoh(self.ptr(name), (n, h, w, c), self.dtypes[name])
+            return np.ascontiguousarray(dev.transpose(0, 3, 1, 2))
+        return self.ctx.dtoh(self.ptr(name), shp, self.dtypes[name])
 
     def write(self, name: str, arr: np.ndarray) -> None:
         arr = np.ascontiguousarray(arr, dtype=self.dtypes[name])
         if tuple(arr.shape) != tuple(self.shapes[name]):
             raise HipError(f"{name!r}: shape {arr.shape} != {self.shapes[name]}")
+        if self._nhwc(name):
+            arr = np.ascontiguousarray(arr.transpose(0, 2, 3, 1))
         self.ctx.htod(self.ptr(name), arr)
 
     def run(self, feeds: dict, *, timing: bool = False, warmup: int = 3, iters: int = 10) -> dict:

@@ -313,3 +313,74 @@ def elementwise_signature(node: Node, scalar_consts: dict) -> tuple:
         extra = tuple(sorted((k, v) for k, v in n.attrs.items() if isinstance(v, (int, float, str))))
         ops.append((n.op_type, tuple(tag(e) for e in n.inputs if e), tag(n.outputs[0]), extra))
     return tuple(ops), tuple(tag(o) for o in node.outputs)
+
+
+# ----- INT8 quantized path ----------------------------------------------------
+
+def qgemm_kernel(name: str, sched: MfmaSchedule, *, amode: int, out_f32: bool, lo: int,
+                 win: Optional[tuple] = None) -> tuple:
+    """int8 MFMA GEMM / implicit conv with the requant (or dequant) epilogue.
+    ABI: (A, B, bias, mult, C, int M, int N, int K, int lda, int ldb, int ldc,
+    int Cin, int H, int W, int OH, int OW)."""
+    s = sched
+    winty = "mdlc::NoWin" if win is None else "mdlc::ConvWin<%d, %d, %d, %d, %d, %d, %d, %d>" % tuple(win)
+    nt = s.threads_per_block()
+    tmpl = (f"mdlc::qgemm_i8_mfma<{s.BM}, {s.BN}, {s.BK}, {s.WGM}, {s.WGN}, {s.MS}, {amode}, "
+            f"{1 if out_f32 else 0}, {int(lo)}, {winty}>")
+    return name, (
+        f'extern "C" __global__ __launch_bounds__({nt}) void {name}(\n'
+        "    const signed char* __restrict__ A, const signed char* __restrict__ B,\n"
+        "    const int* __restrict__ bias, const float* __restrict__ mult, void* __restrict__ C,\n"
+        "    int M, int N, int K, int lda, int ldb, int ldc, int Cin, int H, int W, int OH, int OW) {\n"
+        "  mdlc::QGemmArgs g{A, B, bias, mult, C, M, N, K, lda, ldb, ldc, Cin, H, W, OH, OW};\n"
+        f"  {tmpl}(g);\n}}\n")
+
+
+def qdwconv_kernel(name: str, win: tuple, *, cv: int, lo: int) -> tuple:
+    """int8 depthwise conv over NHWC. ``win`` = (KH, KW, SH, SW, DH, DW).
+    ABI: (x, w, bias, mult, y, int N, int C, int H, int W, int OH, int OW, int PT, int PL)."""
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const signed char* __restrict__ x, const signed char* __restrict__ w,\n"
+        "    const int* __restrict__ bias, const float* __restrict__ mult, signed char* __restrict__ y,\n"
+        "    int N, int C, int H, int W, int OH, int OW, int PT, int PL) {\n"
+        f"  mdlc::qdwconv_nhwc<{', '.join(str(v) for v in win)}, {cv}, {int(lo)}>(x, w, bias, mult, y, "
+        "N, C, H, W, OH, OW, PT, PL);\n}\n")
+
+
+def quantize_kernel(name: str = "quantize_nchw_nhwc") -> tuple:
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const float* __restrict__ x, signed char* __restrict__ y, int N, int C, int HW, float inv_s) {\n"
+        "  mdlc::quantize_nchw_nhwc(x, y, N, C, HW, inv_s);\n}\n")
+
+
+def qadd_kernel(name: str = "qadd") -> tuple:
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const signed char* __restrict__ a, const signed char* __restrict__ b,\n"
+        "    signed char* __restrict__ y, long long n, float ma, float mb) {\n"
+        "  mdlc::qadd_i8(a, b, y, n, ma, mb);\n}\n")
+
+
+def qlut_kernel(name: str = "qlut") -> tuple:
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const signed char* __restrict__ x, const signed char* __restrict__ table,\n"
+        "    signed char* __restrict__ y, long long n) {\n"
+        "  mdlc::qlut_i8(x, table, y, n);\n}\n")
+
+
+def qgap_kernel(name: str = "qgap") -> tuple:
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const signed char* __restrict__ x, signed char* __restrict__ y, int N, int C, int HW, float m) {\n"
+        "  mdlc::qgap_nhwc(x, y, N, C, HW, m);\n}\n")
+
+
+def dequantize_kernel(name: str = "dequantize") -> tuple:
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const signed char* __restrict__ x, float* __restrict__ y, long long n, int C, int HW,\n"
+        "    float s) {\n"
+        "  mdlc::dequantize_i8(x, y, n, C, HW, s);\n}\n")

@@ -138,3 +138,57 @@ def default_schedule(M: int, N: int, K: int) -> MfmaSchedule:
     ms = 32 if min(bm // wgm, bn // wgn) >= 32 else 16
     s = MfmaSchedule(bm, bn, 16, wgm, wgn, ms, True, sk)
     return s if s.is_valid() else DEFAULT_GEMM
+
+
+# ----- int8 schedules ---------------------------------------------------------
+# The same MfmaSchedule fields describe the int8 kernel, with BK counted in
+# bytes: MS = 32 selects v_mfma_i32_32x32x32_i8 (32 k per instruction), MS = 16
+# v_mfma_i32_16x16x64_i8 (64 k); LDS rows are BK + 16 bytes, double buffered.
+
+def qsched_valid(s: MfmaSchedule) -> bool:
+    if s.MS not in (16, 32) or s.SK != 1:
+        return False
+    wm, wn = s.wave_tile()
+    if s.BM % s.WGM or s.BN % s.WGN or wm % s.MS or wn % s.MS:
+        return False
+    kg = 64 // s.MS
+    if s.BK % (16 * kg):
+        return False
+    nt = s.threads_per_block()
+    if nt > 1024 or nt % (s.BK // 16):
+        return False
+    if 2 * (s.BM + s.BN) * (s.BK + 16) > LDS_LIMIT or s.acc_regs() > MAX_ACC_REGS:
+        return False
+    return True
+
+
+def default_qschedule(M: int, N: int, K: int) -> MfmaSchedule:
+    """Shape-aware int8 default: 128-wide tiles shrunk until the grid covers
+    the chip twice, BK = 64 bytes (2 MFMA steps of 32)."""
+    bm = 128 if M > 64 else (64 if M > 32 else 32)
+    bn = 128 if N > 64 else (64 if N > 32 else 32)
+    tiles = lambda: -(-M // bm) * -(-N // bn)  # noqa: E731
+    while tiles() < 2 * CUS and (bm > 64 or bn > 64):
+        if bm >= bn and bm > 64:
+            bm //= 2
+        else:
+            bn //= 2
+    wgm = 2 if bm >= 64 else 1
+    wgn = 2 if bn >= 64 else 1
+    ms = 32 if min(bm // wgm, bn // wgn) >= 32 else 16
+    bk = 64 if ms == 32 else 64
+    s = MfmaSchedule(bm, bn, bk, wgm, wgn, ms, True, 1)
+    if not qsched_valid(s):
+        s = MfmaSchedule(64, 64, 64, 2, 2, 32, True, 1)
+    return s
+
+
+def qgemm_search_space():
+    for bm in (32, 64, 128, 256):
+        for bn in (32, 64, 128, 256):
+            for bk in (64, 128):
+                for wgm, wgn in ((1, 1), (2, 1), (1, 2), (2, 2), (4, 1), (1, 4), (4, 2), (2, 4)):
+                    for ms in (32, 16):
+                        s = MfmaSchedule(bm, bn, bk, wgm, wgn, ms, True, 1)
+                        if qsched_valid(s):
+                            yield s

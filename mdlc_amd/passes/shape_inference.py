@@ -110,7 +110,9 @@ def node_output_infos(node: Node, shape_of, dtype_of, const_of) -> list:
         sa, sb = shape_of(ins[0]), shape_of(ins[1])
         m = sa[1] if a.get("transA", 0) else sa[0]
         nn = sb[0] if a.get("transB", 0) else sb[1]
-        return [((m, nn), DType.INT8 if op == "QGemm" else d0)]
+        if op == "QGemm":
+            return [((m, nn), DType.FLOAT32 if a.get("out_dtype") == "float32" else DType.INT8)]
+        return [((m, nn), d0)]
     if op == "MatMul":
         sa, sb = shape_of(ins[0]), shape_of(ins[1])
         return [(np.matmul(np.empty(sa, np.float32), np.empty(sb, np.float32)).shape, d0)]

@@ -128,3 +128,15 @@ def test_unsupported_op_raises_instead_of_host_fallback():
     b.output("y")
     with pytest.raises(NotImplementedError, match="no device lowering"):
         compile_graph(b.graph())
+
+
+def test_repvit_int8_module_compiles_and_is_channels_last():
+    from mdlc_amd.tools.build_repvit_int8 import build_repvit_int8, make_input
+
+    c = compile_graph(build_repvit_int8(batch=2), feeds={"input": make_input(2)})
+    kinds = {l.kind for l in c.module.plan}
+    assert kinds >= {"quantize", "qgemm", "qdwconv", "qadd", "qlut", "qgap"}
+    assert c.module.fallbacks() == []
+    assert all(c.module.device_layout.get(l.outputs[0]) == "NHWC"
+               for l in c.module.plan if l.kind in ("qdwconv", "qlut", "qadd"))
+    R.compile_code_object(c.module.sources())

@@ -1,0 +1,168 @@
+"""INT8 path on the device: every int8 code and int32-derived output is
+bit-exact against the oracle's build-defined semantics (oracle/quant.py).
+
+The reference has no quantized operator, so these are the only parity
+checks for this row; the oracle's own semantics are pinned on the CPU in
+tests/test_oracle.py (integer closed forms, float64 route, round-half-even).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from gpu_util import assert_close, device_run
+from mdlc_amd.codegen.schedule import MfmaSchedule
+from mdlc_amd.tools.build_repvit_int8 import build_repvit_int8, gelu_table, make_input
+from mdlc_amd.tools.graph_builder import GraphBuilder
+
+pytestmark = pytest.mark.gpu
+
+
+def _qconv_graph(n, c, h, w, oc, k, s, *, group=1, relu=False, seed=0, scale_in=0.05):
+    rng = np.random.default_rng(seed)
+    b = GraphBuilder("qc")
+    b.input("x", (n, c, h, w))
+    b.node("QuantizeLinear", ["x"], "xq", inv_scale=float(np.float32(1 / scale_in)))
+    icg = c // group
+    b.const("w", rng.integers(-127, 128, (oc, icg, k, k)).astype(np.int8))
+    b.const("b", rng.integers(-3000, 3000, oc).astype(np.int32))
+    b.const("m", rng.uniform(0.0005, 0.004, oc).astype(np.float32))
+    p = (k - 1) // 2
+    attrs = dict(kernel_shape=[k, k], strides=[s, s], pads=[p] * 4, group=group)
+    if relu:
+        attrs["activation"] = "Relu"
+    b.node("QConv", ["xq", "w", "b", "m"], "y", **attrs)
+    b.output("y")
+    b.output("xq")
+    x = (rng.standard_normal((n, c, h, w)) * 3).astype(np.float32)
+    return b.graph(), {"x": x}
+
+
+QCONV_CASES = [
+    # n, c, h, w, oc, k, s, group
+    (2, 48, 14, 14, 96, 1, 1, 1),        # pointwise: dense GEMM over NHWC
+    (1, 96, 9, 9, 48, 1, 1, 1),
+    (2, 32, 12, 12, 64, 3, 1, 1),        # tap-major gather, C % 16 == 0
+    (2, 32, 13, 13, 48, 3, 2, 1),
+    (2, 3, 30, 30, 24, 3, 2, 1),         # byte gather, C = 3
+    (2, 24, 15, 15, 48, 3, 2, 1),        # byte gather, C = 24
+    (2, 48, 14, 14, 48, 3, 1, 48),       # depthwise, 16-channel vectors
+    (2, 48, 15, 15, 48, 3, 2, 48),
+    (1, 24, 10, 10, 24, 3, 1, 24),       # depthwise, scalar channels
+]
+
+
+@pytest.mark.parametrize("relu", [False, True])
+@pytest.mark.parametrize("case", QCONV_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_qconv_bit_exact(case, relu, hip_ctx):
+    n, c, h, w, oc, k, s, group = case
+    g, feeds = _qconv_graph(n, c, h, w, oc, k, s, group=group, relu=relu)
+    cmod, got, want = device_run(g, feeds, ctx=hip_ctx)
+    assert cmod.module.fallbacks() == []
+    assert got["xq"].dtype == np.int8 and got["y"].dtype == np.int8
+    np.testing.assert_array_equal(got["xq"], want["xq"])
+    np.testing.assert_array_equal(got["y"], want["y"])
+    v = want["y"].astype(int)
+    assert v.std() > 3 and np.mean(np.abs(v) == 127) < 0.5        # non-degenerate
+
+
+@pytest.mark.parametrize("sched", [None, MfmaSchedule(64, 64, 128, 2, 2, 16, True),
+                                   MfmaSchedule(128, 128, 64, 2, 2, 32, True),
+                                   MfmaSchedule(32, 64, 64, 1, 2, 32, True)],
+                         ids=lambda s: "default" if s is None else s.key())
+@pytest.mark.parametrize("out", ["int8", "float32"])
+def test_qgemm_bit_exact(sched, out, hip_ctx):
+    rng = np.random.default_rng(3)
+    M, N, K = 77, 130, 384
+    b = GraphBuilder("qg")
+    b.input("x", (M, K))
+    b.node("QuantizeLinear", ["x"], "xq", inv_scale=20.0)
+    b.const("w", rng.integers(-127, 128, (N, K)).astype(np.int8))
+    b.const("b", rng.integers(-20000, 20000, N).astype(np.int32))
+    b.const("m", rng.uniform(1e-4, 1e-3, N).astype(np.float32))
+    b.node("QGemm", ["xq", "w", "b", "m"], "y", transB=1, out_dtype=out)
+    b.output("y")
+    feeds = {"x": rng.standard_normal((M, K)).astype(np.float32)}
+    fn = None if sched is None else (lambda node, mnk: sched)
+
+    class _Fixed:
+        def schedule_problem(self, problem):
+            return sched
+
+    _, got, want = device_run(b.graph(), feeds, ctx=hip_ctx,
+                              schedule_fn=None if sched is None else _Fixed())
+    assert got["y"].dtype == want["y"].dtype
+    np.testing.assert_array_equal(got["y"], want["y"])
+    _ = fn
+
+
+def test_qadd_qlut_qgap(hip_ctx):
+    rng = np.random.default_rng(5)
+    b = GraphBuilder("q")
+    b.input("x", (2, 32, 7, 7))
+    b.input("z", (2, 32, 7, 7))
+    b.node("QuantizeLinear", ["x"], "xq", inv_scale=10.0)
+    b.node("QuantizeLinear", ["z"], "zq", inv_scale=30.0)
+    b.node("QAdd", ["xq", "zq"], "s", ma=0.75, mb=0.5)
+    b.const("t", gelu_table(0.1, 0.05))
+    b.node("QLut", ["s", "t"], "l")
+    b.node("QGlobalAveragePool", ["l"], "p", mult=float(np.float32(1 / 49)))
+    b.node("Flatten", ["p"], "f", axis=1)
+    for o in ("s", "l", "f"):
+        b.output(o)
+    feeds = {"x": (rng.standard_normal((2, 32, 7, 7)) * 5).astype(np.float32),
+             "z": (rng.standard_normal((2, 32, 7, 7)) * 5).astype(np.float32)}
+    _, got, want = device_run(b.graph(), feeds, ctx=hip_ctx, all_tensors=True)
+    for name in want:
+        if name in got:
+            np.testing.assert_array_equal(got[name], want[name], err_msg=name)
+    assert np.mean(np.abs(got["s"].astype(int)) == 127) > 0.01          # clamp path exercised
+
+
+@pytest.mark.parametrize("batch", [2, 32])
+def test_repvit_int8_every_tensor_bit_exact(batch, hip_ctx):
+    g = build_repvit_int8(batch=batch)
+    feeds = {"input": make_input(batch)}
+    c, got, want = device_run(g, feeds, ctx=hip_ctx, all_tensors=True)
+    assert c.module.fallbacks() == []
+    n = 0
+    for name, v in got.items():
+        w = want[name]
+        if w.dtype == np.int8:
+            np.testing.assert_array_equal(v, w, err_msg=name)
+            n += 1
+    assert n >= 120
+    np.testing.assert_array_equal(got["logits"], want["logits"])
+
+
+def test_int8_gemm_4096_cube_rows_exact(hip_ctx):
+    """The compute-bound int8 shape (M = N = K = 4096): a sample of output
+    rows against an exact float64 product (|acc| < 2^53)."""
+    from mdlc_amd.codegen.hip.hip_executor import HipExecutor
+    from mdlc_amd.compiler import compile_graph
+
+    rng = np.random.default_rng(11)
+    M = N = K = 4096
+    b = GraphBuilder("q4k")
+    b.input("xq", (M, K), dtype="int8")
+    wq = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    bias = rng.integers(-10000, 10000, N).astype(np.int32)
+    mult = rng.uniform(2e-6, 1e-5, N).astype(np.float32)
+    b.const("w", wq)
+    b.const("b", bias)
+    b.const("m", mult)
+    b.node("QGemm", ["xq", "w", "b", "m"], "y", transB=1)
+    b.output("y")
+    xq = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    c = compile_graph(b.graph(), feeds={"xq": xq})
+    ex = HipExecutor(c.module, hip_ctx)
+    try:
+        y = ex.run({"xq": xq})["outputs"]["y"]
+    finally:
+        ex.close()
+    rows = rng.choice(M, 48, replace=False)
+    acc = (xq[rows].astype(np.float64) @ wq.T.astype(np.float64)).astype(np.int64) + bias
+    f = acc.astype(np.int32).astype(np.float32) * mult
+    want = np.clip(np.rint(f), -127, 127).astype(np.int8)
+    np.testing.assert_array_equal(y[rows], want)
