@@ -126,11 +126,21 @@ class AutotuneCache:
             json.dump(self.entries, f, indent=1, sort_keys=True)
 
 
-def candidates(M: int, N: int, K: int, *, budget: int = 24, seed: int = 0, extra_random: int = 4) -> list:
+def is_implicit_conv(problem: dict) -> bool:
+    """True for convolutions lowered to the implicit-GEMM gather kernels,
+    whose schedules must also satisfy ``MfmaSchedule.conv_valid``."""
+    return problem.get("kind") == "conv" and problem.get("mode", "implicit") == "implicit"
+
+
+def candidates(M: int, N: int, K: int, *, budget: int = 24, seed: int = 0, extra_random: int = 4,
+               conv: bool = False) -> list:
     """The ``budget`` best schedules by the cost model, a seeded random few
-    more, and the shape-aware default."""
+    more, and the shape-aware default (``conv``: implicit-GEMM convolution
+    schedules only)."""
     space = list(gemm_search_space(SPLITS))
     space = [s for s in space if split_slices(K, s)[0] == s.SK or s.SK == 1]
+    if conv:
+        space = [s for s in space if s.conv_valid()]
     ranked = sorted(space, key=lambda s: analytical_cost(s, M, N, K))
     pick = ranked[:budget]
     rest = ranked[budget:]
@@ -209,7 +219,7 @@ def measure(problem: dict, sched: MfmaSchedule, ctx, *, iters: int = 20, warmup:
 
 def tune_problem(problem: dict, *, budget: int = 24, ctx=None, seed: int = 0) -> TuneResult:
     M, N, K = problem["M"], problem["N"], problem["K"]
-    cands = candidates(M, N, K, budget=budget, seed=seed)
+    cands = candidates(M, N, K, budget=budget, seed=seed, conv=is_implicit_conv(problem))
     scored = []
     for s in cands:
         if ctx is not None:
@@ -248,7 +258,7 @@ class Tuner:
     def schedule_problem(self, problem: dict) -> MfmaSchedule:
         key = problem_key(problem)
         hit = self.cache.get_key(key)
-        if hit is not None and hit.is_valid():
+        if hit is not None and (hit.conv_valid() if is_implicit_conv(problem) else hit.is_valid()):
             return hit
         if problem.get("kind") in ("qconv", "qgemm"):
             return default_qschedule(problem["M"], problem["N"], problem["K"])
@@ -276,6 +286,7 @@ def tuned_schedules() -> Tuner:
                  tune_misses=False)
 
 
-__all__ = ["AutotuneCache", "Tuner", "TuneResult", "analytical_cost", "candidates", "measure",
+__all__ = ["AutotuneCache", "Tuner", "TuneResult", "analytical_cost", "candidates",
+           "is_implicit_conv", "measure",
            "precompile", "problem_key", "tune_gemm", "tune_problem", "tuned_schedules",
            "DEFAULT_GEMM"]

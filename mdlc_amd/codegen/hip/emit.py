@@ -173,6 +173,9 @@ class HipCodegen(Int8LoweringMixin):
                    **{k: geo[k] for k in ("C", "H", "W", "KH", "KW", "SH", "SW", "DH", "DW",
                                           "PT", "PB", "PL", "PR", "OH", "OW")}}
         sched = self._schedule(node, (OC, P, K), problem)
+        if self.conv_mode == "implicit" and not sched.conv_valid():
+            raise ValueError(f"schedule {sched.key_full()} does not fit the convolution gather "
+                             f"(threads per block must be a multiple of BN and BK of NT/BN)")
         tap_major = self.conv_mode == "implicit" and geo["C"] % sched.BK == 0
         if tap_major:
             # k ordered (kh, kw, c): weights [OC][KH][KW][C]

@@ -7,30 +7,35 @@
 // 1 = dense row-major read as scalars, 2 = implicit im2col of an NCHW input x
 // (B[k][p] = x[n][c][oh*SH-PT+kh*DH][ow*SW-PL+kw*DW], zero outside) with k
 // ordered (c, kh, kw), 3 = the same gather with k ordered (kh, kw, c) — the
-// weights are packed to match — for Cin % BK == 0: every K tile is then one
-// filter tap, so a column's bounds check and pixel address are computed once
-// per tile and each element costs one add and one load. Either way a
-// convolution needs no column buffer. The output is row-major C[M][ldc]
-// (OUT = 0) or, for convolutions, NCHW: column p = n*hw + s goes to
-// C[(n*M + row)*hw + s] (OUT = 1). With split-K (OUT = 2) the grid holds
-// ksplit slices of K; slice s writes its raw partial sums to the workspace
-// C[(s*M + row)*N + col] and splitk_reduce_f32 adds the slices in order and
-// applies the epilogue.
+// weights are packed to match — for Cin % BK == 0, so every K tile is one
+// filter tap. Either way a convolution needs no column buffer. The output is
+// row-major C[M][ldc] (OUT = 0) or, for convolutions, NCHW: column
+// p = n*hw + s goes to C[(n*M + row)*hw + s] (OUT = 1). With split-K (OUT = 2)
+// the grid holds ksplit slices of K; slice s writes its raw partial sums to
+// the workspace C[(s*M + row)*N + col] and splitk_reduce_f32 adds the slices
+// in order and applies the epilogue.
 //
 // Tiling: a workgroup of WGM x WGN waves (64 lanes each) owns a BM x BN tile;
 // each wave owns (BM/WGM) x (BN/WGN) as a grid of MS x MS MFMA blocks
 // (MS = 32: v_mfma_f32_32x32x2_f32, MS = 16: v_mfma_f32_16x16x4_f32).
-// A and B tiles of depth BK are staged through LDS, double buffered: the next
-// tile's global loads are in flight while the current tile feeds the MFMAs,
-// with one barrier per K step (DB), or single buffered with two barriers
-// per K step (!DB). LDS rows are padded by 4 floats so rows stay
-// 16-byte aligned for ds_read_b128 and consecutive rows shift banks.
+// A and B tiles of depth BK are staged through LDS, double buffered (DB: the
+// next tile's global loads are in flight while the current tile feeds the
+// MFMAs, one barrier per K step) or single buffered (two barriers per step).
+// LDS rows are padded by 4 floats: rows stay 16-byte aligned for
+// ds_read_b128 and consecutive rows start on different banks.
+//
+// Staging cost is kept off the K loop: every global and LDS address a thread
+// touches is computed once before the loop and advanced by k0 per tile. For
+// the convolution gathers each thread owns one output pixel (a B column) and
+// a contiguous run of k rows, so the pixel's bounds check and address are
+// computed once per tile and each element costs one address add and one load;
+// B is then kept k-contiguous in LDS ([n][k]) so a lane's B fragment is one
+// ds_read_b128, like A's.
 //
 // K order inside a tile: the 64 lanes of an MFMA split into 64/MS groups that
 // each supply one k of every instruction. Lane group g walks the contiguous
-// k range [g*BK/(64/MS), (g+1)*BK/(64/MS)), so its A fragment is a run of
-// consecutive floats (one ds_read_b128 per 4 k) and every k of the tile is
-// covered exactly once.
+// k range [g*BK/(64/MS), (g+1)*BK/(64/MS)), so its fragments are runs of
+// consecutive floats and every k of the tile is covered exactly once.
 namespace mdlc {
 
 template <int MS> struct Mfma;
@@ -66,6 +71,10 @@ struct GemmArgs {
   int ksplit, kchunk;            // K slices (grid = tiles * ksplit) and slice depth
 };
 
+__device__ __forceinline__ float pick(const float4& v, int q) {
+  return q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w;
+}
+
 template <int BM, int BN, int BK, int WGM, int WGN, int MS, bool DB, bool VA, int BMODE, int OUT,
           class Epi, class Win>
 __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
@@ -74,7 +83,10 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
   constexpr int MI = WM / MS, NI = WN / MS;
   constexpr int KG = 64 / MS;          // lane groups along k
   constexpr int KSUB = BK / KG;        // k per lane group per tile
-  constexpr int LDA_S = BK + 4, LDB_S = BN + 4;
+  constexpr bool BT = BMODE >= 2;      // B kept k-contiguous in LDS ([n][k])
+  constexpr int LDA_S = BK + 4;
+  constexpr int LDB_S = BT ? BK + 4 : BN + 4;
+  constexpr int B_LDS = BT ? BN * LDB_S : BK * LDB_S;
   static_assert(WM % MS == 0 && WN % MS == 0, "wave tile must be a multiple of the MFMA");
   static_assert(KSUB % 4 == 0, "BK too small for this MFMA shape");
   static_assert(BN % 4 == 0 && BK % 4 == 0, "tile dims must be multiples of 4");
@@ -82,7 +94,7 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
 
   constexpr int NBUF = DB ? 2 : 1;
   __shared__ __attribute__((aligned(16))) float As[NBUF][BM * LDA_S];
-  __shared__ __attribute__((aligned(16))) float Bs[NBUF][BK * LDB_S];
+  __shared__ __attribute__((aligned(16))) float Bs[NBUF][B_LDS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -105,184 +117,159 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
   const int kbeg = ks * g.kchunk;
   const int kend = min(g.K, kbeg + g.kchunk);
 
-  // ---- A tile staging ----------------------------------------------------
+  // ---- A staging: addresses fixed per thread, advanced by k0 --------------
   constexpr int A_ELEMS = VA ? BM * BK / 4 : BM * BK;
   constexpr int A_PT = (A_ELEMS + NT - 1) / NT;
+  const float* a_ptr[A_PT];
+  int a_k[A_PT], a_lds[A_PT];
+  bool a_ok[A_PT];
+#pragma unroll
+  for (int i = 0; i < A_PT; ++i) {
+    const int idx = tid + i * NT;
+    const int cpr = VA ? BK / 4 : BK;
+    const int r = idx / cpr, kc = idx % cpr;
+    const int kk = VA ? kc * 4 : kc;
+    a_ok[i] = idx < A_ELEMS && m0 + r < g.M;
+    a_ptr[i] = g.A + (size_t)min(m0 + r, g.M - 1) * g.lda + kk;
+    a_k[i] = kk;
+    a_lds[i] = r * LDA_S + kk;
+  }
   float4 ra[VA ? A_PT : 1];
   float rs[VA ? 1 : A_PT];
 
-  // ---- B tile staging ----------------------------------------------------
-  constexpr bool BQ = (BMODE != 1);    // quads of 4 consecutive columns
-  constexpr int B_ELEMS = BQ ? BK * BN / 4 : BK * BN;
-  constexpr int B_PT = (B_ELEMS + NT - 1) / NT;
-  static_assert(!BQ || (NT % (BN / 4) == 0), "thread count must cover whole column quads");
-  float4 rb[BQ ? B_PT : 1];
-  float rbs[BQ ? 1 : B_PT];
-
-  // Implicit-im2col state: the column quad each thread gathers is fixed.
-  int cbase[4], cih[4], ciw[4];
-  if (BMODE >= 2) {
-    const int nq = tid % (BN / 4);
-    const int ohw = g.OH * g.OW;
+  // ---- B staging ------------------------------------------------------------
+  // dense: quads (BMODE 0) or scalars (BMODE 1) along n, LDS [k][n]
+  constexpr int BD_ELEMS = BMODE == 0 ? BK * BN / 4 : BK * BN;
+  constexpr int BD_PT = BT ? 1 : (BD_ELEMS + NT - 1) / NT;
+  const float* b_ptr[BD_PT];
+  int b_k[BD_PT], b_lds[BD_PT];
+  bool b_ok[BD_PT];
+  float4 rb[BMODE == 0 ? BD_PT : 1];
+  float rbs[BMODE == 1 ? BD_PT : 1];
+  if (!BT) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      int p = n0 + nq * 4 + j;
-      if (p < g.N) {
-        int n = p / ohw;
-        int s = p - n * ohw;
-        int oh = s / g.OW;
-        int ow = s - oh * g.OW;
-        cbase[j] = n * g.Cin * g.H * g.W;
-        cih[j] = oh * Win::SH - Win::PT;
-        ciw[j] = ow * Win::SW - Win::PL;
-      } else {
-        cbase[j] = 0;
-        cih[j] = -(1 << 28);
-        ciw[j] = 0;
-      }
+    for (int i = 0; i < BD_PT; ++i) {
+      const int idx = tid + i * NT;
+      const int cpr = BMODE == 0 ? BN / 4 : BN;
+      const int kr = idx / cpr, nc = idx % cpr;
+      const int nn = BMODE == 0 ? nc * 4 : nc;
+      b_ok[i] = idx < BD_ELEMS && n0 + nn < g.N;
+      b_ptr[i] = g.B + (size_t)kr * g.ldb + min(n0 + nn, g.N - 1);
+      b_k[i] = kr;
+      b_lds[i] = kr * LDB_S + nn;
+    }
+  }
+  // conv gather: one column (output pixel) per thread, RPT contiguous k rows
+  constexpr int TPC = BT ? NT / BN : 1;           // threads per column
+  constexpr int RPT = BT ? BK / TPC : 1;          // rows per thread per tile
+  static_assert(!BT || (NT % BN == 0 && BK % (NT / BN) == 0), "conv gather needs NT % BN == 0");
+  float rg[RPT];
+  int g_base = 0, g_ih = -(1 << 28), g_iw = 0, g_row = 0, g_lds = 0;
+  if (BT) {
+    const int col = tid % BN;
+    g_row = (tid / BN) * RPT;
+    g_lds = col * LDB_S + g_row;
+    const int p = n0 + col;
+    if (p < g.N) {
+      const int ohw = g.OH * g.OW;
+      const int n = p / ohw;
+      const int s = p - n * ohw;
+      const int oh = s / g.OW;
+      const int ow = s - oh * g.OW;
+      g_base = n * g.Cin * g.H * g.W;
+      g_ih = oh * Win::SH - Win::PT;
+      g_iw = ow * Win::SW - Win::PL;
     }
   }
 
   auto load_tiles = [&](int k0) {
-    if (VA) {
 #pragma unroll
-      for (int i = 0; i < A_PT; ++i) {
-        int idx = tid + i * NT;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (idx < A_ELEMS) {
-          int r = idx / (BK / 4), kq = idx % (BK / 4);
-          int gm = m0 + r, gk = k0 + kq * 4;
-          if (gm < g.M && gk < kend) v = ld4(g.A + (size_t)gm * g.lda + gk);
-        }
-        ra[i] = v;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < A_PT; ++i) {
-        int idx = tid + i * NT;
-        float v = 0.f;
-        if (idx < A_ELEMS) {
-          int r = idx / BK, kk = idx % BK;
-          int gm = m0 + r, gk = k0 + kk;
-          if (gm < g.M && gk < kend) v = g.A[(size_t)gm * g.lda + gk];
-        }
-        rs[i] = v;
+    for (int i = 0; i < A_PT; ++i) {
+      const bool ok = a_ok[i] && k0 + a_k[i] < kend;
+      if (VA) {
+        ra[i] = ok ? ld4(a_ptr[i] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        rs[i] = ok ? a_ptr[i][k0] : 0.f;
       }
     }
     if (BMODE == 0) {
 #pragma unroll
-      for (int i = 0; i < B_PT; ++i) {
-        int idx = tid + i * NT;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (idx < B_ELEMS) {
-          int kr = idx / (BN / 4), nq = idx % (BN / 4);
-          int gk = k0 + kr, gn = n0 + nq * 4;
-          if (gk < kend && gn < g.N) v = ld4(g.B + (size_t)gk * g.ldb + gn);
-        }
-        rb[i] = v;
+      for (int i = 0; i < BD_PT; ++i) {
+        const bool ok = b_ok[i] && k0 + b_k[i] < kend;
+        rb[i] = ok ? ld4(b_ptr[i] + (size_t)k0 * g.ldb) : make_float4(0.f, 0.f, 0.f, 0.f);
       }
     } else if (BMODE == 1) {
 #pragma unroll
-      for (int i = 0; i < B_PT; ++i) {
-        int idx = tid + i * NT;
-        float v = 0.f;
-        if (idx < B_ELEMS) {
-          int kr = idx / BN, nn = idx % BN;
-          int gk = k0 + kr, gn = n0 + nn;
-          if (gk < kend && gn < g.N) v = g.B[(size_t)gk * g.ldb + gn];
-        }
-        rbs[i] = v;
+      for (int i = 0; i < BD_PT; ++i) {
+        const bool ok = b_ok[i] && k0 + b_k[i] < kend;
+        rbs[i] = ok ? b_ptr[i][(size_t)k0 * g.ldb] : 0.f;
       }
     } else if (BMODE == 3) {
-      // One filter tap per tile: k0 = tap * Cin + c0 with c0 % BK == 0.
+      // the whole tile is one tap: k0 = tap * Cin + c0, c0 % BK == 0
       const int HW = g.H * g.W;
       const int tap = k0 / g.Cin;
-      const int c0 = k0 - tap * g.Cin;
+      const int c0 = k0 - tap * g.Cin + g_row;
       const int kh = tap / Win::KW;
       const int kw = tap - kh * Win::KW;
-      int pix[4];
-      bool ok[4];
+      const int ih = g_ih + kh * Win::DH;
+      const int iw = g_iw + kw * Win::DW;
+      const bool ok = (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W && k0 < kend;
+      const float* src = g.B + g_base + (size_t)c0 * HW + (ok ? ih * g.W + iw : 0);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int ih = cih[j] + kh * Win::DH;
-        const int iw = ciw[j] + kw * Win::DW;
-        ok[j] = (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W && k0 < kend;
-        pix[j] = cbase[j] + ih * g.W + iw;
-      }
-#pragma unroll
-      for (int i = 0; i < B_PT; ++i) {
-        int idx = tid + i * NT;
-        float e[4] = {0.f, 0.f, 0.f, 0.f};
-        if (idx < B_ELEMS) {
-          const int cofs = (c0 + idx / (BN / 4)) * HW;
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (ok[j]) e[j] = g.B[pix[j] + cofs];
-        }
-        rb[i] = make_float4(e[0], e[1], e[2], e[3]);
-      }
+      for (int i = 0; i < RPT; ++i) rg[i] = ok ? src[(size_t)i * HW] : 0.f;
     } else {
+      // general (c, kh, kw) order: walk the thread's rows incrementally
       constexpr int KHW = Win::KH * Win::KW;
       const int HW = g.H * g.W;
+      const int k = k0 + g_row;
+      int c = k / KHW;
+      int rr = k - c * KHW;
+      int kh = rr / Win::KW;
+      int kw = rr - kh * Win::KW;
 #pragma unroll
-      for (int i = 0; i < B_PT; ++i) {
-        int idx = tid + i * NT;
-        float e[4] = {0.f, 0.f, 0.f, 0.f};
-        if (idx < B_ELEMS) {
-          int kr = idx / (BN / 4);
-          int k = k0 + kr;
-          if (k < kend) {
-            int c = k / KHW;
-            int rr = k - c * KHW;
-            int kh = rr / Win::KW;
-            int kw = rr - kh * Win::KW;
-            int coff = c * HW;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              int ih = cih[j] + kh * Win::DH;
-              int iw = ciw[j] + kw * Win::DW;
-              if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
-                e[j] = g.B[cbase[j] + coff + ih * g.W + iw];
-            }
+      for (int i = 0; i < RPT; ++i) {
+        const int ih = g_ih + kh * Win::DH;
+        const int iw = g_iw + kw * Win::DW;
+        const bool ok = k + i < kend && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
+        rg[i] = ok ? g.B[g_base + c * HW + ih * g.W + iw] : 0.f;
+        if (++kw == Win::KW) {
+          kw = 0;
+          if (++kh == Win::KH) {
+            kh = 0;
+            ++c;
           }
         }
-        rb[i] = make_float4(e[0], e[1], e[2], e[3]);
       }
     }
   };
 
   auto store_tiles = [&](int buf) {
-    if (VA) {
 #pragma unroll
-      for (int i = 0; i < A_PT; ++i) {
-        int idx = tid + i * NT;
-        if (idx < A_ELEMS) {
-          int r = idx / (BK / 4), kq = idx % (BK / 4);
-          st4(&As[buf][r * LDA_S + kq * 4], ra[i]);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < A_PT; ++i) {
-        int idx = tid + i * NT;
-        if (idx < A_ELEMS) As[buf][(idx / BK) * LDA_S + idx % BK] = rs[i];
+    for (int i = 0; i < A_PT; ++i) {
+      if (tid + i * NT < A_ELEMS) {
+        if (VA) st4(&As[buf][a_lds[i]], ra[i]);
+        else As[buf][a_lds[i]] = rs[i];
       }
     }
-    if (BQ) {
+    if (BMODE == 0) {
 #pragma unroll
-      for (int i = 0; i < B_PT; ++i) {
-        int idx = tid + i * NT;
-        if (idx < B_ELEMS) {
-          int kr = idx / (BN / 4), nq = idx % (BN / 4);
-          st4(&Bs[buf][kr * LDB_S + nq * 4], rb[i]);
-        }
-      }
+      for (int i = 0; i < BD_PT; ++i)
+        if (tid + i * NT < BD_ELEMS) st4(&Bs[buf][b_lds[i]], rb[i]);
+    } else if (BMODE == 1) {
+#pragma unroll
+      for (int i = 0; i < BD_PT; ++i)
+        if (tid + i * NT < BD_ELEMS) Bs[buf][b_lds[i]] = rbs[i];
+    } else if (RPT % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < RPT; i += 4)
+        st4(&Bs[buf][g_lds + i], make_float4(rg[i], rg[i + 1], rg[i + 2], rg[i + 3]));
+    } else if (RPT % 2 == 0) {
+#pragma unroll
+      for (int i = 0; i < RPT; i += 2)
+        *reinterpret_cast<float2*>(&Bs[buf][g_lds + i]) = make_float2(rg[i], rg[i + 1]);
     } else {
 #pragma unroll
-      for (int i = 0; i < B_PT; ++i) {
-        int idx = tid + i * NT;
-        if (idx < B_ELEMS) Bs[buf][(idx / BN) * LDB_S + idx % BN] = rbs[i];
-      }
+      for (int i = 0; i < RPT; ++i) Bs[buf][g_lds + i] = rg[i];
     }
   };
 
@@ -303,20 +290,23 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
       float4 af[MI];
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi) af[mi] = ld4(as + (wm0 + mi * MS + li) * LDA_S + kk);
-      float bf[NI][4];
+      float4 bf[NI];
 #pragma unroll
-      for (int ni = 0; ni < NI; ++ni)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) bf[ni][q] = bs[(kk + q) * LDB_S + wn0 + ni * MS + li];
+      for (int ni = 0; ni < NI; ++ni) {
+        if (BT) {
+          bf[ni] = ld4(bs + (wn0 + ni * MS + li) * LDB_S + kk);
+        } else {
+          const float* bp = bs + kk * LDB_S + wn0 + ni * MS + li;
+          bf[ni] = make_float4(bp[0], bp[LDB_S], bp[2 * LDB_S], bp[3 * LDB_S]);
+        }
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-          for (int ni = 0; ni < NI; ++ni) {
-            float a = q == 0 ? af[mi].x : q == 1 ? af[mi].y : q == 2 ? af[mi].z : af[mi].w;
-            acc[mi][ni] = Mfma<MS>::step(a, bf[ni][q], acc[mi][ni]);
-          }
+          for (int ni = 0; ni < NI; ++ni)
+            acc[mi][ni] = Mfma<MS>::step(pick(af[mi], q), pick(bf[ni], q), acc[mi][ni]);
     }
   };
 

@@ -49,9 +49,11 @@ class MfmaSchedule:
         per = 16 if self.MS == 32 else 4
         return (wm // self.MS) * (wn // self.MS) * per
 
-    def lds_bytes(self, elem_bytes: int = 4) -> int:
-        one = self.BM * (self.BK + 4) + self.BK * (self.BN + 4)
-        return (2 if self.DB else 1) * one * elem_bytes
+    def lds_bytes(self, elem_bytes: int = 4, b_kmajor: bool = False) -> int:
+        """LDS of the A and B tiles; ``b_kmajor`` for the convolution
+        gathers, which keep B as [BN][BK + 4] instead of [BK][BN + 4]."""
+        b = self.BN * (self.BK + 4) if b_kmajor else self.BK * (self.BN + 4)
+        return (2 if self.DB else 1) * (self.BM * (self.BK + 4) + b) * elem_bytes
 
     def is_valid(self) -> bool:
         if min(self.BM, self.BN, self.BK, self.WGM, self.WGN, self.SK) <= 0 or self.MS not in (16, 32):
@@ -70,6 +72,16 @@ class MfmaSchedule:
         if self.lds_bytes() > LDS_LIMIT or self.acc_regs() > MAX_ACC_REGS:
             return False
         return True
+
+    def conv_valid(self) -> bool:
+        """Valid for the implicit-GEMM convolution kernels, whose gather gives
+        each B column to NT / BN threads with BK / (NT / BN) k rows each."""
+        if not self.is_valid():
+            return False
+        nt = self.threads_per_block()
+        if nt % self.BN or self.BK % (nt // self.BN):
+            return False
+        return self.lds_bytes(b_kmajor=True) <= LDS_LIMIT
 
     def key(self) -> str:
         return (f"BM{self.BM}_BN{self.BN}_BK{self.BK}_W{self.WGM}x{self.WGN}"
@@ -137,7 +149,7 @@ def default_schedule(M: int, N: int, K: int) -> MfmaSchedule:
     wgn = 2 if bn >= 64 else 1
     ms = 32 if min(bm // wgm, bn // wgn) >= 32 else 16
     s = MfmaSchedule(bm, bn, 16, wgm, wgn, ms, True, sk)
-    return s if s.is_valid() else DEFAULT_GEMM
+    return s if s.conv_valid() else DEFAULT_GEMM
 
 
 # ----- int8 schedules ---------------------------------------------------------

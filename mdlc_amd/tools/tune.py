@@ -17,7 +17,7 @@ import time
 from concurrent.futures import ProcessPoolExecutor
 
 from mdlc_amd.autotuner.tuner import (
-    TUNED_PATH, AutotuneCache, candidates, precompile, problem_key, tune_problem,
+    TUNED_PATH, AutotuneCache, candidates, is_implicit_conv, precompile, problem_key, tune_problem,
 )
 from mdlc_amd.codegen.schedule import default_schedule
 
@@ -71,7 +71,8 @@ def main(argv=None) -> int:
              if args.only in problem_key(p)]
     print(f"{len(probs)} problems", flush=True)
     if args.precompile:
-        work = [(p, s) for p in probs for s in candidates(p["M"], p["N"], p["K"], budget=args.budget)]
+        work = [(p, s) for p in probs for s in candidates(p["M"], p["N"], p["K"], budget=args.budget,
+                                                          conv=is_implicit_conv(p))]
         t0 = time.time()
         with ProcessPoolExecutor(args.jobs) as pool:
             for i, _ in enumerate(pool.map(_precompile_one, work, chunksize=2), 1):

@@ -136,6 +136,32 @@ def test_conv_split_k(case, sk, mode, hip_ctx):
     assert_close("y", got["y"], want["y"])
 
 
+# Implicit-GEMM schedules covering every gather/staging shape: threads per
+# column 1..16, k rows per thread 1..32 (scalar, pair and quad LDS stores),
+# both MFMA shapes, single and double buffering.
+CONV_SCHEDULES = [
+    MfmaSchedule(64, 64, 16, 2, 2, 32, True),       # 4 threads/column, 4 rows each
+    MfmaSchedule(128, 32, 16, 4, 2, 16, True),      # 16 threads/column, 1 row each
+    MfmaSchedule(128, 64, 16, 4, 2, 16, True),      # 8 threads/column, 2 rows each
+    MfmaSchedule(64, 64, 32, 4, 2, 16, True),       # 8 threads/column, 4 rows each
+    MfmaSchedule(32, 128, 32, 1, 2, 32, False),     # 1 thread/column, 32 rows, single buffered
+]
+
+
+@pytest.mark.parametrize("sched", CONV_SCHEDULES, ids=lambda s: s.key())
+@pytest.mark.parametrize("case", [CONV_CASES[3], CONV_CASES[4], CONV_CASES[6]],
+                         ids=lambda c: "x".join(map(str, c)))
+def test_conv_gather_schedules(case, sched, hip_ctx):
+    """Channel-major (C % BK != 0) and tap-major (C % BK == 0) gathers."""
+    assert sched.conv_valid()
+    g, feeds = _conv_graph(*case)
+    c, got, want = device_run(g, feeds, conv_mode="implicit", ctx=hip_ctx,
+                              schedule_fn=lambda n, mnk: sched)
+    (launch,) = [l for l in c.module.plan if l.kind == "conv"]
+    assert launch.meta["k_order"] == ("tap" if case[1] % sched.BK == 0 else "channel")
+    assert_close("y", got["y"], want["y"])
+
+
 @pytest.mark.parametrize("n", [1, 2, 8])
 def test_conv_no_bias_no_act(n, hip_ctx):
     g, feeds = _conv_graph(n, 5, 11, 11, 6, 3, 1, 1, act=None, bias=False, seed=4)
