@@ -38,20 +38,41 @@ class Int8LoweringMixin:
             raise ValueError(f"{name!r} is {None if info is None else info.dtype}, the kernel "
                              f"writes {want}; rerun shape inference")
 
-    def _emit_qgemm(self, node, sched, a_in, b_dev, bias, mult, out, meta, *, amode, out_f32, lo, win):
-        M, N = meta["M"], meta["N"]
+    def _emit_qgemm(self, node, sched, a_in, b_dev, bias, mult, out, meta, *, amode, out_f32, lo, win,
+                    gv=16):
+        """One int8 GEMM launch. The kernel reads bias and mult four columns
+        at a time, so both are packed zero padded to a multiple of 16; its
+        buffer loads take 32-bit offsets, so every operand stays under 2 GiB."""
+        M, N, K = meta["M"], meta["N"], meta["K"]
         g = self._graph
         self._check_dtype(g, a_in, "int8")
         self._check_dtype(g, out, "float32" if out_f32 else "int8")
-        sig = ("qgemm", sched, amode, out_f32, lo, win)
+        if meta["ldb"] % sched.BK or meta["ldb"] < K:
+            raise ValueError(f"int8 weights must be padded to a multiple of BK={sched.BK}")
+        a_bytes = (M * meta["lda"] if amode == 0 else
+                   (M // (meta["OH"] * meta["OW"])) * meta["H"] * meta["W"] * meta["Cin"])
+        if max(a_bytes, N * meta["ldb"], M * meta["ldc"]) >= 2 ** 31 - 2 ** 20:
+            raise NotImplementedError("HIP codegen: int8 GEMM operand of 2 GiB or more")
+        for name in (bias, mult):
+            if not g.is_constant(name):
+                raise NotImplementedError("HIP codegen: int8 bias and multipliers must be constants")
+        n16 = round16(N)
+        bpad = np.zeros(n16, np.int32)
+        bpad[:N] = np.asarray(g.initializers[bias], np.int32).ravel()
+        mpad = np.zeros(n16, np.float32)
+        mpad[:N] = np.asarray(g.initializers[mult], np.float32).ravel()
+        bias_dev = self._pack_raw(f"{bias}__dev{n16}", bpad)
+        mult_dev = self._pack_raw(f"{mult}__dev{n16}", mpad)
+        cin = meta["Cin"] if amode else 0
+        sig = ("qgemm", sched, amode, gv, cin, out_f32, lo, win)
         tag = "qconv" if amode else "qgemm"
         kname = self._kernel(sig, lambda i: T.qgemm_kernel(
-            f"{tag}_{sched.key()}_a{amode}_{'f32' if out_f32 else 'i8'}_{i}", sched, amode=amode,
-            out_f32=out_f32, lo=lo, win=win))
+            f"{tag}_{sched.key()}_a{amode}{'' if not amode else f'g{gv}'}_{'f32' if out_f32 else 'i8'}_{i}",
+            sched, amode=amode, out_f32=out_f32, lo=lo, win=win, gv=gv, cin=cin))
         tiles = -(-M // sched.BM) * -(-N // sched.BN)
-        self.plan.append(Launch("qgemm", kname, [a_in, b_dev, bias, mult], [out], (tiles, 1, 1),
+        self.plan.append(Launch("qgemm", kname, [a_in, b_dev, bias_dev, mult_dev], [out], (tiles, 1, 1),
                                 (sched.threads_per_block(), 1, 1),
-                                dict(meta, node=node, sched=sched, ops=2 * M * N * meta["K"])))
+                                dict(meta, node=node, sched=sched, ops=2 * M * N * K)))
 
     def _lower_quantizelinear(self, g, node):
         """float32 -> int8 codes; a 4-D NCHW input becomes channels-last."""
@@ -99,16 +120,13 @@ class Int8LoweringMixin:
         P = geo["N"] * geo["OH"] * geo["OW"]
         pointwise = (KH == KW == 1 and geo["SH"] == geo["SW"] == 1 and
                      geo["PT"] == geo["PL"] == geo["PB"] == geo["PR"] == 0)
-        if pointwise and C % 16 == 0:
-            amode = 0
-        elif C % 16 == 0:
-            amode = 1
-        else:
-            amode = 2
-        problem = {"kind": "qconv", "M": P, "N": OC, "K": K, "amode": amode,
+        # gather width: the widest of 16/8/4/2/1 bytes that divides Cin
+        gv = next(v for v in (16, 8, 4, 2, 1) if C % v == 0)
+        amode = 0 if pointwise and gv == 16 else 1
+        problem = {"kind": "qconv", "M": P, "N": OC, "K": K, "amode": amode, "gv": gv,
                    "allow_tuned": True, **{k: geo[k] for k in ("C", "H", "W", "KH", "KW", "SH")}}
         sched = self._qsched(node, (P, OC, K), problem)
-        ldb = round16(K)
+        ldb = -(-K // sched.BK) * sched.BK
         wt = np.zeros((OC, ldb), np.int8)
         wt[:, :K] = warr.transpose(0, 2, 3, 1).reshape(OC, K)        # k = (kh, kw, c)
         wdev = self._pack_raw(f"{w}__dev_tap{ldb}", wt)
@@ -116,7 +134,7 @@ class Int8LoweringMixin:
         meta = {"M": P, "N": OC, "K": K, "lda": C, "ldb": ldb, "ldc": OC, "Cin": C,
                 "H": geo["H"], "W": geo["W"], "OH": geo["OH"], "OW": geo["OW"]}
         self._emit_qgemm(node, sched, x, wdev, b, m, y, meta, amode=amode, out_f32=False, lo=lo,
-                         win=None if amode == 0 else win)
+                         win=None if amode == 0 else win, gv=gv)
 
     def _lower_qgemm(self, g, node):
         x, w, b, m = node.inputs[:4]
@@ -128,9 +146,11 @@ class Int8LoweringMixin:
         lo = 0 if node.attrs.get("activation") == "Relu" else -127
         if K % 16:
             raise NotImplementedError("HIP codegen: QGemm needs K % 16 == 0")
-        ldb = round16(K)
-        wdev = self._pack_raw(f"{w}__dev", np.asarray(g.initializers[w], np.int8))
         sched = self._qsched(node, (M, N, K), {"kind": "qgemm", "M": M, "N": N, "K": K})
+        ldb = -(-K // sched.BK) * sched.BK
+        wt = np.zeros((N, ldb), np.int8)
+        wt[:, :K] = np.asarray(g.initializers[w], np.int8)
+        wdev = self._pack_raw(f"{w}__dev{ldb}", wt)
         meta = {"M": M, "N": N, "K": K, "lda": K, "ldb": ldb, "ldc": N, "Cin": 0, "H": 0, "W": 0,
                 "OH": 0, "OW": 0}
         self._emit_qgemm(node, sched, x, wdev, b, m, node.outputs[0], meta, amode=0,

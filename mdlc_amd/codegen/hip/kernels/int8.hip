@@ -32,24 +32,58 @@ template <> struct MfmaI8<16> {            // v_mfma_i32_16x16x64_i8: 64 k per s
 };
 
 struct QGemmArgs {
-  const i8* __restrict__ A;       // AMODE 0: [M][lda]; AMODE 1/2: NHWC conv input
+  const i8* __restrict__ A;       // AMODE 0: [M][lda]; AMODE 1: NHWC conv input
   const i8* __restrict__ B;       // [N][ldb], K contiguous, zero padded to ldb
-  const int* __restrict__ bias;   // [N]
-  const float* __restrict__ mult; // [N]
+  const int* __restrict__ bias;   // [round16(N)], zero padded
+  const float* __restrict__ mult; // [round16(N)], zero padded
   void* __restrict__ C;           // int8 [M][ldc] or float [M][ldc]
   int M, N, K, lda, ldb, ldc;
-  int Cin, H, W, OH, OW;          // conv geometry (AMODE 1/2); M = batch*OH*OW
+  int Cin, H, W, OH, OW;          // conv geometry (AMODE 1); M = batch*OH*OW
 };
 
+// Raw buffer resource over [p, p + bytes): a load whose offset is at or
+// beyond `bytes` returns zeros instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_over(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+constexpr int kOutside = 0x7ffffff0;   // an offset past every buffer (sizes < 2^31)
+
+template <int BYTES> __device__ __forceinline__ void buffer_gather(__amdgpu_buffer_rsrc_t r, int off,
+                                                                   i8* dst) {
+  if (BYTES == 16) {
+    *reinterpret_cast<intx4*>(dst) = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  } else if (BYTES == 8) {
+    *reinterpret_cast<int2*>(dst) = __builtin_bit_cast(int2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+  } else if (BYTES == 4) {
+    *reinterpret_cast<int*>(dst) = (int)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  } else if (BYTES == 2) {
+    *reinterpret_cast<short*>(dst) = (short)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  } else {
+    *dst = (i8)__builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
+  }
+}
+
 // C[m][n] = q(sum_k A[m][k] * B[n][k] + bias[n]).
-// AMODE 0: dense A, 16-byte loads (K % 16 == 0).
-// AMODE 1: implicit im2col over an NHWC input with k = (kh, kw, c) and
-//          Cin % 16 == 0: each 16-byte chunk is one tap's 16 channels of one
-//          pixel, a single aligned load.
-// AMODE 2: the same gather one byte at a time (any Cin).
+//
+// AMODE 0: dense A [M][lda] (lda % 16 == 0).
+// AMODE 1: implicit im2col over an NHWC input (CIN channels, compile time)
+//          with k = (kh, kw, c); the gather moves GV bytes at a time
+//          (GV divides CIN: one tap's GV channels of one pixel).
 // OUT 0: int8 requantized output (LO = lower clamp); OUT 1: float32
 //        float(acc) * mult[n] (dequantized logits).
-template <int BM, int BN, int BK, int WGM, int WGN, int MS, int AMODE, int OUT, int LO, class Win>
+//
+// Staging goes through raw buffer loads. The K tail needs no test: B is zero
+// padded to ldb (a multiple of BK), so whatever A holds past K is multiplied
+// by zero; rows past M or N and gathered pixels outside the image use an
+// offset past the buffer end and load zeros. Each thread keeps one 16-byte
+// k chunk (kc) of a few tile rows; for dense operands the per-tile k0 moves
+// the buffer base (scalar work), so a load costs no vector ALU at all.
+//
+// The MFMA takes the B tile as its row operand: a lane then holds four
+// consecutive output columns per accumulator group, stored as one 32-bit
+// (int8) or 128-bit (float) write.
+template <int BM, int BN, int BK, int WGM, int WGN, int MS, int AMODE, int GV, int CIN, int OUT, int LO,
+          class Win>
 __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   constexpr int NT = WGM * WGN * 64;
   constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -57,7 +91,12 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   constexpr int KG = 64 / MS;
   constexpr int KSUB = BK / KG;
   constexpr int LDS_ROW = BK + 16;
+  constexpr int CPR = BK / 16;               // 16-byte chunks per tile row
+  constexpr int RSTEP = NT / CPR;            // tile rows between one thread's slots
+  constexpr int A_PT = (BM + RSTEP - 1) / RSTEP, B_PT = (BN + RSTEP - 1) / RSTEP;
   static_assert(KSUB % 16 == 0, "BK too small for this MFMA shape");
+  static_assert(NT % CPR == 0, "rows must map to fixed threads");
+  static_assert(AMODE == 0 || (CIN % GV == 0 && 16 % GV == 0), "gather width must divide Cin");
   typedef typename MfmaI8<MS>::acc_t acc_t;
 
   __shared__ __attribute__((aligned(16))) i8 As[2][BM * LDS_ROW];
@@ -77,101 +116,93 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   const int m0 = (t % tiles_m) * BM;
   const int n0 = (t / tiles_m) * BN;
 
-  constexpr int CPR = BK / 16;               // 16-byte chunks per row
-  constexpr int A_CH = BM * CPR, B_CH = BN * CPR;
-  constexpr int A_PT = (A_CH + NT - 1) / NT, B_PT = (B_CH + NT - 1) / NT;
-  static_assert(NT % CPR == 0, "rows must map to fixed threads");
-  intx4 ra[A_PT], rb[B_PT];
+  const int kc = tid % CPR;
+  const int r0 = tid / CPR;
 
-  // per-thread conv rows (fixed across K tiles)
-  int rbase[A_PT], rih[A_PT], riw[A_PT];
-  if (AMODE != 0) {
-    const int ohw = g.OH * g.OW;
+  // ---- per-thread row state, fixed across K tiles ---------------------------
+  int b_off[B_PT];
 #pragma unroll
-    for (int i = 0; i < A_PT; ++i) {
-      const int p = m0 + (tid + i * NT) / CPR;
-      if (p < g.M) {
-        const int n = p / ohw;
-        const int s = p - n * ohw;
-        const int oh = s / g.OW;
-        const int ow = s - oh * g.OW;
-        rbase[i] = n * g.H * g.W;
-        rih[i] = oh * Win::SH - Win::PT;
-        riw[i] = ow * Win::SW - Win::PL;
-      } else {
-        rbase[i] = 0;
-        rih[i] = -(1 << 28);
-        riw[i] = 0;
-      }
+  for (int i = 0; i < B_PT; ++i) {
+    const int r = r0 + i * RSTEP;
+    b_off[i] = (r < BN && n0 + r < g.N) ? (n0 + r) * g.ldb + kc * 16 : kOutside;
+  }
+  int a_off[A_PT];                  // AMODE 0: row offset; AMODE 1: pixel (ih0, iw0) offset
+  int a_ih[A_PT], a_iw[A_PT];
+#pragma unroll
+  for (int i = 0; i < A_PT; ++i) {
+    const int r = r0 + i * RSTEP;
+    const int p = m0 + r;
+    const bool live = r < BM && p < g.M;
+    if (AMODE == 0) {
+      a_off[i] = live ? p * g.lda + kc * 16 : kOutside;
+    } else {
+      const int ohw = g.OH * g.OW;
+      const int n = p / ohw;
+      const int s = p - n * ohw;
+      const int oh = s / g.OW;
+      const int ow = s - oh * g.OW;
+      const int ih0 = oh * Win::SH - Win::PT;
+      a_ih[i] = live ? ih0 : -(1 << 28);
+      a_iw[i] = ow * Win::SW - Win::PL;
+      a_off[i] = live ? ((n * g.H + ih0) * g.W + a_iw[i]) * CIN : 0;
     }
   }
+  const int a_bytes = AMODE == 0 ? g.M * g.lda : (g.M / (g.OH * g.OW)) * g.H * g.W * CIN;
+  const int b_bytes = g.N * g.ldb;
 
+  intx4 ra[A_PT], rb[B_PT];
+
+  // byte offset in A of k for slot i (gather), or kOutside for padding
+  auto gather_off = [&](int i, int k) -> int {
+    const int tap = k / CIN;
+    const int c = k - tap * CIN;
+    const int kh = tap / Win::KW;
+    const int kw = tap - kh * Win::KW;
+    const int ih = a_ih[i] + kh * Win::DH;
+    const int iw = a_iw[i] + kw * Win::DW;
+    const bool ok = (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
+    return ok ? a_off[i] + (kh * Win::DH * g.W + kw * Win::DW) * CIN + c : kOutside;
+  };
+
+  // k0 may be one tile past K (the loop prefetches unconditionally): the
+  // clamped sizes keep every such load inside its operand or zero.
   auto load_tiles = [&](int k0) {
+    const __amdgpu_buffer_rsrc_t rB = buffer_over(g.B + k0, max(b_bytes - k0, 0));
 #pragma unroll
-    for (int i = 0; i < A_PT; ++i) {
-      const int idx = tid + i * NT;
-      intx4 v = {0, 0, 0, 0};
-      if (idx < A_CH) {
-        const int r = idx / CPR, kc = idx % CPR;
-        const int gm = m0 + r, gk = k0 + kc * 16;
-        if (AMODE == 0) {
-          if (gm < g.M && gk < g.K) v = *reinterpret_cast<const intx4*>(g.A + (size_t)gm * g.lda + gk);
-        } else if (AMODE == 1) {
-          if (gk < g.K) {
-            const int tap = gk / g.Cin;
-            const int c = gk - tap * g.Cin;
-            const int kh = tap / Win::KW, kw = tap - (tap / Win::KW) * Win::KW;
-            const int ih = rih[i] + kh * Win::DH, iw = riw[i] + kw * Win::DW;
-            if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
-              v = *reinterpret_cast<const intx4*>(g.A + ((size_t)rbase[i] + ih * g.W + iw) * g.Cin + c);
-          }
+    for (int i = 0; i < B_PT; ++i)
+      rb[i] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rB, b_off[i], 0, 0));
+    if (AMODE == 0) {
+      const __amdgpu_buffer_rsrc_t rA = buffer_over(g.A + k0, max(a_bytes - k0, 0));
+#pragma unroll
+      for (int i = 0; i < A_PT; ++i)
+        ra[i] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[i], 0, 0));
+    } else {
+      const __amdgpu_buffer_rsrc_t rA = buffer_over(g.A, a_bytes);
+      const int kb = k0 + kc * 16;
+#pragma unroll
+      for (int i = 0; i < A_PT; ++i) {
+        if (GV == 16) {
+          ra[i] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rA, gather_off(i, kb), 0, 0));
         } else {
-          union { intx4 v4; i8 b[16]; } u;
-          u.v4 = v;
+          union { intx4 v; i8 b[16]; } u;
 #pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int k = gk + j;
-            i8 e = 0;
-            if (k < g.K) {
-              const int tap = k / g.Cin;
-              const int c = k - tap * g.Cin;
-              const int kh = tap / Win::KW, kw = tap - (tap / Win::KW) * Win::KW;
-              const int ih = rih[i] + kh * Win::DH, iw = riw[i] + kw * Win::DW;
-              if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
-                e = g.A[((size_t)rbase[i] + ih * g.W + iw) * g.Cin + c];
-            }
-            u.b[j] = e;
-          }
-          v = u.v4;
+          for (int j = 0; j < 16; j += GV) buffer_gather<GV>(rA, gather_off(i, kb + j), &u.b[j]);
+          ra[i] = u.v;
         }
       }
-      ra[i] = v;
-    }
-#pragma unroll
-    for (int i = 0; i < B_PT; ++i) {
-      const int idx = tid + i * NT;
-      intx4 v = {0, 0, 0, 0};
-      if (idx < B_CH) {
-        const int r = idx / CPR, kc = idx % CPR;
-        const int gn = n0 + r, gk = k0 + kc * 16;
-        if (gn < g.N && gk < g.K) v = *reinterpret_cast<const intx4*>(g.B + (size_t)gn * g.ldb + gk);
-      }
-      rb[i] = v;
     }
   };
 
   auto store_tiles = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < A_PT; ++i) {
-      const int idx = tid + i * NT;
-      if (idx < A_CH)
-        *reinterpret_cast<intx4*>(&As[buf][(idx / CPR) * LDS_ROW + (idx % CPR) * 16]) = ra[i];
+      const int r = r0 + i * RSTEP;
+      if (BM % RSTEP == 0 || r < BM) *reinterpret_cast<intx4*>(&As[buf][r * LDS_ROW + kc * 16]) = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < B_PT; ++i) {
-      const int idx = tid + i * NT;
-      if (idx < B_CH)
-        *reinterpret_cast<intx4*>(&Bs[buf][(idx / CPR) * LDS_ROW + (idx % CPR) * 16]) = rb[i];
+      const int r = r0 + i * RSTEP;
+      if (BN % RSTEP == 0 || r < BN) *reinterpret_cast<intx4*>(&Bs[buf][r * LDS_ROW + kc * 16]) = rb[i];
     }
   };
 
@@ -187,9 +218,12 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   load_tiles(0);
   store_tiles(0);
   __syncthreads();
+  // The next tile's loads and LDS stores are unconditional (the last
+  // iteration's go to the idle buffer and are never read), so the loop body
+  // is one basic block the scheduler can interleave with the MFMAs.
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < nk) load_tiles((kt + 1) * BK);
+    load_tiles((kt + 1) * BK);
     const i8* as = &As[cur][0];
     const i8* bs = &Bs[cur][0];
 #pragma unroll
@@ -205,32 +239,57 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = MfmaI8<MS>::step(af[mi], bf[ni], acc[mi][ni]);
+        for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = MfmaI8<MS>::step(bf[ni], af[mi], acc[mi][ni]);
     }
-    if (kt + 1 < nk) store_tiles(cur ^ 1);
+    store_tiles(cur ^ 1);
     __syncthreads();
   }
 
+  // ---- epilogue ---------------------------------------------------------------
+  // acc[mi][ni][4q + j] is C[m0 + wm0 + mi*MS + li][n0 + wn0 + ni*MS + q*8 + lk*4 + j]
+  // (MS = 32; for MS = 16 the single group is at lk*4 + j).
+  constexpr int NG = MfmaI8<MS>::kAcc / 4;
+  const bool vec_ok = (g.ldc & 3) == 0;
 #pragma unroll
-  for (int ni = 0; ni < NI; ++ni) {
-    const int col = n0 + wn0 + ni * MS + li;
-    if (col >= g.N) continue;
-    const int bv = g.bias[col];
-    const float mv = g.mult[col];
+  for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
+    for (int q = 0; q < NG; ++q) {
+      const int col = n0 + wn0 + ni * MS + q * 8 + lk * 4;
+      if (col >= g.N) continue;
+      const intx4 bv = *reinterpret_cast<const intx4*>(g.bias + col);
+      const floatx4 mv = *reinterpret_cast<const floatx4*>(g.mult + col);
+      const bool full = vec_ok && col + 4 <= g.N;
 #pragma unroll
-      for (int r = 0; r < MfmaI8<MS>::kAcc; ++r) {
-        const int row = m0 + wm0 + mi * MS + (r / 4) * 8 + lk * 4 + (r % 4);
-        if (row < g.M) {
-          const int a = acc[mi][ni][r] + bv;
-          if (OUT == 1)
-            static_cast<float*>(g.C)[(size_t)row * g.ldc + col] = (float)a * mv;
-          else
-            static_cast<i8*>(g.C)[(size_t)row * g.ldc + col] = requant(a, mv, (float)LO);
+      for (int mi = 0; mi < MI; ++mi) {
+        const int row = m0 + wm0 + mi * MS + li;
+        if (row >= g.M) continue;
+        if (OUT == 1) {
+          float* cp = static_cast<float*>(g.C) + (size_t)row * g.ldc + col;
+          float o[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[j] = (float)(acc[mi][ni][4 * q + j] + bv[j]) * mv[j];
+          if (full) {
+            *reinterpret_cast<float4*>(cp) = make_float4(o[0], o[1], o[2], o[3]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (col + j < g.N) cp[j] = o[j];
+          }
+        } else {
+          i8* cp = static_cast<i8*>(g.C) + (size_t)row * g.ldc + col;
+          union { int w; i8 b[4]; } o;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o.b[j] = requant(acc[mi][ni][4 * q + j] + bv[j], mv[j], (float)LO);
+          if (full) {
+            *reinterpret_cast<int*>(cp) = o.w;
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (col + j < g.N) cp[j] = o.b[j];
+          }
         }
       }
-  }
+    }
 }
 
 // Depthwise conv over NHWC int8 (one input channel per output channel),

@@ -318,15 +318,16 @@ def elementwise_signature(node: Node, scalar_consts: dict) -> tuple:
 # ----- INT8 quantized path ----------------------------------------------------
 
 def qgemm_kernel(name: str, sched: MfmaSchedule, *, amode: int, out_f32: bool, lo: int,
-                 win: Optional[tuple] = None) -> tuple:
+                 win: Optional[tuple] = None, gv: int = 16, cin: int = 0) -> tuple:
     """int8 MFMA GEMM / implicit conv with the requant (or dequant) epilogue.
-    ABI: (A, B, bias, mult, C, int M, int N, int K, int lda, int ldb, int ldc,
-    int Cin, int H, int W, int OH, int OW)."""
+    ``amode`` 0 = dense A, 1 = NHWC gather of ``gv`` bytes over ``cin``
+    channels. ABI: (A, B, bias, mult, C, int M, int N, int K, int lda,
+    int ldb, int ldc, int Cin, int H, int W, int OH, int OW)."""
     s = sched
     winty = "mdlc::NoWin" if win is None else "mdlc::ConvWin<%d, %d, %d, %d, %d, %d, %d, %d>" % tuple(win)
     nt = s.threads_per_block()
     tmpl = (f"mdlc::qgemm_i8_mfma<{s.BM}, {s.BN}, {s.BK}, {s.WGM}, {s.WGN}, {s.MS}, {amode}, "
-            f"{1 if out_f32 else 0}, {int(lo)}, {winty}>")
+            f"{gv}, {cin}, {1 if out_f32 else 0}, {int(lo)}, {winty}>")
     return name, (
         f'extern "C" __global__ __launch_bounds__({nt}) void {name}(\n'
         "    const signed char* __restrict__ A, const signed char* __restrict__ B,\n"

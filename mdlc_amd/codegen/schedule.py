@@ -24,7 +24,8 @@ from dataclasses import asdict, dataclass
 from typing import Iterator
 
 LDS_LIMIT = 160 * 1024         # bytes one workgroup may allocate (gfx950: 160 KB per CU)
-MAX_ACC_REGS = 128             # accumulator registers per lane we allow
+MAX_ACC_REGS = 128             # fp32 accumulator registers per lane we allow
+MAX_QACC_REGS = 256            # int8: a 128x128 wave tile, accumulators in AGPRs
 
 
 @dataclass(frozen=True)
@@ -169,7 +170,7 @@ def qsched_valid(s: MfmaSchedule) -> bool:
     nt = s.threads_per_block()
     if nt > 1024 or nt % (s.BK // 16):
         return False
-    if 2 * (s.BM + s.BN) * (s.BK + 16) > LDS_LIMIT or s.acc_regs() > MAX_ACC_REGS:
+    if 2 * (s.BM + s.BN) * (s.BK + 16) > LDS_LIMIT or s.acc_regs() > MAX_QACC_REGS:
         return False
     return True
 
