@@ -24,7 +24,7 @@ from typing import Optional
 
 from mdlc_amd.codegen.schedule import (
     CUS, DEFAULT_GEMM, MfmaSchedule, default_qschedule, default_schedule, gemm_search_space,
-    split_slices,
+    qgemm_search_space, qsched_valid, split_slices,
 )
 
 LDS_PER_CU = 160 * 1024
@@ -72,10 +72,39 @@ def analytical_cost(sched: MfmaSchedule, M: int, N: int, K: int) -> float:
     return t
 
 
+INT8_OPS_PER_CU_CLK = 8192          # v_mfma_i32_32x32x32_i8, dense
+
+
+def analytical_qcost(sched: MfmaSchedule, M: int, N: int, K: int) -> float:
+    """Estimated microseconds for one int8 GEMM: the fp32 model's occupancy
+    and tile-quantization terms at the int8 MFMA rate, with K padded to BK
+    and one byte per operand element."""
+    tiles = -(-M // sched.BM) * -(-N // sched.BN)
+    waves = sched.WGM * sched.WGN
+    by_lds = max(1, LDS_PER_CU // (2 * (sched.BM + sched.BN) * (sched.BK + 16)))
+    vgprs = 64 + sched.acc_regs() + 32
+    by_regs = max(1, (512 // vgprs) * 4 // waves)
+    resident = max(1, min(by_lds, by_regs, 32 // waves))
+    rounds = -(-tiles // (CUS * resident))
+    per_cu = min(resident, -(-tiles // CUS))
+    eff = min(1.0, 0.35 + 0.3 * per_cu * waves / 4.0)
+    kp = -(-K // sched.BK) * sched.BK
+    round_us = 2.0 * sched.BM * sched.BN * kp * per_cu / (INT8_OPS_PER_CU_CLK * CLOCK_GHZ * 1e3) / eff
+    traffic = -(-N // sched.BN) * M * K + -(-M // sched.BM) * K * N + M * N
+    return max(rounds * round_us, traffic / (HBM_GBS * 1e3)) + LAUNCH_US
+
+
+def is_int8(problem: dict) -> bool:
+    return problem.get("kind") in ("qconv", "qgemm")
+
+
 def problem_key(problem: dict) -> str:
     M, N, K = problem["M"], problem["N"], problem["K"]
-    if problem.get("kind") in ("qconv", "qgemm"):
-        return f"i8:{problem['kind']}:{M}x{N}x{K}:a{problem.get('amode', 0)}"
+    if problem.get("kind") == "qconv":
+        return (f"i8:qconv:{M}x{N}x{K}:{problem['KH']}x{problem['KW']}s{problem['SH']}"
+                f":{problem['C']}x{problem['H']}x{problem['W']}")
+    if problem.get("kind") == "qgemm":
+        return f"i8:qgemm:{M}x{N}x{K}"
     if problem.get("kind") == "conv":
         return (f"conv:{M}x{N}x{K}:{problem['KH']}x{problem['KW']}s{problem['SH']}"
                 f":{problem['C']}x{problem['H']}x{problem['W']}:{problem.get('mode', 'implicit')}")
@@ -152,6 +181,28 @@ def candidates(M: int, N: int, K: int, *, budget: int = 24, seed: int = 0, extra
     return pick
 
 
+def qcandidates(M: int, N: int, K: int, *, budget: int = 24, seed: int = 0,
+                extra_random: int = 4) -> list:
+    """int8 counterpart of ``candidates`` over ``qgemm_search_space``."""
+    space = list(qgemm_search_space())
+    ranked = sorted(space, key=lambda s: analytical_qcost(s, M, N, K))
+    pick = ranked[:budget]
+    rest = ranked[budget:]
+    rng = random.Random(seed)
+    pick += rng.sample(rest, min(extra_random, len(rest)))
+    d = default_qschedule(M, N, K)
+    if d not in pick:
+        pick.append(d)
+    return pick
+
+
+def problem_candidates(problem: dict, *, budget: int = 24, seed: int = 0) -> list:
+    M, N, K = problem["M"], problem["N"], problem["K"]
+    if is_int8(problem):
+        return qcandidates(M, N, K, budget=budget, seed=seed)
+    return candidates(M, N, K, budget=budget, seed=seed, conv=is_implicit_conv(problem))
+
+
 def _problem_graph(problem: dict, sched_seed: int = 0):
     """A one-group graph (and feeds) that lowers to exactly this problem."""
     import numpy as np
@@ -160,6 +211,32 @@ def _problem_graph(problem: dict, sched_seed: int = 0):
 
     rng = np.random.default_rng(sched_seed)
     b = GraphBuilder("tune")
+    if problem["kind"] == "qconv":
+        n, c, h, w = problem["batch"], problem["C"], problem["H"], problem["W"]
+        oc, kh, kw = problem["N"], problem["KH"], problem["KW"]
+        b.input("x", (n, c, h, w))
+        b.node("QuantizeLinear", ["x"], "xq", inv_scale=20.0)
+        b.const("w", rng.integers(-127, 128, (oc, c, kh, kw)).astype(np.int8))
+        b.const("b", rng.integers(-1000, 1000, oc).astype(np.int32))
+        b.const("m", rng.uniform(1e-4, 1e-3, oc).astype(np.float32))
+        attrs = dict(kernel_shape=[kh, kw], strides=[problem["SH"], problem["SW"]],
+                     dilations=[problem["DH"], problem["DW"]],
+                     pads=[problem["PT"], problem["PL"], problem["PB"], problem["PR"]])
+        if problem.get("relu"):
+            attrs["activation"] = "Relu"
+        b.node("QConv", ["xq", "w", "b", "m"], "y", **attrs)
+        b.output("y")
+        return b.graph(), {"x": rng.standard_normal((n, c, h, w)).astype(np.float32)}
+    if problem["kind"] == "qgemm":
+        M, N, K = problem["M"], problem["N"], problem["K"]
+        b.input("xq", (M, K), dtype="int8")
+        b.const("w", rng.integers(-127, 128, (N, K)).astype(np.int8))
+        b.const("b", rng.integers(-1000, 1000, N).astype(np.int32))
+        b.const("m", rng.uniform(2e-6, 1e-5, N).astype(np.float32))
+        b.node("QGemm", ["xq", "w", "b", "m"], "y", transB=1,
+               out_dtype="float32" if problem.get("out_f32") else "int8")
+        b.output("y")
+        return b.graph(), {"xq": rng.integers(-127, 128, (M, K)).astype(np.int8)}
     if problem["kind"] == "conv":
         n, c, h, w = problem["batch"], problem["C"], problem["H"], problem["W"]
         oc, kh, kw = problem["M"], problem["KH"], problem["KW"]
@@ -219,7 +296,8 @@ def measure(problem: dict, sched: MfmaSchedule, ctx, *, iters: int = 20, warmup:
 
 def tune_problem(problem: dict, *, budget: int = 24, ctx=None, seed: int = 0) -> TuneResult:
     M, N, K = problem["M"], problem["N"], problem["K"]
-    cands = candidates(M, N, K, budget=budget, seed=seed, conv=is_implicit_conv(problem))
+    cands = problem_candidates(problem, budget=budget, seed=seed)
+    model = analytical_qcost if is_int8(problem) else analytical_cost
     scored = []
     for s in cands:
         if ctx is not None:
@@ -228,7 +306,7 @@ def tune_problem(problem: dict, *, budget: int = 24, ctx=None, seed: int = 0) ->
             except Exception:
                 continue
         else:
-            metric = analytical_cost(s, M, N, K)
+            metric = model(s, M, N, K)
         scored.append((s, metric))
     scored.sort(key=lambda t: t[1])
     best, best_metric = scored[0]
@@ -258,10 +336,13 @@ class Tuner:
     def schedule_problem(self, problem: dict) -> MfmaSchedule:
         key = problem_key(problem)
         hit = self.cache.get_key(key)
-        if hit is not None and (hit.conv_valid() if is_implicit_conv(problem) else hit.is_valid()):
+        if is_int8(problem):
+            if hit is not None and qsched_valid(hit):
+                return hit
+            if not self.tune_misses:
+                return default_qschedule(problem["M"], problem["N"], problem["K"])
+        elif hit is not None and (hit.conv_valid() if is_implicit_conv(problem) else hit.is_valid()):
             return hit
-        if problem.get("kind") in ("qconv", "qgemm"):
-            return default_qschedule(problem["M"], problem["N"], problem["K"])
         if not self.tune_misses:
             return default_schedule(problem["M"], problem["N"], problem["K"])
         res = tune_problem(problem, budget=self.budget, ctx=self.ctx)
@@ -287,6 +368,7 @@ def tuned_schedules() -> Tuner:
 
 
 __all__ = ["AutotuneCache", "Tuner", "TuneResult", "analytical_cost", "candidates",
-           "is_implicit_conv", "measure",
+           "is_implicit_conv", "is_int8", "measure", "problem_candidates", "qcandidates",
+           "analytical_qcost",
            "precompile", "problem_key", "tune_gemm", "tune_problem", "tuned_schedules",
            "DEFAULT_GEMM"]

@@ -27,7 +27,7 @@ class Int8LoweringMixin:
 
     def _qsched(self, node, mnk, problem):
         fn = getattr(self.schedule_fn, "schedule_problem", None)
-        sched = fn(problem) if fn is not None and problem.get("allow_tuned", True) else None
+        sched = fn(problem) if fn is not None else self.schedule_fn(node, mnk)
         if sched is None or not qsched_valid(sched):
             sched = default_qschedule(*mnk)
         return sched
@@ -124,7 +124,9 @@ class Int8LoweringMixin:
         gv = next(v for v in (16, 8, 4, 2, 1) if C % v == 0)
         amode = 0 if pointwise and gv == 16 else 1
         problem = {"kind": "qconv", "M": P, "N": OC, "K": K, "amode": amode, "gv": gv,
-                   "allow_tuned": True, **{k: geo[k] for k in ("C", "H", "W", "KH", "KW", "SH")}}
+                   "batch": geo["N"], "relu": lo == 0,
+                   **{k: geo[k] for k in ("C", "H", "W", "KH", "KW", "SH", "SW", "DH", "DW",
+                                          "PT", "PB", "PL", "PR", "OH", "OW")}}
         sched = self._qsched(node, (P, OC, K), problem)
         ldb = -(-K // sched.BK) * sched.BK
         wt = np.zeros((OC, ldb), np.int8)
@@ -146,7 +148,8 @@ class Int8LoweringMixin:
         lo = 0 if node.attrs.get("activation") == "Relu" else -127
         if K % 16:
             raise NotImplementedError("HIP codegen: QGemm needs K % 16 == 0")
-        sched = self._qsched(node, (M, N, K), {"kind": "qgemm", "M": M, "N": N, "K": K})
+        sched = self._qsched(node, (M, N, K), {"kind": "qgemm", "M": M, "N": N, "K": K,
+                                               "out_f32": out_f32})
         ldb = -(-K // sched.BK) * sched.BK
         wt = np.zeros((N, ldb), np.int8)
         wt[:, :K] = np.asarray(g.initializers[w], np.int8)

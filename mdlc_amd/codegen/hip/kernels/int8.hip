@@ -150,8 +150,6 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   const int a_bytes = AMODE == 0 ? g.M * g.lda : (g.M / (g.OH * g.OW)) * g.H * g.W * CIN;
   const int b_bytes = g.N * g.ldb;
 
-  intx4 ra[A_PT], rb[B_PT];
-
   // byte offset in A of k for slot i (gather), or kOutside for padding
   auto gather_off = [&](int i, int k) -> int {
     const int tap = k / CIN;
@@ -164,9 +162,9 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
     return ok ? a_off[i] + (kh * Win::DH * g.W + kw * Win::DW) * CIN + c : kOutside;
   };
 
-  // k0 may be one tile past K (the loop prefetches unconditionally): the
-  // clamped sizes keep every such load inside its operand or zero.
-  auto load_tiles = [&](int k0) {
+  // k0 may be up to two tiles past K (the loop prefetches unconditionally):
+  // the clamped sizes keep every such load inside its operand or zero.
+  auto load_tiles = [&](int k0, intx4 (&ra)[A_PT], intx4 (&rb)[B_PT]) {
     const __amdgpu_buffer_rsrc_t rB = buffer_over(g.B + k0, max(b_bytes - k0, 0));
 #pragma unroll
     for (int i = 0; i < B_PT; ++i)
@@ -193,7 +191,7 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
     }
   };
 
-  auto store_tiles = [&](int buf) {
+  auto store_tiles = [&](int buf, const intx4 (&ra)[A_PT], const intx4 (&rb)[B_PT]) {
 #pragma unroll
     for (int i = 0; i < A_PT; ++i) {
       const int r = r0 + i * RSTEP;
@@ -214,18 +212,9 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
 #pragma unroll
       for (int r = 0; r < MfmaI8<MS>::kAcc; ++r) acc[mi][ni][r] = 0;
 
-  const int nk = (g.K + BK - 1) / BK;
-  load_tiles(0);
-  store_tiles(0);
-  __syncthreads();
-  // The next tile's loads and LDS stores are unconditional (the last
-  // iteration's go to the idle buffer and are never read), so the loop body
-  // is one basic block the scheduler can interleave with the MFMAs.
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    load_tiles((kt + 1) * BK);
-    const i8* as = &As[cur][0];
-    const i8* bs = &Bs[cur][0];
+  auto compute = [&](int buf) {
+    const i8* as = &As[buf][0];
+    const i8* bs = &Bs[buf][0];
 #pragma unroll
     for (int s = 0; s < KSUB / 16; ++s) {
       const int kk = lk * KSUB + s * 16;
@@ -241,8 +230,51 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = MfmaI8<MS>::step(bf[ni], af[mi], acc[mi][ni]);
     }
-    store_tiles(cur ^ 1);
+  };
+
+  // Global loads run ahead of the MFMAs through registers. With two
+  // register sets (when the accumulators leave room) they run two K tiles
+  // ahead: iteration kt issues tile kt+2's loads into the set tile kt
+  // arrived in, computes tile kt from LDS, then stores tile kt+1 (loaded an
+  // iteration earlier) into the idle LDS buffer. With one set, iteration kt
+  // loads tile kt+1 and stores it at its end. Loads and stores are
+  // unconditional (past the end they fetch zeros or stay inside the
+  // operands, and land in a buffer nobody reads), so each iteration is one
+  // basic block the scheduler can interleave with the MFMAs. The waves raise
+  // their issue priority while they feed the matrix cores.
+  constexpr bool kTwoSets = MfmaI8<MS>::kAcc * MI * NI + 8 * (A_PT + B_PT) <= 192;
+  intx4 ra0[A_PT], rb0[B_PT], ra1[kTwoSets ? A_PT : 1], rb1[kTwoSets ? B_PT : 1];
+  const int nk = (g.K + BK - 1) / BK;
+  if constexpr (kTwoSets) {
+    load_tiles(0, ra0, rb0);
+    load_tiles(BK, ra1, rb1);
+    store_tiles(0, ra0, rb0);
     __syncthreads();
+    auto step = [&](int kt, intx4 (&ra_in)[A_PT], intx4 (&rb_in)[B_PT], intx4 (&ra_nx)[A_PT],
+                    intx4 (&rb_nx)[B_PT]) {
+      load_tiles((kt + 2) * BK, ra_in, rb_in);
+      __builtin_amdgcn_s_setprio(1);
+      compute(kt & 1);
+      __builtin_amdgcn_s_setprio(0);
+      store_tiles((kt + 1) & 1, ra_nx, rb_nx);
+      __syncthreads();
+    };
+    for (int kt = 0; kt < nk; kt += 2) {
+      step(kt, ra0, rb0, ra1, rb1);
+      if (kt + 1 < nk) step(kt + 1, ra1, rb1, ra0, rb0);
+    }
+  } else {
+    load_tiles(0, ra0, rb0);
+    store_tiles(0, ra0, rb0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      load_tiles((kt + 1) * BK, ra0, rb0);
+      __builtin_amdgcn_s_setprio(1);
+      compute(kt & 1);
+      __builtin_amdgcn_s_setprio(0);
+      store_tiles((kt + 1) & 1, ra0, rb0);
+      __syncthreads();
+    }
   }
 
   // ---- epilogue ---------------------------------------------------------------

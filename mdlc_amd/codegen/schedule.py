@@ -176,24 +176,20 @@ def qsched_valid(s: MfmaSchedule) -> bool:
 
 
 def default_qschedule(M: int, N: int, K: int) -> MfmaSchedule:
-    """Shape-aware int8 default: 128-wide tiles shrunk until the grid covers
-    the chip twice, BK = 64 bytes (2 MFMA steps of 32)."""
-    bm = 128 if M > 64 else (64 if M > 32 else 32)
-    bn = 128 if N > 64 else (64 if N > 32 else 32)
-    tiles = lambda: -(-M // bm) * -(-N // bn)  # noqa: E731
-    while tiles() < 2 * CUS and (bm > 64 or bn > 64):
-        if bm >= bn and bm > 64:
-            bm //= 2
-        else:
-            bn //= 2
-    wgm = 2 if bm >= 64 else 1
-    wgn = 2 if bn >= 64 else 1
-    ms = 32 if min(bm // wgm, bn // wgn) >= 32 else 16
-    bk = 64 if ms == 32 else 64
-    s = MfmaSchedule(bm, bn, bk, wgm, wgn, ms, True, 1)
-    if not qsched_valid(s):
-        s = MfmaSchedule(64, 64, 64, 2, 2, 32, True, 1)
-    return s
+    """Shape-aware int8 default: the largest of a few measured tiles whose
+    grid still covers every CU once, else the smallest."""
+    ladder = (MfmaSchedule(256, 256, 128, 4, 2, 32, True, 1),
+              MfmaSchedule(256, 128, 128, 4, 2, 32, True, 1),
+              MfmaSchedule(128, 128, 64, 2, 2, 32, True, 1),
+              MfmaSchedule(128, 64, 64, 2, 2, 32, True, 1),
+              MfmaSchedule(64, 64, 64, 2, 2, 32, True, 1),
+              MfmaSchedule(64, 32, 64, 2, 1, 32, True, 1),
+              MfmaSchedule(32, 32, 64, 1, 1, 32, True, 1))
+    kpad = -(-K // 64) * 64
+    for s in ladder:
+        if s.BK <= kpad and s.BN <= max(32, N) * 2 and -(-M // s.BM) * -(-N // s.BN) >= CUS:
+            return s
+    return ladder[-1]
 
 
 def qgemm_search_space():

@@ -17,9 +17,9 @@ import time
 from concurrent.futures import ProcessPoolExecutor
 
 from mdlc_amd.autotuner.tuner import (
-    TUNED_PATH, AutotuneCache, candidates, is_implicit_conv, precompile, problem_key, tune_problem,
+    TUNED_PATH, AutotuneCache, is_int8, precompile, problem_candidates, problem_key, tune_problem,
 )
-from mdlc_amd.codegen.schedule import default_schedule
+from mdlc_amd.codegen.schedule import default_qschedule, default_schedule
 
 
 class _Recorder:
@@ -37,15 +37,21 @@ class _Recorder:
 def model_problems(model: str, batch: int, conv_mode: str) -> list:
     from mdlc_amd.compiler import compile_graph
 
+    if model == "int8_gemm":          # the square int8 GEMM benchmark, M = N = K = batch
+        return [{"kind": "qgemm", "M": batch, "N": batch, "K": batch, "out_f32": False}]
     if model == "resnet18":
-        from mdlc_amd.tools.build_resnet18 import build_resnet18 as build
+        from mdlc_amd.tools.build_resnet18 import build_resnet18
+        graph = build_resnet18(batch=batch, calibrate=False)
     elif model == "mobilenetv2":
-        from mdlc_amd.tools.build_mobilenetv2 import build_mobilenetv2 as build
+        from mdlc_amd.tools.build_mobilenetv2 import build_mobilenetv2
+        graph = build_mobilenetv2(batch=batch, calibrate=False)
+    elif model == "repvit_int8":
+        from mdlc_amd.tools.build_repvit_int8 import build_repvit_int8
+        graph = build_repvit_int8(batch=batch)
     else:
         raise SystemExit(f"unknown model {model!r}")
     rec = _Recorder()
-    compile_graph(build(batch=batch, calibrate=False), batch=batch, schedule_fn=rec,
-                  conv_mode=conv_mode)
+    compile_graph(graph, batch=batch, schedule_fn=rec, conv_mode=conv_mode)
     return list(rec.problems.values())
 
 
@@ -71,8 +77,7 @@ def main(argv=None) -> int:
              if args.only in problem_key(p)]
     print(f"{len(probs)} problems", flush=True)
     if args.precompile:
-        work = [(p, s) for p in probs for s in candidates(p["M"], p["N"], p["K"], budget=args.budget,
-                                                          conv=is_implicit_conv(p))]
+        work = [(p, s) for p in probs for s in problem_candidates(p, budget=args.budget)]
         t0 = time.time()
         with ProcessPoolExecutor(args.jobs) as pool:
             for i, _ in enumerate(pool.map(_precompile_one, work, chunksize=2), 1):
@@ -88,7 +93,7 @@ def main(argv=None) -> int:
     for p in probs:
         t0 = time.time()
         res = tune_problem(p, budget=args.budget, ctx=ctx)
-        d = default_schedule(p["M"], p["N"], p["K"]).key_full()
+        d = (default_qschedule if is_int8(p) else default_schedule)(p["M"], p["N"], p["K"]).key_full()
         dflt = next((m for k, m in res.ranking if k == d), float("nan"))
         cache.put_key(res.key, res.best, res.best_metric, True)
         cache.save()

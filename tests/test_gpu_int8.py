@@ -67,9 +67,41 @@ def test_qconv_bit_exact(case, relu, hip_ctx):
     assert v.std() > 3 and np.mean(np.abs(v) == 127) < 0.5        # non-degenerate
 
 
+class _Fixed:
+    """A schedule source that returns one schedule for every problem."""
+
+    def __init__(self, sched):
+        self.sched = sched
+
+    def schedule_problem(self, problem):
+        return self.sched
+
+
+QSCHEDULES = [MfmaSchedule(256, 256, 128, 4, 2, 32, True),   # two register sets in flight
+              MfmaSchedule(256, 256, 64, 2, 2, 32, True),    # 256 accumulators, one set
+              MfmaSchedule(128, 64, 128, 2, 1, 16, True),
+              MfmaSchedule(32, 32, 64, 1, 1, 32, True)]
+
+
+@pytest.mark.parametrize("sched", QSCHEDULES, ids=lambda s: s.key())
+@pytest.mark.parametrize("case", [(2, 3, 17, 17, 24, 3, 2), (2, 6, 11, 11, 40, 3, 1),
+                                  (2, 12, 11, 11, 24, 3, 2), (2, 24, 9, 9, 48, 3, 1),
+                                  (2, 48, 9, 9, 72, 3, 2), (2, 64, 7, 7, 264, 1, 1)],
+                         ids=lambda c: "x".join(map(str, c)))
+def test_qconv_gather_widths_and_tiles(case, sched, hip_ctx):
+    """Gather widths 1/2/4/8/16 bytes (C = 3, 6, 12, 24, 48) and a dense
+    pointwise conv whose N is not a tile multiple, under tiles from 32x32 to
+    256x256 (ragged M, N and K everywhere)."""
+    g, feeds = _qconv_graph(*case, relu=True, seed=4)
+    cmod, got, want = device_run(g, feeds, ctx=hip_ctx, schedule_fn=_Fixed(sched))
+    (launch,) = [l for l in cmod.module.plan if l.kind == "qgemm"]
+    assert launch.meta["sched"] == sched
+    np.testing.assert_array_equal(got["y"], want["y"])
+
+
 @pytest.mark.parametrize("sched", [None, MfmaSchedule(64, 64, 128, 2, 2, 16, True),
                                    MfmaSchedule(128, 128, 64, 2, 2, 32, True),
-                                   MfmaSchedule(32, 64, 64, 1, 2, 32, True)],
+                                   MfmaSchedule(32, 64, 64, 1, 2, 32, True)] + QSCHEDULES[:2],
                          ids=lambda s: "default" if s is None else s.key())
 @pytest.mark.parametrize("out", ["int8", "float32"])
 def test_qgemm_bit_exact(sched, out, hip_ctx):
@@ -84,17 +116,10 @@ def test_qgemm_bit_exact(sched, out, hip_ctx):
     b.node("QGemm", ["xq", "w", "b", "m"], "y", transB=1, out_dtype=out)
     b.output("y")
     feeds = {"x": rng.standard_normal((M, K)).astype(np.float32)}
-    fn = None if sched is None else (lambda node, mnk: sched)
-
-    class _Fixed:
-        def schedule_problem(self, problem):
-            return sched
-
     _, got, want = device_run(b.graph(), feeds, ctx=hip_ctx,
-                              schedule_fn=None if sched is None else _Fixed())
+                              schedule_fn=None if sched is None else _Fixed(sched))
     assert got["y"].dtype == want["y"].dtype
     np.testing.assert_array_equal(got["y"], want["y"])
-    _ = fn
 
 
 def test_qadd_qlut_qgap(hip_ctx):
