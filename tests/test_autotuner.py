@@ -86,14 +86,24 @@ def test_tuner_caches_per_shape(tmp_path):
 
 def test_shipped_tuned_schedules_are_valid():
     """The measured gfx950 schedules shipped with the backend parse and are
-    valid, and cover every conv/GEMM problem of ResNet-18 at batch 32."""
+    valid for their kernel (fp32 GEMM, implicit-GEMM conv gather, or int8),
+    and cover every conv/GEMM problem of the benchmarked models."""
+    from mdlc_amd.codegen.schedule import qsched_valid
     from mdlc_amd.tools.tune import model_problems
 
     cache = AutotuneCache(TUNED_PATH)
     assert cache.entries
     for key, e in cache.entries.items():
-        assert MfmaSchedule(**e["sched"]).is_valid(), key
+        s = MfmaSchedule(**e["sched"])
+        if key.startswith("i8:"):
+            assert qsched_valid(s), key
+        elif key.startswith("conv:") and key.endswith(":implicit"):
+            assert s.conv_valid(), key
+        else:
+            assert s.is_valid(), key
         assert e["measured"]
-    for p in model_problems("resnet18", 32, "implicit"):
-        assert problem_key(p) in cache.entries, problem_key(p)
-    assert DEFAULT_GEMM.is_valid()
+    for model, batch in (("resnet18", 32), ("resnet18", 1), ("mobilenetv2", 32),
+                         ("mobilenetv2", 1), ("repvit_int8", 32)):
+        for p in model_problems(model, batch, "implicit"):
+            assert problem_key(p) in cache.entries, (model, batch, problem_key(p))
+    assert DEFAULT_GEMM.is_valid() and DEFAULT_GEMM.conv_valid()
