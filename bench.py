@@ -105,15 +105,20 @@ def roofline(prof, *, traffic_json: str = "") -> tuple:
         log(f"  {name:58s} {d['launches']:3d}x {d['ms']:8.3f} ms {rate}")
     name, d = max(per.items(), key=lambda kv: kv[1]["ms"])
     avg = d["ms"] / d["launches"]
-    if d["flops"]:
-        ach = d["flops"] / d["launches"] / (avg * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": ach, "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s"}
-    elif d["ops"]:
-        ach = d["ops"] / d["launches"] / (avg * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": ach, "peak": PEAK_INT8_MFMA_TOPS, "unit": "TOP/s"}
+    # The bound is the roofline's: matrix cores when the kernel's algorithmic
+    # intensity (flops or ops per algorithmic HBM byte) is at or above the
+    # ridge point peak/8 TB/s, else HBM bandwidth.
+    work, peak, unit = ((d["flops"], PEAK_FP32_MFMA_TFLOPS, "TFLOP/s") if d["flops"] else
+                        (d["ops"], PEAK_INT8_MFMA_TOPS, "TOP/s"))
+    ridge = peak * 1e12 / (PEAK_HBM_GBS * 1e9)
+    if work and (not d["bytes"] or work / d["bytes"] >= ridge):
+        ach = work / d["launches"] / (avg * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": ach, "peak": peak, "unit": unit}
     else:
         ach = d["bytes"] / d["launches"] / (avg * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": ach, "peak": PEAK_HBM_GBS, "unit": "GB/s"}
+    if work and d["bytes"]:
+        roof["intensity"] = work / d["bytes"]
     roof["frac"] = roof["achieved"] / roof["peak"]
     roof["traffic"] = None
     if traffic_json and os.path.exists(traffic_json):

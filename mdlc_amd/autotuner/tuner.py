@@ -23,8 +23,8 @@ from dataclasses import dataclass, field
 from typing import Optional
 
 from mdlc_amd.codegen.schedule import (
-    CUS, DEFAULT_GEMM, MfmaSchedule, default_qschedule, default_schedule, gemm_search_space,
-    qgemm_search_space, qsched_valid, split_slices,
+    CUS, DEFAULT_GEMM, MfmaSchedule, default_qdw_schedule, default_qschedule, default_schedule,
+    gemm_search_space, qdw_search_space, qdw_valid, qgemm_search_space, qsched_valid, split_slices,
 )
 
 LDS_PER_CU = 160 * 1024
@@ -95,7 +95,7 @@ def analytical_qcost(sched: MfmaSchedule, M: int, N: int, K: int) -> float:
 
 
 def is_int8(problem: dict) -> bool:
-    return problem.get("kind") in ("qconv", "qgemm")
+    return problem.get("kind") in ("qconv", "qgemm", "qdw")
 
 
 def problem_key(problem: dict) -> str:
@@ -105,6 +105,9 @@ def problem_key(problem: dict) -> str:
                 f":{problem['C']}x{problem['H']}x{problem['W']}")
     if problem.get("kind") == "qgemm":
         return f"i8:qgemm:{M}x{N}x{K}"
+    if problem.get("kind") == "qdw":
+        return (f"i8:qdw:{M}x{N}:{problem['KH']}x{problem['KW']}s{problem['SH']}"
+                f":{problem['C']}x{problem['H']}x{problem['W']}")
     if problem.get("kind") == "conv":
         return (f"conv:{M}x{N}x{K}:{problem['KH']}x{problem['KW']}s{problem['SH']}"
                 f":{problem['C']}x{problem['H']}x{problem['W']}:{problem.get('mode', 'implicit')}")
@@ -198,6 +201,8 @@ def qcandidates(M: int, N: int, K: int, *, budget: int = 24, seed: int = 0,
 
 def problem_candidates(problem: dict, *, budget: int = 24, seed: int = 0) -> list:
     M, N, K = problem["M"], problem["N"], problem["K"]
+    if problem.get("kind") == "qdw":          # the small space is measured whole
+        return list(qdw_search_space())
     if is_int8(problem):
         return qcandidates(M, N, K, budget=budget, seed=seed)
     return candidates(M, N, K, budget=budget, seed=seed, conv=is_implicit_conv(problem))
@@ -211,16 +216,17 @@ def _problem_graph(problem: dict, sched_seed: int = 0):
 
     rng = np.random.default_rng(sched_seed)
     b = GraphBuilder("tune")
-    if problem["kind"] == "qconv":
+    if problem["kind"] in ("qconv", "qdw"):
         n, c, h, w = problem["batch"], problem["C"], problem["H"], problem["W"]
         oc, kh, kw = problem["N"], problem["KH"], problem["KW"]
+        group = c if problem["kind"] == "qdw" else 1
         b.input("x", (n, c, h, w))
         b.node("QuantizeLinear", ["x"], "xq", inv_scale=20.0)
-        b.const("w", rng.integers(-127, 128, (oc, c, kh, kw)).astype(np.int8))
+        b.const("w", rng.integers(-127, 128, (oc, c // group, kh, kw)).astype(np.int8))
         b.const("b", rng.integers(-1000, 1000, oc).astype(np.int32))
         b.const("m", rng.uniform(1e-4, 1e-3, oc).astype(np.float32))
         attrs = dict(kernel_shape=[kh, kw], strides=[problem["SH"], problem["SW"]],
-                     dilations=[problem["DH"], problem["DW"]],
+                     dilations=[problem["DH"], problem["DW"]], group=group,
                      pads=[problem["PT"], problem["PL"], problem["PB"], problem["PR"]])
         if problem.get("relu"):
             attrs["activation"] = "Relu"
@@ -336,7 +342,12 @@ class Tuner:
     def schedule_problem(self, problem: dict) -> MfmaSchedule:
         key = problem_key(problem)
         hit = self.cache.get_key(key)
-        if is_int8(problem):
+        if problem.get("kind") == "qdw":
+            if hit is not None and qdw_valid(hit):
+                return hit
+            if not self.tune_misses:
+                return default_qdw_schedule(problem["M"])
+        elif is_int8(problem):
             if hit is not None and qsched_valid(hit):
                 return hit
             if not self.tune_misses:

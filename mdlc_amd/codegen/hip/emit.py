@@ -49,9 +49,16 @@ VIEW_OPS = {"Flatten", "Reshape", "Identity", "Squeeze", "Unsqueeze"}
 
 
 class HipCodegen(Int8LoweringMixin):
-    def __init__(self, schedule_fn: Optional[ScheduleFn] = None, *, conv_mode: str = "implicit") -> None:
+    def __init__(self, schedule_fn: Optional[ScheduleFn] = None, *, conv_mode: str = "implicit",
+                 int8_depthwise: str = "mfma") -> None:
+        """``int8_depthwise``: "mfma" runs 16-channel-aligned int8 depthwise
+        convs as block-diagonal GEMMs on the matrix cores, "vector" keeps
+        them on the per-pixel vector kernel."""
         if conv_mode not in ("implicit", "im2col"):
             raise ValueError(f"conv_mode must be 'implicit' or 'im2col', not {conv_mode!r}")
+        if int8_depthwise not in ("mfma", "vector"):
+            raise ValueError(f"int8_depthwise must be 'mfma' or 'vector', not {int8_depthwise!r}")
+        self.int8_depthwise_mfma = int8_depthwise == "mfma"
         if schedule_fn is None:
             from mdlc_amd.autotuner.tuner import tuned_schedules
 
@@ -186,7 +193,10 @@ class HipCodegen(Int8LoweringMixin):
         bias = [node.inputs[2]] if has_bias else []
         meta = {"M": OC, "N": P, "K": K, "lda": lda, "with_bias": has_bias, "node": node,
                 "weight_2d": (OC, K), "out_4d": (N, OC, OH, OW), "sched": sched,
-                "flops": 2 * OC * P * K}
+                "flops": 2 * OC * P * K,
+                # algorithmic HBM bytes: input, weights, bias and output once each
+                "bytes": 4 * (N * geo["C"] * geo["H"] * geo["W"] + OC * K + P * OC
+                              + (OC if has_bias else 0))}
         epi = dict(bias_mode="row", act=act, attrs=self._act_attrs(a), act_sig=self._act_sig(a),
                    alpha=1.0, beta=1.0, ldc=0, hw=OH * OW)
         if self.conv_mode == "implicit":
@@ -273,7 +283,9 @@ class HipCodegen(Int8LoweringMixin):
             "dwconv", kname, ins, [node.outputs[0]], (-(-total // 256), 1, 1), (256, 1, 1),
             {**{k: geo[k] for k in ("N", "C", "H", "W", "OC", "OH", "OW", "PT", "PL")},
              "with_bias": has_bias, "node": node,
-             "flops": 2 * total * geo["KH"] * geo["KW"]}))
+             "flops": 2 * total * geo["KH"] * geo["KW"],
+             "bytes": 4 * (geo["N"] * geo["C"] * geo["H"] * geo["W"] + total
+                           + geo["OC"] * geo["KH"] * geo["KW"] + (geo["OC"] if has_bias else 0))}))
 
     def _lower_gemm(self, g: Graph, node: Node) -> None:
         a = node.attrs
@@ -321,7 +333,8 @@ class HipCodegen(Int8LoweringMixin):
         sched = self._schedule(node, (M, N, K), problem)
         meta = {"M": M, "N": N, "K": K, "lda": lda, "ldb": ldb, "transA": ta, "transB": tb,
                 "alpha": alpha, "beta": beta, "with_bias": has_bias, "node": node,
-                "sched": sched, "flops": 2 * M * N * K}
+                "sched": sched, "flops": 2 * M * N * K,
+                "bytes": 4 * (M * K + K * N + M * N + (N if has_bias else 0))}
         epi = dict(bias_mode="col", act=act, attrs=self._act_attrs(a), act_sig=self._act_sig(a),
                    alpha=alpha, beta=beta, ldc=N, hw=0)
         self._emit_gemm("gemm", sched, [adev, bdev], bias_ins, node.outputs[0], meta, epi,
@@ -418,5 +431,5 @@ class HipCodegen(Int8LoweringMixin):
 
 
 def emit_hip_module(graph: Graph, schedule_fn: Optional[ScheduleFn] = None, *,
-                    conv_mode: str = "implicit") -> HipModule:
-    return HipCodegen(schedule_fn, conv_mode=conv_mode).lower(graph)
+                    conv_mode: str = "implicit", int8_depthwise: str = "mfma") -> HipModule:
+    return HipCodegen(schedule_fn, conv_mode=conv_mode, int8_depthwise=int8_depthwise).lower(graph)

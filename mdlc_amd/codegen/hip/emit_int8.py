@@ -15,7 +15,9 @@ import numpy as np
 
 from mdlc_amd.codegen.hip import templates as T
 from mdlc_amd.codegen.hip.plan import Launch, round16
-from mdlc_amd.codegen.schedule import default_qschedule, qsched_valid
+from mdlc_amd.codegen.schedule import (
+    default_qdw_schedule, default_qschedule, qdw_valid, qsched_valid,
+)
 from mdlc_amd.passes.shape_inference import conv_geometry
 
 
@@ -39,7 +41,7 @@ class Int8LoweringMixin:
                              f"writes {want}; rerun shape inference")
 
     def _emit_qgemm(self, node, sched, a_in, b_dev, bias, mult, out, meta, *, amode, out_f32, lo, win,
-                    gv=16):
+                    gv=16, epi=0, aux=None, depthwise=False):
         """One int8 GEMM launch. The kernel reads bias and mult four columns
         at a time, so both are packed zero padded to a multiple of 16; its
         buffer loads take 32-bit offsets, so every operand stays under 2 GiB."""
@@ -63,16 +65,25 @@ class Int8LoweringMixin:
         mpad[:N] = np.asarray(g.initializers[mult], np.float32).ravel()
         bias_dev = self._pack_raw(f"{bias}__dev{n16}", bpad)
         mult_dev = self._pack_raw(f"{mult}__dev{n16}", mpad)
-        cin = meta["Cin"] if amode else 0
-        sig = ("qgemm", sched, amode, gv, cin, out_f32, lo, win)
-        tag = "qconv" if amode else "qgemm"
+        cin = sched.BN if depthwise else (meta["Cin"] if amode else 0)
+        sig = ("qgemm", sched, amode, gv, cin, out_f32, lo, win, epi, depthwise)
+        tag = "qdwmfma" if depthwise else ("qconv" if amode else "qgemm")
+        etag = ("", "_lut", "_add")[epi]
         kname = self._kernel(sig, lambda i: T.qgemm_kernel(
-            f"{tag}_{sched.key()}_a{amode}{'' if not amode else f'g{gv}'}_{'f32' if out_f32 else 'i8'}_{i}",
-            sched, amode=amode, out_f32=out_f32, lo=lo, win=win, gv=gv, cin=cin))
+            f"{tag}_{sched.key()}_a{amode}{'' if not amode else f'g{gv}'}_{'f32' if out_f32 else 'i8'}"
+            f"{etag}_{i}", sched, amode=amode, out_f32=out_f32, lo=lo, win=win, gv=gv, cin=cin, epi=epi,
+            depthwise=depthwise))
         tiles = -(-M // sched.BM) * -(-N // sched.BN)
-        self.plan.append(Launch("qgemm", kname, [a_in, b_dev, bias_dev, mult_dev], [out], (tiles, 1, 1),
+        ins = [a_in, b_dev, bias_dev, mult_dev] + ([aux] if aux else [])
+        # algorithmic HBM bytes: activation, weights, bias/mult, output, residual
+        a_read = a_bytes if amode else M * K
+        w_read = N * (K // sched.BN if depthwise else K)
+        ops = meta.get("depthwise_ops", 2 * M * N * K)
+        nbytes = (a_read + w_read + 8 * N + M * N * (4 if out_f32 else 1) + (M * N if epi == 2 else 0))
+        self.plan.append(Launch("qgemm", kname, ins, [out], (tiles, 1, 1),
                                 (sched.threads_per_block(), 1, 1),
-                                dict(meta, node=node, sched=sched, ops=2 * M * N * K)))
+                                dict(meta, node=node, sched=sched, ops=ops, bytes=nbytes,
+                                     epilogue=epi)))
 
     def _lower_quantizelinear(self, g, node):
         """float32 -> int8 codes; a 4-D NCHW input becomes channels-last."""
@@ -100,9 +111,14 @@ class Int8LoweringMixin:
         self.layout[y] = "NHWC"
         warr = np.asarray(g.initializers[w], np.int8)
         if geo["group"] != 1:
+            if node.attrs.get("epilogue"):
+                raise NotImplementedError("HIP codegen: fused epilogue on a grouped int8 conv")
             if geo["ICG"] != 1 or geo["OC"] != geo["C"]:
                 raise NotImplementedError("HIP codegen: int8 grouped conv (only depthwise)")
             C = geo["C"]
+            if C % 16 == 0 and self.int8_depthwise_mfma:
+                self._lower_qdw_mfma(g, node, geo, warr, lo)
+                return
             win = (geo["KH"], geo["KW"], geo["SH"], geo["SW"], geo["DH"], geo["DW"])
             cv = 16 if C % 16 == 0 else 1
             kname = self._kernel(("qdw", win, cv, lo), lambda i: T.qdwconv_kernel(
@@ -135,8 +151,51 @@ class Int8LoweringMixin:
         win = (KH, KW, geo["SH"], geo["SW"], geo["DH"], geo["DW"], geo["PT"], geo["PL"])
         meta = {"M": P, "N": OC, "K": K, "lda": C, "ldb": ldb, "ldc": OC, "Cin": C,
                 "H": geo["H"], "W": geo["W"], "OH": geo["OH"], "OW": geo["OW"]}
+        epi, aux = 0, None
+        kind = node.attrs.get("epilogue")
+        if kind == "lut":
+            epi, aux = 1, node.inputs[4]
+            if not g.is_constant(aux) or np.asarray(g.initializers[aux]).size != 256:
+                raise NotImplementedError("HIP codegen: a fused lookup needs a constant 256-entry table")
+        elif kind == "add":
+            epi, aux = 2, node.inputs[4]
+            if self.layout.get(aux) != "NHWC" or self._shape(g, aux) != self._shape(g, y):
+                raise NotImplementedError("HIP codegen: a fused residual must match the conv output")
+            meta.update(res_mult=float(node.attrs["res_mult"]), acc_mult=float(node.attrs["acc_mult"]))
+        elif kind:
+            raise NotImplementedError(f"HIP codegen: QConv epilogue {kind!r}")
         self._emit_qgemm(node, sched, x, wdev, b, m, y, meta, amode=amode, out_f32=False, lo=lo,
-                         win=None if amode == 0 else win, gv=gv)
+                         win=None if amode == 0 else win, gv=gv, epi=epi, aux=aux)
+
+    def _lower_qdw_mfma(self, g, node, geo, warr, lo):
+        """Depthwise int8 conv (C % 16 == 0) on the matrix cores: 16-channel
+        blocks, k = (tap, channel within the block), block-diagonal weights."""
+        x, _, b, m = node.inputs[:4]
+        y = node.outputs[0]
+        C, KH, KW = geo["C"], geo["KH"], geo["KW"]
+        P = geo["N"] * geo["OH"] * geo["OW"]
+        problem = {"kind": "qdw", "M": P, "N": C, "K": KH * KW * 16, "batch": geo["N"],
+                   "relu": lo == 0,
+                   **{k: geo[k] for k in ("C", "H", "W", "KH", "KW", "SH", "SW", "DH", "DW",
+                                          "PT", "PB", "PL", "PR", "OH", "OW")}}
+        fn = getattr(self.schedule_fn, "schedule_problem", None)
+        sched = fn(problem) if fn is not None else self.schedule_fn(node, (P, C, problem["K"]))
+        if sched is None or not qdw_valid(sched):
+            sched = default_qdw_schedule(P)
+        K = KH * KW * sched.BN
+        ldb = -(-K // sched.BK) * sched.BK
+        wt = np.zeros((C, ldb), np.int8)
+        n = np.arange(C)
+        taps = warr.reshape(C, KH * KW)
+        for t in range(KH * KW):
+            wt[n, t * sched.BN + n % sched.BN] = taps[:, t]
+        wdev = self._pack_raw(f"{node.inputs[1]}__dev_blockdiag{ldb}", wt)
+        win = (KH, KW, geo["SH"], geo["SW"], geo["DH"], geo["DW"], geo["PT"], geo["PL"])
+        meta = {"M": P, "N": C, "K": K, "lda": C, "ldb": ldb, "ldc": C, "Cin": C,
+                "H": geo["H"], "W": geo["W"], "OH": geo["OH"], "OW": geo["OW"],
+                "depthwise_ops": 2 * P * C * KH * KW}
+        self._emit_qgemm(node, sched, x, wdev, b, m, y, meta, amode=1, out_f32=False, lo=lo, win=win,
+                         gv=16, depthwise=True)
 
     def _lower_qgemm(self, g, node):
         x, w, b, m = node.inputs[:4]

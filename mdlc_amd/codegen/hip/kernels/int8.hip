@@ -37,8 +37,10 @@ struct QGemmArgs {
   const int* __restrict__ bias;   // [round16(N)], zero padded
   const float* __restrict__ mult; // [round16(N)], zero padded
   void* __restrict__ C;           // int8 [M][ldc] or float [M][ldc]
+  const i8* __restrict__ aux;     // EPI 1: 256-entry table; EPI 2: residual [M][ldc]
   int M, N, K, lda, ldb, ldc;
   int Cin, H, W, OH, OW;          // conv geometry (AMODE 1); M = batch*OH*OW
+  float res_mult, acc_mult;       // EPI 2 multipliers of the residual and of the codes
 };
 
 // Raw buffer resource over [p, p + bytes): a load whose offset is at or
@@ -69,8 +71,20 @@ template <int BYTES> __device__ __forceinline__ void buffer_gather(__amdgpu_buff
 // AMODE 1: implicit im2col over an NHWC input (CIN channels, compile time)
 //          with k = (kh, kw, c); the gather moves GV bytes at a time
 //          (GV divides CIN: one tap's GV channels of one pixel).
+// DWG 1:   depthwise conv as a block-diagonal GEMM: the input has g.Cin
+//          channels, k = (kh, kw, c) runs over CIN = BN channels, and a
+//          workgroup gathers the BN channels of its own output columns
+//          (offset n0). B row n holds w[n][tap] at k = (tap, n - n0) and
+//          zeros elsewhere, so the matrix cores do BN times the depthwise
+//          arithmetic — cheap next to what the vector ALUs would take — and
+//          each input byte is still fetched once per tap.
 // OUT 0: int8 requantized output (LO = lower clamp); OUT 1: float32
 //        float(acc) * mult[n] (dequantized logits).
+// EPI (OUT 0 only): 0 = the requantized codes; 1 = table[code + 128] (a
+//        fused lookup, table staged in LDS); 2 = a fused residual add,
+//        clamp(rint(f32(f32(r) * res_mult) + f32(f32(code) * acc_mult)))
+//        with r read at the output's position. Both are the unfused ops'
+//        arithmetic, so the fused kernel is bit-identical to the pair.
 //
 // Staging goes through raw buffer loads. The K tail needs no test: B is zero
 // padded to ldb (a multiple of BK), so whatever A holds past K is multiplied
@@ -83,7 +97,7 @@ template <int BYTES> __device__ __forceinline__ void buffer_gather(__amdgpu_buff
 // consecutive output columns per accumulator group, stored as one 32-bit
 // (int8) or 128-bit (float) write.
 template <int BM, int BN, int BK, int WGM, int WGN, int MS, int AMODE, int GV, int CIN, int OUT, int LO,
-          class Win>
+          int EPI, int DWG, class Win>
 __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   constexpr int NT = WGM * WGN * 64;
   constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -97,6 +111,7 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   static_assert(KSUB % 16 == 0, "BK too small for this MFMA shape");
   static_assert(NT % CPR == 0, "rows must map to fixed threads");
   static_assert(AMODE == 0 || (CIN % GV == 0 && 16 % GV == 0), "gather width must divide Cin");
+  static_assert(DWG == 0 || (AMODE == 1 && CIN == BN), "depthwise tiles span one channel block");
   typedef typename MfmaI8<MS>::acc_t acc_t;
 
   __shared__ __attribute__((aligned(16))) i8 As[2][BM * LDS_ROW];
@@ -126,6 +141,7 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
     const int r = r0 + i * RSTEP;
     b_off[i] = (r < BN && n0 + r < g.N) ? (n0 + r) * g.ldb + kc * 16 : kOutside;
   }
+  const int pix_stride = DWG ? g.Cin : CIN;   // bytes between neighbouring pixels (AMODE 1)
   int a_off[A_PT];                  // AMODE 0: row offset; AMODE 1: pixel (ih0, iw0) offset
   int a_ih[A_PT], a_iw[A_PT];
 #pragma unroll
@@ -144,10 +160,10 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
       const int ih0 = oh * Win::SH - Win::PT;
       a_ih[i] = live ? ih0 : -(1 << 28);
       a_iw[i] = ow * Win::SW - Win::PL;
-      a_off[i] = live ? ((n * g.H + ih0) * g.W + a_iw[i]) * CIN : 0;
+      a_off[i] = live ? ((n * g.H + ih0) * g.W + a_iw[i]) * pix_stride + (DWG ? n0 : 0) : 0;
     }
   }
-  const int a_bytes = AMODE == 0 ? g.M * g.lda : (g.M / (g.OH * g.OW)) * g.H * g.W * CIN;
+  const int a_bytes = AMODE == 0 ? g.M * g.lda : (g.M / (g.OH * g.OW)) * g.H * g.W * pix_stride;
   const int b_bytes = g.N * g.ldb;
 
   // byte offset in A of k for slot i (gather), or kOutside for padding
@@ -159,7 +175,7 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
     const int ih = a_ih[i] + kh * Win::DH;
     const int iw = a_iw[i] + kw * Win::DW;
     const bool ok = (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
-    return ok ? a_off[i] + (kh * Win::DH * g.W + kw * Win::DW) * CIN + c : kOutside;
+    return ok ? a_off[i] + (kh * Win::DH * g.W + kw * Win::DW) * pix_stride + c : kOutside;
   };
 
   // k0 may be up to two tiles past K (the loop prefetches unconditionally):
@@ -282,6 +298,19 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   // (MS = 32; for MS = 16 the single group is at lk*4 + j).
   constexpr int NG = MfmaI8<MS>::kAcc / 4;
   const bool vec_ok = (g.ldc & 3) == 0;
+  __shared__ i8 table[EPI == 1 ? 256 : 1];
+  if (EPI == 1) {                 // the K loop ended with a barrier: LDS is free
+    for (int i = tid; i < 256; i += NT) table[i] = g.aux[i];
+    __syncthreads();
+  }
+  auto finish = [&](i8 code, i8 res) -> i8 {
+    if (EPI == 1) return table[(int)code + 128];
+    if (EPI == 2) {
+      const float v = (float)res * g.res_mult + (float)code * g.acc_mult;
+      return (i8)(int)fminf(fmaxf(rintf(v), -127.0f), 127.0f);
+    }
+    return code;
+  };
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
@@ -308,10 +337,22 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
               if (col + j < g.N) cp[j] = o[j];
           }
         } else {
-          i8* cp = static_cast<i8*>(g.C) + (size_t)row * g.ldc + col;
-          union { int w; i8 b[4]; } o;
+          const size_t off = (size_t)row * g.ldc + col;
+          i8* cp = static_cast<i8*>(g.C) + off;
+          union { int w; i8 b[4]; } o, r;
+          r.w = 0;
+          if (EPI == 2) {
+            if (full) {
+              r.w = *reinterpret_cast<const int*>(g.aux + off);
+            } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) o.b[j] = requant(acc[mi][ni][4 * q + j] + bv[j], mv[j], (float)LO);
+              for (int j = 0; j < 4; ++j)
+                if (col + j < g.N) r.b[j] = g.aux[off + j];
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            o.b[j] = finish(requant(acc[mi][ni][4 * q + j] + bv[j], mv[j], (float)LO), r.b[j]);
           if (full) {
             *reinterpret_cast<int*>(cp) = o.w;
           } else {

@@ -318,22 +318,30 @@ def elementwise_signature(node: Node, scalar_consts: dict) -> tuple:
 # ----- INT8 quantized path ----------------------------------------------------
 
 def qgemm_kernel(name: str, sched: MfmaSchedule, *, amode: int, out_f32: bool, lo: int,
-                 win: Optional[tuple] = None, gv: int = 16, cin: int = 0) -> tuple:
+                 win: Optional[tuple] = None, gv: int = 16, cin: int = 0, epi: int = 0,
+                 depthwise: bool = False) -> tuple:
     """int8 MFMA GEMM / implicit conv with the requant (or dequant) epilogue.
     ``amode`` 0 = dense A, 1 = NHWC gather of ``gv`` bytes over ``cin``
-    channels. ABI: (A, B, bias, mult, C, int M, int N, int K, int lda,
-    int ldb, int ldc, int Cin, int H, int W, int OH, int OW)."""
+    channels; ``epi`` 1 = fused table lookup, 2 = fused residual add;
+    ``depthwise``: block-diagonal depthwise conv (``cin`` = BN channels per
+    block, the tensor's channel count passed as Cin).
+    ABI: (A, B, bias, mult, C, aux, int M, int N, int K, int lda, int ldb,
+    int ldc, int Cin, int H, int W, int OH, int OW, float res_mult,
+    float acc_mult)."""
     s = sched
     winty = "mdlc::NoWin" if win is None else "mdlc::ConvWin<%d, %d, %d, %d, %d, %d, %d, %d>" % tuple(win)
     nt = s.threads_per_block()
     tmpl = (f"mdlc::qgemm_i8_mfma<{s.BM}, {s.BN}, {s.BK}, {s.WGM}, {s.WGN}, {s.MS}, {amode}, "
-            f"{gv}, {cin}, {1 if out_f32 else 0}, {int(lo)}, {winty}>")
+            f"{gv}, {cin}, {1 if out_f32 else 0}, {int(lo)}, {epi}, {1 if depthwise else 0}, {winty}>")
     return name, (
         f'extern "C" __global__ __launch_bounds__({nt}) void {name}(\n'
         "    const signed char* __restrict__ A, const signed char* __restrict__ B,\n"
         "    const int* __restrict__ bias, const float* __restrict__ mult, void* __restrict__ C,\n"
-        "    int M, int N, int K, int lda, int ldb, int ldc, int Cin, int H, int W, int OH, int OW) {\n"
-        "  mdlc::QGemmArgs g{A, B, bias, mult, C, M, N, K, lda, ldb, ldc, Cin, H, W, OH, OW};\n"
+        "    const signed char* __restrict__ aux,\n"
+        "    int M, int N, int K, int lda, int ldb, int ldc, int Cin, int H, int W, int OH, int OW,\n"
+        "    float res_mult, float acc_mult) {\n"
+        "  mdlc::QGemmArgs g{A, B, bias, mult, C, aux, M, N, K, lda, ldb, ldc, Cin, H, W, OH, OW,\n"
+        "                    res_mult, acc_mult};\n"
         f"  {tmpl}(g);\n}}\n")
 
 

@@ -192,6 +192,26 @@ def default_qschedule(M: int, N: int, K: int) -> MfmaSchedule:
     return ladder[-1]
 
 
+def qdw_valid(s: MfmaSchedule) -> bool:
+    """Schedules of the block-diagonal depthwise int8 kernel: 16-channel
+    column tiles on 16x16x64 MFMAs, one wave column."""
+    return qsched_valid(s) and s.BN == 16 and s.MS == 16 and s.WGN == 1
+
+
+def default_qdw_schedule(M: int) -> MfmaSchedule:
+    return (MfmaSchedule(256, 16, 64, 4, 1, 16, True, 1) if M >= 256 * 64
+            else MfmaSchedule(64, 16, 64, 1, 1, 16, True, 1))
+
+
+def qdw_search_space():
+    for bm in (64, 128, 256, 512):
+        for bk in (64, 128, 256):
+            for wgm in (1, 2, 4, 8):
+                s = MfmaSchedule(bm, 16, bk, wgm, 1, 16, True, 1)
+                if qdw_valid(s):
+                    yield s
+
+
 def qgemm_search_space():
     for bm in (32, 64, 128, 256):
         for bn in (32, 64, 128, 256):

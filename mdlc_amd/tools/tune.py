@@ -19,7 +19,7 @@ from concurrent.futures import ProcessPoolExecutor
 from mdlc_amd.autotuner.tuner import (
     TUNED_PATH, AutotuneCache, is_int8, precompile, problem_candidates, problem_key, tune_problem,
 )
-from mdlc_amd.codegen.schedule import default_qschedule, default_schedule
+from mdlc_amd.codegen.schedule import default_qdw_schedule, default_qschedule, default_schedule
 
 
 class _Recorder:
@@ -93,7 +93,10 @@ def main(argv=None) -> int:
     for p in probs:
         t0 = time.time()
         res = tune_problem(p, budget=args.budget, ctx=ctx)
-        d = (default_qschedule if is_int8(p) else default_schedule)(p["M"], p["N"], p["K"]).key_full()
+        if p["kind"] == "qdw":
+            d = default_qdw_schedule(p["M"]).key_full()
+        else:
+            d = (default_qschedule if is_int8(p) else default_schedule)(p["M"], p["N"], p["K"]).key_full()
         dflt = next((m for k, m in res.ranking if k == d), float("nan"))
         cache.put_key(res.key, res.best, res.best_metric, True)
         cache.save()

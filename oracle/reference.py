@@ -180,7 +180,13 @@ class ReferenceExecutor:
                                  pads=a.get("pads"), dilations=a.get("dilations", [1, 1]),
                                  group=a.get("group", 1))
             lo = 0 if a.get("activation") == "Relu" else quant.QMIN
-            return [quant.requant(acc, ins[3].reshape(1, -1, 1, 1), lo)]
+            q = quant.requant(acc, ins[3].reshape(1, -1, 1, 1), lo)
+            # fused epilogues: the composition of the unfused QLut / QAdd
+            if a.get("epilogue") == "lut":
+                return [quant.lut(q, ins[4])]
+            if a.get("epilogue") == "add":
+                return [quant.qadd(ins[4], q, a["res_mult"], a["acc_mult"])]
+            return [q]
         if op == "QGemm":
             acc = quant.gemm_acc(ins[0], ins[1], opt(2))
             if a.get("out_dtype", "int8") == "float32":

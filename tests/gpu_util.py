@@ -11,10 +11,11 @@ from mdlc_amd.testing import DEVICE_TENSOR, compare_arrays, tolerance_ratio
 from oracle.reference import run_reference
 
 
-def device_run(graph, feeds, *, schedule_fn=None, conv_mode="implicit", ctx=None, all_tensors=False):
+def device_run(graph, feeds, *, schedule_fn=None, conv_mode="implicit", ctx=None, all_tensors=False,
+               **compile_kw):
     """Compile ``graph`` (fused by the default pipeline) and run it on the
     device. Returns (compiled, device values, oracle values)."""
-    c = compile_graph(graph, feeds=feeds, schedule_fn=schedule_fn, conv_mode=conv_mode)
+    c = compile_graph(graph, feeds=feeds, schedule_fn=schedule_fn, conv_mode=conv_mode, **compile_kw)
     ex = HipExecutor(c.module, ctx)
     try:
         got = ex.run_all(feeds) if all_tensors else ex.run(feeds)["outputs"]

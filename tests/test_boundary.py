@@ -133,10 +133,15 @@ def test_unsupported_op_raises_instead_of_host_fallback():
 def test_repvit_int8_module_compiles_and_is_channels_last():
     from mdlc_amd.tools.build_repvit_int8 import build_repvit_int8, make_input
 
-    c = compile_graph(build_repvit_int8(batch=2), feeds={"input": make_input(2)})
-    kinds = {l.kind for l in c.module.plan}
-    assert kinds >= {"quantize", "qgemm", "qdwconv", "qadd", "qlut", "qgap"}
-    assert c.module.fallbacks() == []
-    assert all(c.module.device_layout.get(l.outputs[0]) == "NHWC"
-               for l in c.module.plan if l.kind in ("qdwconv", "qlut", "qadd"))
-    R.compile_code_object(c.module.sources())
+    for fused, dw in ((True, "mfma"), (False, "vector")):
+        c = compile_graph(build_repvit_int8(batch=2), feeds={"input": make_input(2)},
+                          fuse_int8_epilogues=fused, int8_depthwise=dw)
+        kinds = {l.kind for l in c.module.plan}
+        assert kinds >= {"quantize", "qgemm", "qgap"}
+        assert ("qlut" in kinds and "qadd" in kinds) != fused
+        assert ("qdwconv" in kinds) == (dw == "vector")
+        assert c.module.fallbacks() == []
+        assert all(c.module.device_layout.get(l.outputs[0]) == "NHWC"
+                   for l in c.module.plan if l.kind in ("qdwconv", "qlut", "qadd", "qgemm")
+                   and l.meta.get("OH"))
+        R.compile_code_object(c.module.sources())

@@ -67,6 +67,21 @@ def test_qconv_bit_exact(case, relu, hip_ctx):
     assert v.std() > 3 and np.mean(np.abs(v) == 127) < 0.5        # non-degenerate
 
 
+@pytest.mark.parametrize("impl", ["mfma", "vector"])
+@pytest.mark.parametrize("case", [(2, 48, 14, 14, 3, 1), (2, 48, 15, 15, 3, 2), (1, 64, 9, 9, 5, 1),
+                                  (3, 32, 8, 8, 3, 2), (1, 384, 7, 7, 3, 1)],
+                         ids=lambda c: "x".join(map(str, c)))
+def test_qdepthwise_matrix_core_and_vector_paths(case, impl, hip_ctx):
+    """Depthwise int8 convs (C % 16 == 0) as block-diagonal MFMA GEMMs and on
+    the vector kernel: both bit-exact (5x5 window: 25 taps, K padded to 448)."""
+    n, c, h, w, k, s = case
+    g, feeds = _qconv_graph(n, c, h, w, c, k, s, group=c, relu=True, seed=7)
+    cmod, got, want = device_run(g, feeds, ctx=hip_ctx, int8_depthwise=impl)
+    kinds = [l.kind for l in cmod.module.plan]
+    assert ("qdwconv" in kinds) == (impl == "vector")
+    np.testing.assert_array_equal(got["y"], want["y"])
+
+
 class _Fixed:
     """A schedule source that returns one schedule for every problem."""
 
@@ -145,20 +160,76 @@ def test_qadd_qlut_qgap(hip_ctx):
     assert np.mean(np.abs(got["s"].astype(int)) == 127) > 0.01          # clamp path exercised
 
 
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
 @pytest.mark.parametrize("batch", [2, 32])
-def test_repvit_int8_every_tensor_bit_exact(batch, hip_ctx):
+def test_repvit_int8_every_tensor_bit_exact(batch, fused, hip_ctx):
+    """Every int8 tensor the module materializes, and the logits, equal the
+    oracle's — with the GELU lookups and residual adds folded into the conv
+    epilogues and the depthwise convs on the matrix cores, and with neither
+    (separate lookup/add launches, vector depthwise kernel)."""
     g = build_repvit_int8(batch=batch)
     feeds = {"input": make_input(batch)}
-    c, got, want = device_run(g, feeds, ctx=hip_ctx, all_tensors=True)
+    c, got, want = device_run(g, feeds, ctx=hip_ctx, all_tensors=True, fuse_int8_epilogues=fused,
+                              int8_depthwise="mfma" if fused else "vector")
     assert c.module.fallbacks() == []
+    epis = [l.meta.get("epilogue", 0) for l in c.module.plan if l.kind == "qgemm"]
+    assert (epis.count(1), epis.count(2)) == ((24, 23) if fused else (0, 0))
     n = 0
     for name, v in got.items():
         w = want[name]
         if w.dtype == np.int8:
             np.testing.assert_array_equal(v, w, err_msg=name)
             n += 1
-    assert n >= 120
+    assert n >= (70 if fused else 120)
     np.testing.assert_array_equal(got["logits"], want["logits"])
+
+
+def _qconv_epilogue_graph(n, c, hw, oc, k, epilogue, *, res_first, seed=5):
+    """QConv (3x3 gather or 1x1 dense) followed by a QLut or by a QAdd with a
+    second int8 tensor of the conv output's shape."""
+    rng = np.random.default_rng(seed)
+    b = GraphBuilder("qe")
+    b.input("x", (n, c, hw, hw))
+    b.input("r", (n, oc, hw, hw))
+    b.node("QuantizeLinear", ["x"], "xq", inv_scale=20.0)
+    b.node("QuantizeLinear", ["r"], "rq", inv_scale=25.0)
+    b.const("w", rng.integers(-127, 128, (oc, c, k, k)).astype(np.int8))
+    b.const("b", rng.integers(-3000, 3000, oc).astype(np.int32))
+    b.const("m", rng.uniform(0.0005, 0.004, oc).astype(np.float32))
+    p = (k - 1) // 2
+    b.node("QConv", ["xq", "w", "b", "m"], "y", kernel_shape=[k, k], strides=[1, 1], pads=[p] * 4)
+    if epilogue == "lut":
+        b.const("t", rng.integers(-127, 128, 256).astype(np.int8))
+        b.node("QLut", ["y", "t"], "z")
+    else:
+        ins = ["rq", "y"] if res_first else ["y", "rq"]
+        b.node("QAdd", ins, "z", ma=0.7, mb=0.45)
+    b.output("z")
+    feeds = {"x": (rng.standard_normal((n, c, hw, hw)) * 3).astype(np.float32),
+             "r": (rng.standard_normal((n, oc, hw, hw)) * 3).astype(np.float32)}
+    return b.graph(), feeds
+
+
+@pytest.mark.parametrize("sched", [None] + QSCHEDULES[:1] + QSCHEDULES[2:],
+                         ids=lambda s: "default" if s is None else s.key())
+@pytest.mark.parametrize("case", [("lut", 1, False), ("lut", 3, False), ("add", 1, False),
+                                  ("add", 1, True), ("add", 3, True)],
+                         ids=lambda c: f"{c[0]}_k{c[1]}{'_resfirst' if c[2] else ''}")
+@pytest.mark.parametrize("oc", [48, 30])
+def test_qconv_fused_epilogues(case, oc, sched, hip_ctx):
+    """The fused lookup and residual add equal the unfused ops bit for bit,
+    for either QAdd operand order, an output width that is not a multiple of
+    four (byte stores) and several tiles."""
+    epilogue, k, res_first = case
+    g, feeds = _qconv_epilogue_graph(2, 32, 9, oc, k, epilogue, res_first=res_first)
+    fn = None if sched is None else _Fixed(sched)
+    cmod, got, want = device_run(g, feeds, ctx=hip_ctx, schedule_fn=fn)
+    assert [n.op_type for n in cmod.graph.nodes].count("QConv") == 1
+    assert len(cmod.graph.nodes) == (2 if epilogue == "lut" else 3)    # quantize(s) + fused conv
+    np.testing.assert_array_equal(got["z"], want["z"])
+    g2, _ = _qconv_epilogue_graph(2, 32, 9, oc, k, epilogue, res_first=res_first)
+    _, got2, _ = device_run(g2, feeds, ctx=hip_ctx, schedule_fn=fn, fuse_int8_epilogues=False)
+    np.testing.assert_array_equal(got["z"], got2["z"])
 
 
 def test_int8_gemm_4096_cube_rows_exact(hip_ctx):

@@ -1,0 +1,104 @@
+"""The int8 epilogue fusion pass (CPU): what it folds, what it must leave
+alone, and that the fused graph computes exactly what the unfused one does
+(the oracle evaluates both)."""
+
+from __future__ import annotations
+
+import numpy as np
+
+from mdlc_amd.compiler import compile_graph
+from mdlc_amd.ir import verify_graph
+from mdlc_amd.passes.fuse_quant_epilogue import FuseQuantEpilogue
+from mdlc_amd.tools.build_repvit_int8 import build_repvit_int8, make_input
+from mdlc_amd.tools.graph_builder import GraphBuilder
+from oracle.reference import run_reference
+
+
+def _small_repvit():
+    return build_repvit_int8(batch=1, widths=(16, 32, 48, 64), depths=(1, 2, 2, 1), image=64)
+
+
+def test_repvit_lookups_and_adds_fold_into_convs():
+    g = build_repvit_int8(batch=1)
+    ops = [n.op_type for n in g.nodes]
+    n_lut, n_add = ops.count("QLut"), ops.count("QAdd")
+    assert (n_lut, n_add) == (24, 23)
+    c = compile_graph(g, feeds={"input": make_input(1)})
+    hist = c.graph.op_histogram()
+    assert "QLut" not in hist and "QAdd" not in hist
+    epis = [n.attrs.get("epilogue") for n in c.graph.nodes if n.op_type == "QConv"]
+    assert epis.count("lut") == n_lut and epis.count("add") == n_add
+    verify_graph(c.graph)
+
+
+def test_fused_graph_equals_unfused_everywhere():
+    feeds = {"input": make_input(1, image=64)}
+    cf = compile_graph(_small_repvit(), feeds=feeds)
+    cu = compile_graph(_small_repvit(), feeds=feeds, fuse_int8_epilogues=False)
+    assert len(cf.graph.nodes) < len(cu.graph.nodes)
+    a = run_reference(cf.graph, feeds, return_all=True)
+    b = run_reference(cu.graph, feeds, return_all=True)
+    common = [k for k in a if k in b]
+    assert len(common) > 50
+    for k in common:
+        np.testing.assert_array_equal(a[k], b[k], err_msg=k)
+    assert np.abs(a["logits"]).max() > 0
+
+
+def _conv_then(op, *, extra_use=False, as_output=False, dependent_residual=False):
+    """Quantize -> 1x1 QConv -> QLut or QAdd(xq, y), with optional extra
+    uses of the conv output y."""
+    rng = np.random.default_rng(0)
+    b = GraphBuilder("q")
+    b.input("x", (1, 16, 6, 6))
+    b.node("QuantizeLinear", ["x"], "xq", inv_scale=10.0)
+    b.const("w", rng.integers(-127, 128, (16, 16, 1, 1)).astype(np.int8))
+    b.const("b", np.zeros(16, np.int32))
+    b.const("m", np.full(16, 0.01, np.float32))
+    b.const("t", np.arange(-128, 128).clip(-127, 127).astype(np.int8))
+    b.node("QConv", ["xq", "w", "b", "m"], "y", kernel_shape=[1, 1], strides=[1, 1], pads=[0] * 4)
+    if op == "lut":
+        b.node("QLut", ["y", "t"], "z")
+    else:
+        r = "xq"
+        if dependent_residual:
+            b.node("QLut", ["y", "t"], "ly")
+            r = "ly"
+        b.node("QAdd", [r, "y"], "z", ma=0.25, mb=0.75)
+    b.output("z")
+    if extra_use:
+        b.node("QLut", ["y", "t"], "z2")
+        b.output("z2")
+    if as_output:
+        b.output("y")
+    return b.graph()
+
+
+def _fused(g):
+    p = FuseQuantEpilogue()
+    changed = p.run(g)
+    return changed, [n.attrs.get("epilogue") for n in g.nodes if n.op_type == "QConv"]
+
+
+def test_pass_folds_single_consumer_patterns():
+    assert _fused(_conv_then("lut")) == (True, ["lut"])
+    changed, epis = _fused(_conv_then("add"))
+    assert changed and epis == ["add"]
+
+
+def test_pass_leaves_shared_or_visible_or_cyclic_outputs_alone():
+    assert _fused(_conv_then("lut", extra_use=True)) == (False, [None])
+    assert _fused(_conv_then("lut", as_output=True)) == (False, [None])
+    assert _fused(_conv_then("add", as_output=True)) == (False, [None])
+    # the residual is computed from the conv output itself: folding would cycle
+    # (y also has two consumers here, which alone forbids the fold)
+    changed, epis = _fused(_conv_then("add", dependent_residual=True))
+    assert not changed and epis == [None]
+
+
+def test_add_multipliers_follow_operand_order():
+    g = _conv_then("add")
+    FuseQuantEpilogue().run(g)
+    (conv,) = [n for n in g.nodes if n.op_type == "QConv"]
+    assert conv.inputs[4] == "xq"
+    assert conv.attrs["res_mult"] == 0.25 and conv.attrs["acc_mult"] == 0.75
