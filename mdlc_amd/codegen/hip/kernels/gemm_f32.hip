@@ -312,14 +312,21 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
 
   const int nk = (kend - kbeg + BK - 1) / BK;
   if (DB) {
+    // The next tile's loads and LDS stores are unconditional: past kend
+    // every load is masked to zero and the stores go to the idle buffer,
+    // which nobody reads again. The loop body is then one basic block the
+    // scheduler can interleave with the MFMAs; the waves raise their issue
+    // priority while they feed the matrix cores.
     load_tiles(kbeg);
     store_tiles(0);
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
       const int cur = kt & 1;
-      if (kt + 1 < nk) load_tiles(kbeg + (kt + 1) * BK);
+      load_tiles(kbeg + (kt + 1) * BK);
+      __builtin_amdgcn_s_setprio(1);
       compute(cur);
-      if (kt + 1 < nk) store_tiles(cur ^ 1);
+      __builtin_amdgcn_s_setprio(0);
+      store_tiles(cur ^ 1);
       __syncthreads();
     }
   } else {
