@@ -128,12 +128,27 @@ def test_conv_matches_oracle(case, mode, hip_ctx):
 @pytest.mark.parametrize("case", [CONV_CASES[2], CONV_CASES[4], CONV_CASES[6]],
                          ids=lambda c: "x".join(map(str, c)))
 def test_conv_split_k(case, sk, mode, hip_ctx):
+    """Split-K (partial slices + ordered reduce launch): correct on the first
+    run and on repeated runs of one executor, with a different input in
+    between (the workspace is fully rewritten every run)."""
+    from mdlc_amd.codegen.hip.hip_executor import HipExecutor
+    from mdlc_amd.compiler import compile_graph
+    from oracle.reference import run_reference
+
     sched = MfmaSchedule(64, 64, 16, 2, 2, 32, True, sk)
     g, feeds = _conv_graph(*case)
-    c, got, want = device_run(g, feeds, conv_mode=mode, ctx=hip_ctx,
-                              schedule_fn=lambda n, mnk: sched)
-    assert any(l.kind == "splitk_reduce" for l in c.module.plan)
-    assert_close("y", got["y"], want["y"])
+    c = compile_graph(g, feeds=feeds, conv_mode=mode, schedule_fn=lambda n, mnk: sched)
+    (launch,) = [l for l in c.module.plan if l.kind in ("conv", "gemm")]
+    assert launch.meta["ksplit"] > 1 and launch.grid[0] % launch.meta["ksplit"] == 0
+    assert [l.kind for l in c.module.plan][-1] == "splitk_reduce"
+    feeds2 = {"x": (feeds["x"][::-1] * 0.5).copy()}
+    ex = HipExecutor(c.module, hip_ctx)
+    try:
+        for f in (feeds, feeds2, feeds):
+            got = ex.run(f)["outputs"]
+            assert_close("y", got["y"], run_reference(c.graph, f)["y"])
+    finally:
+        ex.close()
 
 
 # Implicit-GEMM schedules covering every gather/staging shape: threads per
