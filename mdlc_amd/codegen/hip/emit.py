@@ -198,7 +198,9 @@ class HipCodegen(Int8LoweringMixin):
                 "bytes": 4 * (N * geo["C"] * geo["H"] * geo["W"] + OC * K + P * OC
                               + (OC if has_bias else 0))}
         epi = dict(bias_mode="row", act=act, attrs=self._act_attrs(a), act_sig=self._act_sig(a),
-                   alpha=1.0, beta=1.0, ldc=0, hw=OH * OW)
+                   alpha=1.0, beta=1.0, ldc=0, hw=OH * OW, **self._residual_epilogue(g, node))
+        if epi["res_input"]:
+            meta["bytes"] += 4 * P * OC
         if self.conv_mode == "implicit":
             win = (geo["KH"], geo["KW"], geo["SH"], geo["SW"], geo["DH"], geo["DW"], geo["PT"], geo["PL"])
             meta.update({"Cin": geo["C"], "H": geo["H"], "W": geo["W"], "OH": OH, "OW": OW,
@@ -223,6 +225,21 @@ class HipCodegen(Int8LoweringMixin):
         self._emit_gemm("gemm", sched, [wdev, cols], bias, y, meta, epi, bmode=0, vec_a=True,
                         out_nchw=True)
 
+    def _residual_epilogue(self, g: Graph, node: Node) -> dict:
+        """``residual`` (the epilogue's post() body) and ``res_input`` for a
+        conv carrying a folded residual group, else both None."""
+        sub = node.attrs.get("residual_subgraph")
+        if not sub:
+            return {"residual": None, "res_input": None}
+        r = node.inputs[3]
+        y = node.attrs["residual_from"]
+        consts = {}
+        for n in sub:
+            for e in n.real_inputs():
+                if e not in (y, r) and g.is_constant(e):
+                    consts[e] = float(np.asarray(g.initializers[e], np.float32).reshape(()))
+        return {"residual": T.residual_post_body(sub, y, r, consts), "res_input": r}
+
     def _emit_gemm(self, kind: str, sched: MfmaSchedule, operands: list, bias: list, out: str,
                    meta: dict, epi: dict, *, bmode: int, vec_a: bool, out_nchw: bool,
                    win: Optional[tuple] = None) -> None:
@@ -233,17 +250,21 @@ class HipCodegen(Int8LoweringMixin):
         block = (sched.threads_per_block(), 1, 1)
         act = epi["act"]
         tag = "conv" if kind == "conv" else "gemm"
+        residual, res = epi.get("residual"), epi.get("res_input")
+        extra = [res] if res else []
+        rtag = "_res" if residual else ""
         sig = (kind, sched, bool(bias), epi["bias_mode"], epi["act_sig"], bmode, out_nchw, vec_a,
-               epi["alpha"], epi["beta"], win)
+               epi["alpha"], epi["beta"], win, residual)
         meta = dict(meta, ksplit=slices, kchunk=chunk, ldc=epi["ldc"], hw=epi["hw"])
         meta.setdefault("ldb", 0)
         if slices == 1:
             kname = self._kernel(sig, lambda i: T.gemm_kernel(
-                f"{tag}_{sched.key()}_{act or 'none'}_{epi['bias_mode']}_{i}", sched,
+                f"{tag}_{sched.key()}_{act or 'none'}_{epi['bias_mode']}{rtag}_{i}", sched,
                 with_bias=bool(bias), bias_mode=epi["bias_mode"], activation=act,
                 attrs=epi["attrs"], alpha=epi["alpha"], beta=epi["beta"], bmode=bmode,
-                out_nchw=out_nchw, vec_a=vec_a, win=win))
-            self.plan.append(Launch(kind, kname, operands + bias, [out], (tiles, 1, 1), block, meta))
+                out_nchw=out_nchw, vec_a=vec_a, win=win, residual=residual))
+            self.plan.append(Launch(kind, kname, operands + bias + extra, [out], (tiles, 1, 1), block,
+                                    meta))
             return
         ws = out + "__splitk"
         self.scratch[ws] = (slices * M, N)
@@ -254,15 +275,17 @@ class HipCodegen(Int8LoweringMixin):
             win=win))
         self.plan.append(Launch(kind, kname, list(operands), [ws], (tiles * slices, 1, 1), block,
                                 dict(meta, partial=True)))
-        rsig = ("splitk_reduce", bool(bias), epi["bias_mode"], epi["act_sig"], epi["alpha"], epi["beta"])
+        rsig = ("splitk_reduce", bool(bias), epi["bias_mode"], epi["act_sig"], epi["alpha"], epi["beta"],
+                residual)
         rname = self._kernel(rsig, lambda i: T.splitk_reduce_kernel(
-            f"splitk_reduce_{act or 'none'}_{epi['bias_mode']}_{i}", with_bias=bool(bias),
+            f"splitk_reduce_{act or 'none'}_{epi['bias_mode']}{rtag}_{i}", with_bias=bool(bias),
             bias_mode=epi["bias_mode"], activation=act, attrs=epi["attrs"], alpha=epi["alpha"],
-            beta=epi["beta"]))
+            beta=epi["beta"], residual=residual))
         self.plan.append(Launch(
-            "splitk_reduce", rname, [ws] + bias, [out], (-(-(M * N) // 256), 1, 1), (256, 1, 1),
+            "splitk_reduce", rname, [ws] + bias + extra, [out], (-(-(M * N) // 256), 1, 1),
+            (256, 1, 1),
             {"S": slices, "M": M, "N": N, "ldc": epi["ldc"], "hw": epi["hw"],
-             "node": meta["node"], "bytes": 4 * (slices + 1) * M * N}))
+             "node": meta["node"], "bytes": 4 * (slices + 1 + len(extra)) * M * N}))
 
     def _lower_dwconv(self, g: Graph, node: Node, geo: dict, has_bias: bool) -> None:
         if geo["ICG"] != 1 or geo["OC"] % geo["C"] != 0:

@@ -65,6 +65,7 @@ struct GemmArgs {
   const float* __restrict__ A;
   const float* __restrict__ B;   // dense B, or the NCHW conv input
   const float* __restrict__ bias;
+  const float* __restrict__ R;   // folded residual, same layout as C (Epi::residual)
   float* __restrict__ C;
   int M, N, K, lda, ldb, ldc, hw;
   int Cin, H, W, OH, OW;         // conv input / output geometry (BMODE >= 2)
@@ -369,7 +370,10 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
             g.C[cofs + (size_t)row * rstride] = acc[mi][ni][r];
           } else {
             const float bv = (Epi::bias == 1) ? g.bias[row] : bcol;
-            g.C[cofs + (size_t)row * rstride] = Epi::apply(acc[mi][ni][r], bv);
+            const size_t o = cofs + (size_t)row * rstride;
+            float v = Epi::apply(acc[mi][ni][r], bv);
+            if (Epi::residual) v = Epi::post(v, g.R[o]);
+            g.C[o] = v;
           }
         }
       }
@@ -377,11 +381,13 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
 }
 
 // Split-K epilogue: out = epi(sum_s ws[s][row][col], bias) with the slices
-// added in slice order, written row-major (ldc) or NCHW (hw > 0). One thread
+// added in slice order (then a folded residual group, if any), written
+// row-major (ldc) or NCHW (hw > 0). One thread
 // per output element, consecutive threads on consecutive columns.
 template <class Epi>
 __device__ __forceinline__ void splitk_reduce_f32(const float* __restrict__ ws,
                                                   const float* __restrict__ bias,
+                                                  const float* __restrict__ res,
                                                   float* __restrict__ C, int S, int M, int N,
                                                   int ldc, int hw) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -392,13 +398,15 @@ __device__ __forceinline__ void splitk_reduce_f32(const float* __restrict__ ws,
   for (int s = 1; s < S; ++s) v = v + ws[(size_t)s * M * N + i];
   const float b = Epi::bias == 1 ? bias[row] : (Epi::bias == 2 ? bias[col] : 0.f);
   v = Epi::apply(v, b);
+  size_t o;
   if (hw > 0) {
     const int n = col / hw;
-    const int sidx = col - n * hw;
-    C[((size_t)n * M + row) * hw + sidx] = v;
+    o = ((size_t)n * M + row) * hw + (col - n * hw);
   } else {
-    C[(size_t)row * ldc + col] = v;
+    o = (size_t)row * ldc + col;
   }
+  if (Epi::residual) v = Epi::post(v, res[o]);
+  C[o] = v;
 }
 
 }  // namespace mdlc

@@ -76,9 +76,13 @@ BIAS_CODE = {None: 0, "none": 0, "row": 1, "col": 2}
 
 
 def epilogue_struct(name: str, *, bias_mode: Optional[str], activation: Optional[str],
-                    attrs: dict, alpha: float = 1.0, beta: float = 1.0) -> str:
-    """``struct name { bias; apply(acc, b) }``: alpha*acc (+ beta*b), then the
-    activation — the order of mdlc/runtime/ops.py:84-92 followed by the act."""
+                    attrs: dict, alpha: float = 1.0, beta: float = 1.0,
+                    residual: Optional[str] = None) -> str:
+    """``struct name { bias; residual; apply(acc, b); post(v, r) }``:
+    alpha*acc (+ beta*b), then the activation — the order of
+    mdlc/runtime/ops.py:84-92 followed by the act — and, for a folded
+    residual group, ``post`` (the group's code on the conv value and the
+    residual element; see ``residual_post_body``)."""
     code = BIAS_CODE[bias_mode]
     lines = ["float v = acc;"]
     if float(alpha) != 1.0:
@@ -87,8 +91,30 @@ def epilogue_struct(name: str, *, bias_mode: Optional[str], activation: Optional
         lines.append("v = v + b;" if float(beta) == 1.0 else f"v = v + {flit(beta)} * b;")
     lines.append(f"return {activation_expr(activation, 'v', attrs)};")
     body = " ".join(lines)
+    post = residual or "return v;"
     return (f"struct {name} {{\n  static constexpr int bias = {code};\n"
-            f"  __device__ __forceinline__ static float apply(float acc, float b) {{ {body} }}\n}};\n")
+            f"  static constexpr bool residual = {'true' if residual else 'false'};\n"
+            f"  __device__ __forceinline__ static float apply(float acc, float b) {{ {body} }}\n"
+            f"  __device__ __forceinline__ static float post(float v, float r) {{ {post} }}\n}};\n")
+
+
+def residual_post_body(sub: list, y: str, r: str, consts: dict) -> str:
+    """The body of ``post(v, r)`` for a folded residual group: ``sub`` is the
+    group's members (an Add of the conv output ``y`` and the residual ``r``,
+    then single-input pointwise ops), evaluated one float32 operation per
+    member exactly as the elementwise kernel would, with ``y`` read as ``v``
+    and ``r`` as ``r``."""
+    names = {y: "v", r: "r"}
+    lines = []
+
+    def ref(e: str) -> str:
+        return flit(consts[e]) if e in consts else _cname(e, names)
+
+    for n in sub:
+        out = _cname(n.outputs[0], names)
+        lines.append(f"float {out} = {_member_expr(n, ref, consts)};")
+    lines.append(f"return {names[sub[-1].outputs[0]]};")
+    return " ".join(lines)
 
 
 # ----- GEMM / conv ----------------------------------------------------------
@@ -96,31 +122,36 @@ def epilogue_struct(name: str, *, bias_mode: Optional[str], activation: Optional
 def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: str = "col",
                 activation: Optional[str] = None, attrs: Optional[dict] = None,
                 alpha: float = 1.0, beta: float = 1.0, bmode: int = 0, out_nchw: bool = False,
-                vec_a: bool = True, win: Optional[tuple] = None) -> tuple:
+                vec_a: bool = True, win: Optional[tuple] = None,
+                residual: Optional[str] = None) -> tuple:
     """(name, source) of one GEMM instantiation.
 
     Kernel ABI (the reference's gemm ABI plus trailing layout arguments):
-      dense  (bmode 0/1): (A, B, [bias], C, int M, int N, int K, int lda, int ldb, int ldc,
-                           int hw, int ksplit, int kchunk)
-      conv   (bmode 2/3): (W, x, [bias], y, int M, int N, int K, int lda,
+      dense  (bmode 0/1): (A, B, [bias], [res], C, int M, int N, int K, int lda, int ldb,
+                           int ldc, int hw, int ksplit, int kchunk)
+      conv   (bmode 2/3): (W, x, [bias], [res], y, int M, int N, int K, int lda,
                            int Cin, int H, int W, int OH, int OW, int ksplit, int kchunk)
-    ``hw`` > 0 selects the NCHW output scatter for conv-as-GEMM. With
-    ``sched.SK > 1`` the kernel writes raw partial sums of each K slice to
-    its C argument (the split-K workspace) and takes no bias argument; the
-    epilogue then lives in ``splitk_reduce_kernel``.
+    ``hw`` > 0 selects the NCHW output scatter for conv-as-GEMM; ``res`` is a
+    folded residual read at each output's own position (``residual`` is the
+    body of the epilogue's ``post``). With ``sched.SK > 1`` the kernel writes
+    raw partial sums of each K slice to its C argument (the split-K
+    workspace) and takes no bias or residual; the epilogue then lives in
+    ``splitk_reduce_kernel``.
     """
     attrs = attrs or {}
     s = sched
     split = s.SK > 1
     if split:
         with_bias = False
+        residual = None
     epi = f"{name}_epi"
     src = [epilogue_struct(epi, bias_mode=bias_mode if with_bias else None,
                            activation=None if split else activation, attrs=attrs,
-                           alpha=1.0 if split else alpha, beta=beta)]
+                           alpha=1.0 if split else alpha, beta=beta, residual=residual)]
     winty = "mdlc::NoWin" if win is None else "mdlc::ConvWin<%d, %d, %d, %d, %d, %d, %d, %d>" % tuple(win)
-    bias_arg = "const float* __restrict__ bias, " if with_bias else ""
-    bias_val = "bias" if with_bias else "nullptr"
+    bias_arg = ("const float* __restrict__ bias, " if with_bias else "") + \
+        ("const float* __restrict__ res, " if residual else "")
+    bias_val = ("bias" if with_bias else "nullptr") + (", res" if residual else ", nullptr")
     out = 2 if split else (1 if out_nchw else 0)
     tmpl = (f"mdlc::gemm_f32_mfma<{s.BM}, {s.BN}, {s.BK}, {s.WGM}, {s.WGN}, {s.MS}, "
             f"{'true' if s.DB else 'false'}, {'true' if vec_a else 'false'}, {bmode}, "
@@ -149,18 +180,19 @@ def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: s
 
 def splitk_reduce_kernel(name: str, *, with_bias: bool, bias_mode: str,
                          activation: Optional[str], attrs: dict, alpha: float = 1.0,
-                         beta: float = 1.0) -> tuple:
-    """Split-K epilogue. ABI: (ws, [bias], C, int S, int M, int N, int ldc, int hw)."""
+                         beta: float = 1.0, residual: Optional[str] = None) -> tuple:
+    """Split-K epilogue. ABI: (ws, [bias], [res], C, int S, int M, int N, int ldc, int hw)."""
     epi = f"{name}_epi"
     src = epilogue_struct(epi, bias_mode=bias_mode if with_bias else None, activation=activation,
-                          attrs=attrs, alpha=alpha, beta=beta)
+                          attrs=attrs, alpha=alpha, beta=beta, residual=residual)
     bias_arg = "const float* __restrict__ bias, " if with_bias else ""
+    res_arg = "const float* __restrict__ res, " if residual else ""
     return name, src + (
         f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
-        f"    const float* __restrict__ ws, {bias_arg}float* __restrict__ C, int S, int M, int N,\n"
-        "    int ldc, int hw) {\n"
-        f"  mdlc::splitk_reduce_f32<{epi}>(ws, {'bias' if with_bias else 'nullptr'}, C, S, M, N, "
-        "ldc, hw);\n}\n")
+        f"    const float* __restrict__ ws, {bias_arg}{res_arg}float* __restrict__ C, int S, int M,\n"
+        "    int N, int ldc, int hw) {\n"
+        f"  mdlc::splitk_reduce_f32<{epi}>(ws, {'bias' if with_bias else 'nullptr'}, "
+        f"{'res' if residual else 'nullptr'}, C, S, M, N, ldc, hw);\n}}\n")
 
 
 def im2col_kernel(name: str = "im2col") -> tuple:
@@ -219,8 +251,21 @@ _BINARY = {"Add": "+", "Sub": "-", "Mul": "*", "Div": "/"}
 
 def _cname(edge: str, table: dict) -> str:
     if edge not in table:
-        table[edge] = f"v{len(table)}"
+        table[edge] = f"t{len(table)}"
     return table[edge]
+
+
+def _member_expr(n: Node, ref, consts: dict) -> str:
+    """One pointwise group member as a float expression of its inputs."""
+    if n.op_type in _BINARY:
+        return f"{ref(n.inputs[0])} {_BINARY[n.op_type]} {ref(n.inputs[1])}"
+    if n.op_type == "Clip":
+        attrs = dict(n.attrs)
+        lo = consts.get(n.inputs[1]) if len(n.inputs) > 1 and n.inputs[1] else n.attrs.get("min")
+        hi = consts.get(n.inputs[2]) if len(n.inputs) > 2 and n.inputs[2] else n.attrs.get("max")
+        attrs["clip_min"], attrs["clip_max"] = lo, hi
+        return activation_expr("Clip", ref(n.inputs[0]), attrs)
+    return activation_expr(n.op_type, ref(n.inputs[0]), n.attrs)
 
 
 def elementwise_kernel(name: str, node: Node, *, scalar_consts: Optional[dict] = None) -> tuple:
@@ -250,16 +295,7 @@ def elementwise_kernel(name: str, node: Node, *, scalar_consts: Optional[dict] =
     body = []
     for n in sub:
         out = _cname(n.outputs[0], names)
-        if n.op_type in _BINARY:
-            body.append(f"float {out} = {ref(n.inputs[0])} {_BINARY[n.op_type]} {ref(n.inputs[1])};")
-        elif n.op_type == "Clip":
-            attrs = dict(n.attrs)
-            lo = consts.get(n.inputs[1]) if len(n.inputs) > 1 and n.inputs[1] else n.attrs.get("min")
-            hi = consts.get(n.inputs[2]) if len(n.inputs) > 2 and n.inputs[2] else n.attrs.get("max")
-            attrs["clip_min"], attrs["clip_max"] = lo, hi
-            body.append(f"float {out} = {activation_expr('Clip', ref(n.inputs[0]), attrs)};")
-        else:
-            body.append(f"float {out} = {activation_expr(n.op_type, ref(n.inputs[0]), n.attrs)};")
+        body.append(f"float {out} = {_member_expr(n, ref, consts)};")
     in_vars = [_cname(e, names) for e in ext]
     out_vars = [_cname(o, names) for o in node.outputs]
     params = [f"const float* __restrict__ p_{v}" for v in in_vars] + \

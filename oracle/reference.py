@@ -86,6 +86,17 @@ class ReferenceExecutor:
         ins = [env[e] if e else None for e in node.inputs]
         opt = lambda i: ins[i] if len(ins) > i else None  # noqa: E731
 
+        if op in ("Conv", "FusedConvAct", "FusedConvBNAct") and a.get("residual_subgraph"):
+            # backend residual fusion: the folded FusedElementwise group runs on
+            # the conv's output exactly as it did unfused
+            local = dict(env)
+            local[a["residual_from"]] = act(a.get("activation"),
+                                            ops.conv(ins[0], ins[1], opt(2), **_conv_kw(a)), a)
+            for sn in a["residual_subgraph"]:
+                for name, val in zip(sn.outputs, self.exec_node(sn, local)):
+                    if name:
+                        local[name] = val
+            return [local[node.outputs[0]]]
         if op in ("FusedConvAct", "FusedConvBNAct"):
             return [act(a.get("activation"), ops.conv(ins[0], ins[1], opt(2), **_conv_kw(a)), a)]
         if op == "FusedGemmAct":

@@ -77,9 +77,11 @@ def test_resnet18_module_compiles_for_gfx950(mode, batch):
 
 
 def test_mobilenetv2_and_micro_modules_compile():
-    c = compile_graph(build_mobilenetv2(batch=1, calibrate=False))
-    assert {l.kind for l in c.module.plan} >= {"conv", "dwconv", "elementwise", "gap"}
-    R.compile_code_object(c.module.sources())
+    for fold in (True, False):
+        c = compile_graph(build_mobilenetv2(batch=1, calibrate=False), fuse_residual=fold)
+        kinds = {l.kind for l in c.module.plan}
+        assert kinds >= {"conv", "dwconv", "gap"} and ("elementwise" in kinds) != fold
+        R.compile_code_object(c.module.sources())
     for M, N, K in SHAPES:
         g, feeds = build_micro_gemm(M, N, K)
         R.compile_code_object(compile_graph(g, feeds=feeds).module.sources())

@@ -177,6 +177,52 @@ def test_conv_gather_schedules(case, sched, hip_ctx):
     assert_close("y", got["y"], want["y"])
 
 
+def _conv_residual_graph(post, res_first, seed=9):
+    rng = np.random.default_rng(seed)
+    b = GraphBuilder("cres")
+    b.input("x", (2, 32, 10, 10))
+    b.input("r", (2, 48, 10, 10))
+    b.const("w", (rng.standard_normal((48, 32, 3, 3)) * 0.08).astype(np.float32))
+    b.const("b", (rng.standard_normal(48) * 0.1).astype(np.float32))
+    b.node("Conv", ["x", "w", "b"], "c", kernel_shape=[3, 3], pads=[1, 1, 1, 1])
+    b.node("Relu", ["c"], "y")
+    b.node("Add", ["r", "y"] if res_first else ["y", "r"], "s")
+    if post == "relu":
+        b.node("Relu", ["s"], "z")
+    elif post == "clip":
+        b.const("lo", np.float32(0.0))
+        b.const("hi", np.float32(1.5))
+        b.node("Clip", ["s", "lo", "hi"], "z")
+    else:
+        b.node("Identity", ["s"], "z")
+    b.output("z")
+    feeds = {"x": rng.standard_normal((2, 32, 10, 10)).astype(np.float32),
+             "r": rng.standard_normal((2, 48, 10, 10)).astype(np.float32)}
+    return b.graph(), feeds
+
+
+@pytest.mark.parametrize("mode", ["implicit", "im2col"])
+@pytest.mark.parametrize("sk", [1, 3])
+@pytest.mark.parametrize("post,res_first", [("relu", False), ("relu", True), ("clip", False),
+                                            ("none", True)])
+def test_conv_residual_epilogue(post, res_first, sk, mode, hip_ctx):
+    """A residual add (+ Relu / Clip / nothing) folded into the conv epilogue
+    (or the split-K reduce) matches the oracle and equals the unfused
+    device result bit for bit."""
+    sched = MfmaSchedule(64, 64, 16, 2, 2, 32, True, sk)
+    g, feeds = _conv_residual_graph(post, res_first)
+    c, got, want = device_run(g, feeds, conv_mode=mode, ctx=hip_ctx,
+                              schedule_fn=lambda n, mnk: sched)
+    assert sum(1 for n in c.graph.nodes if n.attrs.get("residual_subgraph")) == 1
+    assert "elementwise" not in {l.kind for l in c.module.plan}
+    assert_close("z", got["z"], want["z"])
+    g2, _ = _conv_residual_graph(post, res_first)
+    c2, got2, _ = device_run(g2, feeds, conv_mode=mode, ctx=hip_ctx,
+                             schedule_fn=lambda n, mnk: sched, fuse_residual=False)
+    assert not any(n.attrs.get("residual_subgraph") for n in c2.graph.nodes)
+    np.testing.assert_array_equal(got["z"], got2["z"])
+
+
 @pytest.mark.parametrize("n", [1, 2, 8])
 def test_conv_no_bias_no_act(n, hip_ctx):
     g, feeds = _conv_graph(n, 5, 11, 11, 6, 3, 1, 1, act=None, bias=False, seed=4)
@@ -285,7 +331,7 @@ def test_fused_elementwise_dedup_shares_kernel():
     from mdlc_amd.compiler import compile_graph
     from mdlc_amd.tools.build_resnet18 import build_resnet18
 
-    c = compile_graph(build_resnet18(batch=1))
+    c = compile_graph(build_resnet18(batch=1), fuse_residual=False)
     ew = {l.kernel_name for l in c.module.plan if l.kind == "elementwise"}
     assert len(ew) == 1
     assert isinstance(Node, type)

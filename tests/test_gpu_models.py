@@ -56,15 +56,19 @@ def _isolated(c, feeds, ctx):
     return got, want, chained
 
 
+@pytest.mark.parametrize("fold", [True, False], ids=["residual_folded", "reference_groups"])
 @pytest.mark.parametrize("batch", [1, 2])
 @pytest.mark.parametrize("mode", ["implicit", "im2col"])
-def test_resnet18_every_group(batch, mode, hip_ctx):
+def test_resnet18_every_group(batch, mode, fold, hip_ctx):
+    """Every fused group run in isolation on the oracle's inputs: the
+    reference's 32 groups, or 24 once the 8 residual Add+Relu groups are
+    folded into their convs."""
     g = build_resnet18(batch=batch)
     feeds = {"input": make_input(batch)}
-    c = compile_graph(g, feeds=feeds, conv_mode=mode)
+    c = compile_graph(g, feeds=feeds, conv_mode=mode, fuse_residual=fold)
     assert c.module.fallbacks() == []
     got, want, chained = _isolated(c, feeds, hip_ctx)
-    assert len(got) == 32
+    assert len(got) == (24 if fold else 32)
     _report_ratios(got, want)
     for t, v in got.items():
         assert_close(t, v, want[t], DEVICE_TENSOR)
@@ -96,10 +100,11 @@ def test_resnet18_batch32_rows_match_single_images(hip_ctx):
         assert_close(f"oracle logits[{i}]", y32[i:i + 1], want, FP32_NETWORK)
 
 
-def test_mobilenetv2_every_group(hip_ctx):
+@pytest.mark.parametrize("fold", [True, False], ids=["residual_folded", "reference_groups"])
+def test_mobilenetv2_every_group(fold, hip_ctx):
     g = build_mobilenetv2(batch=1)
     feeds = {"input": make_input(1, seed=3)}
-    c = compile_graph(g, feeds=feeds)
+    c = compile_graph(g, feeds=feeds, fuse_residual=fold)
     assert c.module.fallbacks() == []
     got, want, chained = _isolated(c, feeds, hip_ctx)
     _report_ratios(got, want)

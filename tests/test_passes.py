@@ -196,15 +196,21 @@ def test_resnet18_planner_at_batch32():
 
 def test_resnet18_explicit_lowering_has_reference_launch_count():
     """12 distinct kernels / 52 launches in the reference (docs/GAPS.md:18);
-    the same 52 launches here, none of them on the host."""
+    the same 52 launches here with the reference's pass pipeline alone, none
+    of them on the host — and 44 once the backend folds the 8 residual
+    Add+Relu groups into the conv epilogues."""
+    sched = __import__("mdlc_amd.codegen.schedule", fromlist=["x"]).MfmaSchedule(64, 64, 16, 2, 2, 32)
     c = compile_graph(build_resnet18(batch=1, calibrate=False), conv_mode="im2col",
-                      schedule_fn=lambda n, mnk: __import__(
-                          "mdlc_amd.codegen.schedule", fromlist=["x"]).MfmaSchedule(64, 64, 16, 2, 2, 32))
+                      schedule_fn=lambda n, mnk: sched, fuse_residual=False)
     kinds = [l.kind for l in c.module.plan]
     assert len(kinds) == 52
     assert kinds.count("im2col") == 20 and kinds.count("gemm") == 21
     assert kinds.count("elementwise") == 8
     assert c.module.fallbacks() == []
+    c = compile_graph(build_resnet18(batch=1, calibrate=False), conv_mode="im2col",
+                      schedule_fn=lambda n, mnk: sched)
+    kinds = [l.kind for l in c.module.plan]
+    assert len(kinds) == 44 and kinds.count("elementwise") == 0
 
 
 def test_mobilenetv2_structure():

@@ -1,0 +1,110 @@
+"""The float residual epilogue fold (CPU): which groups it folds into the
+conv that feeds them, which it must leave alone, and that the folded graph
+computes exactly what the unfused one does (the oracle evaluates both)."""
+
+from __future__ import annotations
+
+import numpy as np
+
+from conftest import build_graph
+from mdlc_amd.compiler import compile_graph
+from mdlc_amd.ir import verify_graph
+from mdlc_amd.passes import default_pipeline
+from mdlc_amd.passes.fuse_residual import FuseResidualEpilogue
+from mdlc_amd.passes.shape_inference import infer_shapes
+from mdlc_amd.tools.build_mobilenetv2 import build_mobilenetv2
+from mdlc_amd.tools.build_resnet18 import build_resnet18, make_input
+from mdlc_amd.tools.graph_builder import GraphBuilder
+from oracle.reference import run_reference
+
+
+def _folded(c):
+    return [n for n in c.graph.nodes if n.attrs.get("residual_subgraph")]
+
+
+def test_resnet18_folds_every_block_add_relu():
+    c = compile_graph(build_resnet18(batch=1, calibrate=False))
+    folded = _folded(c)
+    assert len(folded) == 8
+    assert all([s.op_type for s in n.attrs["residual_subgraph"]] == ["Add", "Relu"] for n in folded)
+    assert "FusedElementwise" not in c.graph.op_histogram()
+    verify_graph(c.graph)
+
+
+def test_mobilenetv2_folds_bare_residual_adds():
+    """All 10 residual adds fold, including the chained ones the elementwise
+    pass had grouped together; the folded graph equals the unfused one."""
+    from mdlc_amd.tools.build_mobilenetv2 import make_input as mb_input
+
+    x = mb_input(1)
+    c = compile_graph(build_mobilenetv2(batch=1), feeds={"input": x})
+    folded = _folded(c)
+    assert len(folded) == 10
+    assert all([s.op_type for s in n.attrs["residual_subgraph"]] == ["Add"] for n in folded)
+    verify_graph(c.graph)
+    cu = compile_graph(build_mobilenetv2(batch=1), feeds={"input": x}, fuse_residual=False)
+    a = run_reference(c.graph, {"input": x}, return_all=True)
+    b = run_reference(cu.graph, {"input": x}, return_all=True)
+    common = [k for k in a if k in b and k not in c.graph.initializers]
+    assert len(common) > 40
+    for k in common:
+        np.testing.assert_array_equal(a[k], b[k], err_msg=k)
+
+
+def test_folded_resnet18_equals_unfused_everywhere():
+    x = make_input(1)
+    cf = compile_graph(build_resnet18(batch=1), feeds={"input": x})
+    cu = compile_graph(build_resnet18(batch=1), feeds={"input": x}, fuse_residual=False)
+    assert len(cf.graph.nodes) == len(cu.graph.nodes) - 8
+    a = run_reference(cf.graph, {"input": x}, return_all=True)
+    b = run_reference(cu.graph, {"input": x}, return_all=True)
+    common = [k for k in a if k in b and k not in cf.graph.initializers]
+    assert len(common) > 20 and cf.graph.outputs[0] in common
+    for k in common:
+        np.testing.assert_array_equal(a[k], b[k], err_msg=k)
+    assert np.abs(a[cf.graph.outputs[0]]).max() > 0
+
+
+def test_residual_block_model_folds_and_matches():
+    g, feeds = build_graph("residual_block", c=4, h=8, w=8)
+    golden = run_reference(g.clone(), feeds)
+    c = compile_graph(g, feeds=feeds)
+    assert len(_folded(c)) == 1
+    out = run_reference(c.graph, feeds)
+    for o in c.graph.outputs:
+        np.testing.assert_array_equal(out[o], run_reference(
+            compile_graph(build_graph("residual_block", c=4, h=8, w=8)[0], feeds=feeds,
+                          fuse_residual=False).graph, feeds)[o])
+        assert np.abs(out[o] - golden[o]).max() < 1e-4
+
+
+def _conv_add(*, second_use=False, dependent=False, as_output=False, post="Relu"):
+    rng = np.random.default_rng(0)
+    b = GraphBuilder("ca")
+    b.input("x", (1, 4, 6, 6))
+    b.input("r", (1, 4, 6, 6))
+    b.const("w", rng.standard_normal((4, 4, 3, 3)).astype(np.float32))
+    b.node("Conv", ["x", "w"], "y", kernel_shape=[3, 3], pads=[1, 1, 1, 1])
+    r = "r"
+    if dependent:
+        b.node("Sigmoid", ["y"], "sy")
+        r = "sy"
+    b.node("Add", ["y", r], "s")
+    b.node(post, ["s"], "z")
+    b.output("z")
+    if second_use:
+        b.node("Tanh", ["y"], "t")
+        b.output("t")
+    if as_output:
+        b.output("y")
+    g = default_pipeline().run(b.graph())
+    infer_shapes(g)
+    return g
+
+
+def test_fold_conditions():
+    g = _conv_add()
+    assert FuseResidualEpilogue().run(g)
+    for kw in (dict(second_use=True), dict(dependent=True), dict(as_output=True)):
+        g = _conv_add(**kw)
+        assert not FuseResidualEpilogue().run(g), kw
