@@ -136,6 +136,16 @@ def roofline(prof, *, traffic_json: str = "") -> tuple:
 
 # ----- workloads ------------------------------------------------------------------------
 
+def schedule_source(args):
+    """The shipped measured schedules, or those of ``--schedules PATH`` (a
+    tuner JSON cache), with shape-aware defaults for problems not in it."""
+    if not args.schedules:
+        return None
+    from mdlc_amd.autotuner.tuner import AutotuneCache, Tuner
+
+    return Tuner(AutotuneCache(args.schedules), tune_misses=False)
+
+
 def network(args, name: str) -> dict:
     from mdlc_amd.compiler import compile_graph
 
@@ -148,7 +158,8 @@ def network(args, name: str) -> dict:
         from mdlc_amd.tools.build_repvit_int8 import build_repvit_int8 as build, make_input
     x = make_input(B)
     t0 = time.perf_counter()
-    c = compile_graph(build(batch=B), feeds={"input": x}, conv_mode=args.conv_mode)
+    c = compile_graph(build(batch=B), feeds={"input": x}, conv_mode=args.conv_mode,
+                      schedule_fn=schedule_source(args))
     log(f"{name} b={B}: compiled in {time.perf_counter() - t0:.1f} s, {len(c.module.plan)} launches")
     ms, host_s, prof, arena = time_module(c, {"input": x}, args.steps, args.warmup,
                                           args.profile_iters, args.graph)
@@ -191,7 +202,7 @@ def micro_gemm(args) -> dict:
     shapes, total_flops, total_ms, cpu = {}, 0.0, 0.0, {}
     for M, N, K in SHAPES:
         g, feeds = build_micro_gemm(M, N, K)
-        c = compile_graph(g, feeds=feeds)
+        c = compile_graph(g, feeds=feeds, schedule_fn=schedule_source(args))
         ms, _, _, _ = time_module(c, feeds, args.steps * 10, args.warmup, args.profile_iters)
         fl = 2.0 * M * N * K
         key = f"{M}x{N}x{K}"
@@ -241,7 +252,7 @@ def int8_gemm(args) -> dict:
     b.node("QGemm", ["xq", "w", "b", "m"], "y", transB=1)
     b.output("y")
     feeds = {"xq": rng.integers(-127, 128, (M, K)).astype(np.int8)}
-    c = compile_graph(b.graph(), feeds=feeds)
+    c = compile_graph(b.graph(), feeds=feeds, schedule_fn=schedule_source(args))
     ms, _, prof, _ = time_module(c, feeds, args.steps, args.warmup, args.profile_iters)
     tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     roof, _ = roofline(prof)
@@ -263,6 +274,8 @@ def main(argv=None) -> int:
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--size", type=int, default=4096, help="int8_gemm M = N = K")
     ap.add_argument("--conv-mode", default="implicit", choices=["implicit", "im2col"])
+    ap.add_argument("--schedules", default="", help="tuner JSON cache to use instead of the "
+                    "shipped mdlc_amd/autotuner/tuned_gfx950.json")
     ap.add_argument("--graph", action="store_true", help="replay the plan as a hipGraph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-iters", type=int, default=3)
