@@ -47,6 +47,9 @@ ScheduleFn = Callable[[Optional[Node], tuple], MfmaSchedule]
 
 VIEW_OPS = {"Flatten", "Reshape", "Identity", "Squeeze", "Unsqueeze"}
 
+# fp32 depthwise conv: adjacent outputs per thread, by horizontal stride
+DW_OUTPUTS_PER_THREAD = {1: 4, 2: 2}
+
 
 class HipCodegen(Int8LoweringMixin):
     def __init__(self, schedule_fn: Optional[ScheduleFn] = None, *, conv_mode: str = "implicit",
@@ -294,16 +297,21 @@ class HipCodegen(Int8LoweringMixin):
         a = node.attrs
         act = a.get("activation")
         win = (geo["KH"], geo["KW"], geo["SH"], geo["SW"], geo["DH"], geo["DW"])
-        sig = ("dwconv", win, has_bias, self._act_sig(a))
+        vw = DW_OUTPUTS_PER_THREAD.get(geo["SW"], 1)
+        sig = ("dwconv", win, has_bias, self._act_sig(a), vw)
         kname = self._kernel(sig, lambda i: T.dwconv_kernel(
             f"dwconv_{'x'.join(str(v) for v in win)}_{act or 'none'}_{i}", win,
-            with_bias=has_bias, activation=act, attrs=self._act_attrs(a)))
+            with_bias=has_bias, activation=act, attrs=self._act_attrs(a), vw=vw))
         w = node.inputs[1]
         wdev = self._pack(f"{w}__dev", np.asarray(g.initializers[w], np.float32).reshape(geo["OC"], -1))
         total = geo["N"] * geo["OC"] * geo["OH"] * geo["OW"]
+        vw = DW_OUTPUTS_PER_THREAD.get(geo["SW"], 1)
+        threads = geo["N"] * geo["OC"] * geo["OH"] * -(-geo["OW"] // vw)
+        if max(threads, geo["N"] * geo["C"] * geo["H"] * geo["W"], total) >= 2 ** 31:
+            raise NotImplementedError("HIP codegen: depthwise conv of 2^31 elements or more")
         ins = [node.inputs[0], wdev] + ([node.inputs[2]] if has_bias else [])
         self.plan.append(Launch(
-            "dwconv", kname, ins, [node.outputs[0]], (-(-total // 256), 1, 1), (256, 1, 1),
+            "dwconv", kname, ins, [node.outputs[0]], (-(-threads // 256), 1, 1), (256, 1, 1),
             {**{k: geo[k] for k in ("N", "C", "H", "W", "OC", "OH", "OW", "PT", "PL")},
              "with_bias": has_bias, "node": node,
              "flops": 2 * total * geo["KH"] * geo["KW"],

@@ -229,8 +229,9 @@ def copy_kernel(name: str = "copy_bytes") -> tuple:
 
 
 def dwconv_kernel(name: str, win: tuple, *, with_bias: bool, activation: Optional[str],
-                  attrs: dict) -> tuple:
-    """Depthwise conv with epilogue. ``win`` = (KH, KW, SH, SW, DH, DW).
+                  attrs: dict, vw: int = 4) -> tuple:
+    """Depthwise conv with epilogue, ``vw`` adjacent outputs per thread.
+    ``win`` = (KH, KW, SH, SW, DH, DW).
     ABI: (x, w, [bias], y, N, C, H, W, OC, OH, OW, PT, PL)."""
     epi = f"{name}_epi"
     src = epilogue_struct(epi, bias_mode="row" if with_bias else None,
@@ -240,7 +241,7 @@ def dwconv_kernel(name: str, win: tuple, *, with_bias: bool, activation: Optiona
         f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
         f"    const float* __restrict__ x, const float* __restrict__ w, {bias_arg}"
         "float* __restrict__ y,\n    int N, int C, int H, int W, int OC, int OH, int OW, int PT, int PL) {\n"
-        f"  mdlc::dwconv_f32<{', '.join(str(v) for v in win)}, {epi}>(x, w, "
+        f"  mdlc::dwconv_f32<{', '.join(str(v) for v in win)}, {vw}, {epi}>(x, w, "
         f"{'bias' if with_bias else 'nullptr'}, y, N, C, H, W, OC, OH, OW, PT, PL);\n}}\n")
 
 

@@ -1,0 +1,49 @@
+"""The compile CLI (reference: mdlc/tools/compile.py:15-51) on the CPU:
+report, emit, cost-model tuning, and the clear error for ONNX input."""
+
+from __future__ import annotations
+
+import json
+
+import pytest
+
+from mdlc_amd.tools import compile as cli
+
+
+def test_report_names_passes_kernels_and_planner(capsys):
+    assert cli.main(["resnet18", "--report"]) == 0
+    out = capsys.readouterr().out
+    assert "compile report" in out and "HIP module" in out and "host fallbacks: none" in out
+    assert "fused groups" in out
+
+
+def test_emit_writes_the_hiprtc_translation_unit(tmp_path, capsys):
+    path = tmp_path / "resnet18.hip"
+    assert cli.main(["resnet18", "--emit", str(path)]) == 0
+    src = path.read_text()
+    assert 'extern "C" __global__' in src and "gemm_f32_mfma" in src
+    assert "wrote generated HIP" in capsys.readouterr().out
+
+
+def test_tune_without_a_device_uses_the_cost_model(tmp_path, capsys):
+    cache = tmp_path / "sched.json"
+    assert cli.main(["micro:196x256x2304", "--tune", "--cache", str(cache), "--budget", "4"]) == 0
+    entries = json.loads(cache.read_text())
+    assert list(entries) == ["196x256x2304"]
+    assert "cost model" in capsys.readouterr().out or entries["196x256x2304"]["measured"]
+
+
+def test_no_fold_keeps_the_reference_groups(capsys):
+    assert cli.main(["resnet18", "--no-fold", "--report", "--conv-mode", "im2col"]) == 0
+    out = capsys.readouterr().out
+    assert "elementwisex8" in out and "im2colx20" in out
+
+
+def test_onnx_input_fails_with_a_clear_message(capsys):
+    assert cli.main(["model.onnx"]) == 2
+    assert "onnx" in capsys.readouterr().err.lower()
+
+
+def test_unknown_model_name():
+    with pytest.raises(SystemExit):
+        cli.main(["vgg16"])
