@@ -47,9 +47,6 @@ ScheduleFn = Callable[[Optional[Node], tuple], MfmaSchedule]
 
 VIEW_OPS = {"Flatten", "Reshape", "Identity", "Squeeze", "Unsqueeze"}
 
-# fp32 depthwise conv: adjacent outputs per thread, by horizontal stride
-DW_OUTPUTS_PER_THREAD = {1: 4, 2: 2}
-
 
 class HipCodegen(Int8LoweringMixin):
     def __init__(self, schedule_fn: Optional[ScheduleFn] = None, *, conv_mode: str = "implicit",
@@ -297,18 +294,16 @@ class HipCodegen(Int8LoweringMixin):
         a = node.attrs
         act = a.get("activation")
         win = (geo["KH"], geo["KW"], geo["SH"], geo["SW"], geo["DH"], geo["DW"])
-        vw = DW_OUTPUTS_PER_THREAD.get(geo["SW"], 1)
-        sig = ("dwconv", win, has_bias, self._act_sig(a), vw)
+        sig = ("dwconv", win, has_bias, self._act_sig(a))
         kname = self._kernel(sig, lambda i: T.dwconv_kernel(
             f"dwconv_{'x'.join(str(v) for v in win)}_{act or 'none'}_{i}", win,
-            with_bias=has_bias, activation=act, attrs=self._act_attrs(a), vw=vw))
+            with_bias=has_bias, activation=act, attrs=self._act_attrs(a)))
         w = node.inputs[1]
         wdev = self._pack(f"{w}__dev", np.asarray(g.initializers[w], np.float32).reshape(geo["OC"], -1))
         total = geo["N"] * geo["OC"] * geo["OH"] * geo["OW"]
-        vw = DW_OUTPUTS_PER_THREAD.get(geo["SW"], 1)
-        threads = geo["N"] * geo["OC"] * geo["OH"] * -(-geo["OW"] // vw)
-        if max(threads, geo["N"] * geo["C"] * geo["H"] * geo["W"], total) >= 2 ** 31:
-            raise NotImplementedError("HIP codegen: depthwise conv of 2^31 elements or more")
+        threads = geo["N"] * geo["OC"] * -(-geo["OH"] // T.WINDOW_VH) * geo["OW"]
+        if max(threads, geo["H"] * geo["W"]) >= 2 ** 31:
+            raise NotImplementedError("HIP codegen: depthwise conv too large for 32-bit indices")
         ins = [node.inputs[0], wdev] + ([node.inputs[2]] if has_bias else [])
         self.plan.append(Launch(
             "dwconv", kname, ins, [node.outputs[0]], (-(-threads // 256), 1, 1), (256, 1, 1),
@@ -426,10 +421,15 @@ class HipCodegen(Int8LoweringMixin):
         dh, dw = a.get("dilations", [1, 1])
         (pt, _), (pl, _) = resolve_pads(a.get("auto_pad", "NOTSET"), a.get("pads"), xs[2:],
                                         (kh, kw), (sh, sw), (dh, dw))
-        self._kernel("maxpool", lambda i: T.maxpool_kernel("maxpool"))
+        win = (kh, kw, sh, sw, dh, dw)
+        kname = self._kernel(("maxpool", win), lambda i: T.maxpool_kernel(
+            f"maxpool_{'x'.join(str(v) for v in win)}_{i}", win))
         total = int(np.prod(ys))
+        threads = xs[0] * xs[1] * -(-ys[2] // T.WINDOW_VH) * ys[3]
+        if max(threads, xs[2] * xs[3]) >= 2 ** 31:
+            raise NotImplementedError("HIP codegen: max pool too large for 32-bit indices")
         self.plan.append(Launch(
-            "maxpool", "maxpool", [node.inputs[0]], [node.outputs[0]], (-(-total // 256), 1, 1),
+            "maxpool", kname, [node.inputs[0]], [node.outputs[0]], (-(-threads // 256), 1, 1),
             (256, 1, 1), {"planes": xs[0] * xs[1], "H": xs[2], "W": xs[3], "OH": ys[2],
                           "OW": ys[3], "KH": kh, "KW": kw, "SH": sh, "SW": sw, "PT": pt, "PL": pl,
                           "DH": dh, "DW": dw, "node": node,

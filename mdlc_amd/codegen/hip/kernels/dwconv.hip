@@ -1,65 +1,79 @@
-// Direct depthwise convolution (group == C, one input channel per output
-// channel, channel multiplier OC/C) with a fused bias/activation epilogue.
-//
-// Each thread computes VW horizontally adjacent outputs of one output row:
-// it loads the input span those outputs share once per filter row (for a
-// 3x3 stride-1 window, 6 loads serve 4 outputs instead of 12) and keeps the
-// plane's KH*KW weights in registers. Indices are 32-bit (the host checks
-// the sizes); the taps of each output accumulate in (kh, kw) order.
+// Per-plane sliding-window kernels over NCHW float32: depthwise convolution
+// (group == C, channel multiplier OC/C, fused bias/activation epilogue) and
+// max pooling share one template. Taps are combined in (kh, kw) order.
+// Indices within a plane are 32-bit (the host checks the sizes).
 namespace mdlc {
 
-template <int KH, int KW, int SH, int SW, int DH, int DW, int VW, class Epi>
-__device__ __forceinline__ void dwconv_f32(const float* __restrict__ x, const float* __restrict__ w,
-                                           const float* __restrict__ bias, float* __restrict__ y,
-                                           int N, int C, int H, int W, int OC, int OH, int OW,
-                                           int PT, int PL) {
-  constexpr int SPAN = (VW - 1) * SW + (KW - 1) * DW + 1;
-  const int segs = (OW + VW - 1) / VW;
-  const int per_plane = OH * segs;
+// Depthwise conv: acc = acc + w[kh][kw] * x, then the epilogue.
+template <class Epi>
+struct DwOp {
+  static constexpr bool weights = true;
+  __device__ __forceinline__ static float pad() { return 0.f; }
+  __device__ __forceinline__ static float init() { return 0.f; }
+  __device__ __forceinline__ static float step(float acc, float x, float w) { return acc + w * x; }
+  __device__ __forceinline__ static float finish(float acc, float b) { return Epi::apply(acc, b); }
+};
+
+// Max pool: out-of-range taps are -inf (the NumPy padding value).
+struct MaxOp {
+  static constexpr bool weights = false;
+  __device__ __forceinline__ static float pad() { return -__builtin_inff(); }
+  __device__ __forceinline__ static float init() { return -__builtin_inff(); }
+  __device__ __forceinline__ static float step(float acc, float x, float) { return fmaxf(acc, x); }
+  __device__ __forceinline__ static float finish(float acc, float) { return acc; }
+};
+
+// Column-strip form: each thread owns VH vertically adjacent outputs of one
+// output column and loads the (VH-1)*SH + (KH-1)*DH + 1 input rows x KW taps
+// they need into registers, all loads issued before any arithmetic, so many
+// bytes are in flight per wave. Consecutive threads own consecutive columns,
+// so every load and store instruction is contiguous across the wave.
+template <int KH, int KW, int SH, int SW, int DH, int DW, int VH, class Op>
+__device__ __forceinline__ void window_column_f32(const float* __restrict__ x,
+                                                  const float* __restrict__ w,
+                                                  const float* __restrict__ bias,
+                                                  float* __restrict__ y, int planes, int C, int H,
+                                                  int W, int OC, int OH, int OW, int PT, int PL) {
+  constexpr int NR = (VH - 1) * SH + (KH - 1) * DH + 1;
+  const int strips = (OH + VH - 1) / VH;
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= N * OC * per_plane) return;
-  const int plane = idx / per_plane;               // n * OC + oc
-  const int rem = idx - plane * per_plane;
-  const int oh = rem / segs;
-  const int ow0 = (rem - oh * segs) * VW;
+  if (idx >= planes * strips * OW) return;
+  const int ow = idx % OW;
+  const int ps = idx / OW;                          // plane * strips + strip
+  const int plane = ps / strips;
+  const int oh0 = (ps - plane * strips) * VH;
   const int oc = plane % OC;
   const int n = plane / OC;
   const int c = oc / (OC / C);
   const float* xp = x + ((size_t)n * C + c) * H * W;
+  const int ih0 = oh0 * SH - PT;
+  const int iw0 = ow * SW - PL;
+  float v[NR][KW];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int ih = ih0 + r;
+    const bool row_ok = (unsigned)ih < (unsigned)H;
+#pragma unroll
+    for (int kw = 0; kw < KW; ++kw) {
+      const int iw = iw0 + kw * DW;
+      v[r][kw] = (row_ok && (unsigned)iw < (unsigned)W) ? xp[ih * W + iw] : Op::pad();
+    }
+  }
   float wr[KH * KW];
 #pragma unroll
-  for (int t = 0; t < KH * KW; ++t) wr[t] = w[oc * KH * KW + t];
-  float acc[VW];
+  for (int k = 0; k < KH * KW; ++k) wr[k] = Op::weights ? w[oc * KH * KW + k] : 0.f;
+  const float b = bias ? bias[oc] : 0.f;
+  float* yp = y + (size_t)plane * OH * OW + ow;
 #pragma unroll
-  for (int v = 0; v < VW; ++v) acc[v] = 0.f;
-  const int iw0 = ow0 * SW - PL;
+  for (int j = 0; j < VH; ++j) {
+    if (oh0 + j >= OH) break;
+    float acc = Op::init();
 #pragma unroll
-  for (int kh = 0; kh < KH; ++kh) {
-    const int ih = oh * SH - PT + kh * DH;
-    const bool row_ok = (unsigned)ih < (unsigned)H;
-    float xs[SPAN];
+    for (int kh = 0; kh < KH; ++kh)
 #pragma unroll
-    for (int j = 0; j < SPAN; ++j) {
-      const int iw = iw0 + j;
-      xs[j] = (row_ok && (unsigned)iw < (unsigned)W) ? xp[ih * W + iw] : 0.f;
-    }
-#pragma unroll
-    for (int v = 0; v < VW; ++v)
-#pragma unroll
-      for (int kw = 0; kw < KW; ++kw) acc[v] = acc[v] + wr[kh * KW + kw] * xs[v * SW + kw * DW];
+      for (int kw = 0; kw < KW; ++kw) acc = Op::step(acc, v[j * SH + kh * DH][kw], wr[kh * KW + kw]);
+    yp[(oh0 + j) * OW] = Op::finish(acc, b);
   }
-  const float b = Epi::bias ? bias[oc] : 0.f;
-  float* yp = y + ((size_t)plane * OH + oh) * OW + ow0;
-  if constexpr (VW == 4) {
-    if ((OW & 3) == 0) {            // rows and segments are 16-byte aligned
-      *reinterpret_cast<float4*>(yp) = make_float4(Epi::apply(acc[0], b), Epi::apply(acc[1], b),
-                                                   Epi::apply(acc[2], b), Epi::apply(acc[3], b));
-      return;
-    }
-  }
-#pragma unroll
-  for (int v = 0; v < VW; ++v)
-    if (ow0 + v < OW) yp[v] = Epi::apply(acc[v], b);
 }
 
 }  // namespace mdlc

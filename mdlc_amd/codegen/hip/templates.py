@@ -206,12 +206,20 @@ def im2col_kernel(name: str = "im2col") -> tuple:
         "  mdlc::im2col_f32(x, cols, C, H, W, KH, KW, OH, OW, SH, SW, PH, PW, DH, DW, N, ldc);\n}\n")
 
 
-def maxpool_kernel(name: str = "maxpool") -> tuple:
+WINDOW_VH = 8          # outputs per thread down a column in the window kernels
+
+
+def maxpool_kernel(name: str, win: tuple, vh: int = WINDOW_VH) -> tuple:
+    """Max pool for the window ``win`` = (KH, KW, SH, SW, DH, DW), ``vh``
+    outputs per thread down a column. ABI: (x, y, planes, H, W, OH, OW, KH,
+    KW, SH, SW, PT, PL, DH, DW) — the window arguments repeat the compile-time
+    ones; one thread per (plane, column, strip of ``vh`` rows)."""
     return name, (
         f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
         "    const float* __restrict__ x, float* __restrict__ y, int planes, int H, int W,\n"
         "    int OH, int OW, int KH, int KW, int SH, int SW, int PT, int PL, int DH, int DW) {\n"
-        "  mdlc::maxpool_f32(x, y, planes, H, W, OH, OW, KH, KW, SH, SW, PT, PL, DH, DW);\n}\n")
+        f"  mdlc::window_column_f32<{', '.join(str(v) for v in win)}, {vh}, mdlc::MaxOp>("
+        "x, nullptr, nullptr, y, planes, 1, H, W, 1, OH, OW, PT, PL);\n}\n")
 
 
 def gap_kernel(name: str = "global_avg_pool") -> tuple:
@@ -229,10 +237,11 @@ def copy_kernel(name: str = "copy_bytes") -> tuple:
 
 
 def dwconv_kernel(name: str, win: tuple, *, with_bias: bool, activation: Optional[str],
-                  attrs: dict, vw: int = 4) -> tuple:
-    """Depthwise conv with epilogue, ``vw`` adjacent outputs per thread.
-    ``win`` = (KH, KW, SH, SW, DH, DW).
-    ABI: (x, w, [bias], y, N, C, H, W, OC, OH, OW, PT, PL)."""
+                  attrs: dict, vh: int = WINDOW_VH) -> tuple:
+    """Depthwise conv with epilogue, ``vh`` outputs per thread down a
+    column. ``win`` = (KH, KW, SH, SW, DH, DW).
+    ABI: (x, w, [bias], y, N, C, H, W, OC, OH, OW, PT, PL); one thread per
+    (plane, column, strip of ``vh`` rows)."""
     epi = f"{name}_epi"
     src = epilogue_struct(epi, bias_mode="row" if with_bias else None,
                           activation=activation, attrs=attrs)
@@ -241,8 +250,8 @@ def dwconv_kernel(name: str, win: tuple, *, with_bias: bool, activation: Optiona
         f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
         f"    const float* __restrict__ x, const float* __restrict__ w, {bias_arg}"
         "float* __restrict__ y,\n    int N, int C, int H, int W, int OC, int OH, int OW, int PT, int PL) {\n"
-        f"  mdlc::dwconv_f32<{', '.join(str(v) for v in win)}, {vw}, {epi}>(x, w, "
-        f"{'bias' if with_bias else 'nullptr'}, y, N, C, H, W, OC, OH, OW, PT, PL);\n}}\n")
+        f"  mdlc::window_column_f32<{', '.join(str(v) for v in win)}, {vh}, mdlc::DwOp<{epi}>>("
+        f"x, w, {'bias' if with_bias else 'nullptr'}, y, N * OC, C, H, W, OC, OH, OW, PT, PL);\n}}\n")
 
 
 # ----- fused elementwise ----------------------------------------------------

@@ -47,3 +47,9 @@ def test_onnx_input_fails_with_a_clear_message(capsys):
 def test_unknown_model_name():
     with pytest.raises(SystemExit):
         cli.main(["vgg16"])
+
+
+@pytest.mark.gpu
+def test_run_on_the_device(capsys):
+    assert cli.main(["micro:49x512x4608", "--run"]) == 0
+    assert "ran on the device" in capsys.readouterr().out

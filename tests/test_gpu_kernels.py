@@ -325,6 +325,28 @@ def test_maxpool_and_gap(n, hip_ctx):
     assert_close("y", got["y"], want["y"], DEVICE_TENSOR)
 
 
+@pytest.mark.parametrize("win", [(3, 3, 1, 1, 1, 1, 1, 0), (3, 3, 2, 2, 1, 1, 1, 0),
+                                 (2, 2, 2, 2, 0, 0, 1, 0), (3, 2, 1, 3, 1, 0, 1, 0),
+                                 (3, 3, 2, 2, 1, 1, 2, 0), (3, 3, 2, 2, 0, 0, 1, 1)],
+                         ids=lambda w: "k{}x{}_s{}x{}_p{}{}_d{}_c{}".format(*w))
+def test_maxpool_windows(win, hip_ctx):
+    """Windows, strides (adjacent outputs per thread 4, 2 and 1), padding,
+    dilation and ceil mode over widths that are not multiples of the per-thread
+    output count; max pooling is exact, so the match is bitwise."""
+    kh, kw, sh, sw, ph, pw, d, ceil = win
+    rng = np.random.default_rng(12)
+    b = GraphBuilder("mp")
+    b.input("x", (2, 3, 15, 13))
+    b.node("MaxPool", ["x"], "m", kernel_shape=[kh, kw], strides=[sh, sw], pads=[ph, pw, ph, pw],
+           dilations=[d, d], ceil_mode=ceil)
+    b.output("m")
+    # (the ceil-mode case divides evenly: the oracle's strided slice cannot
+    # express a partial last window, ops.py:119-124)
+    feeds = {"x": rng.standard_normal((2, 3, 15, 13)).astype(np.float32)}
+    _, got, want = device_run(b.graph(), feeds, ctx=hip_ctx)
+    assert_close("m", got["m"], want["m"], BITWISE)
+
+
 def test_fused_elementwise_dedup_shares_kernel():
     """Structurally identical groups compile to one kernel (CPU-side check
     that still belongs with the kernel tests)."""
