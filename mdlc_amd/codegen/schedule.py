@@ -101,7 +101,7 @@ class MfmaSchedule:
 def gemm_search_space(splits=(1,)) -> Iterator[MfmaSchedule]:
     for bm in (32, 64, 128, 256):
         for bn in (32, 64, 128, 256):
-            for bk in (8, 16, 32):
+            for bk in (8, 16, 32, 64):
                 for wgm, wgn in ((1, 1), (2, 1), (1, 2), (2, 2), (4, 1), (1, 4), (4, 2), (2, 4)):
                     for ms in (32, 16):
                         for db in (True, False):
