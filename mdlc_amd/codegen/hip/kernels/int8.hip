@@ -65,6 +65,92 @@ template <int BYTES> __device__ __forceinline__ void buffer_gather(__amdgpu_buff
   }
 }
 
+// Epilogue shared by both staging paths: bias, requant (or dequant), the
+// fused lookup or residual add, and the packed stores. ``acc`` is laid out
+// as the operand-swapped MFMA leaves it (see qgemm_i8_mfma).
+template <int BM, int BN, int WGM, int WGN, int MS, int OUT, int LO, int EPI, class Acc>
+__device__ __forceinline__ void qgemm_epilogue(const QGemmArgs& g, Acc& acc, int m0, int n0) {
+  constexpr int NT = WGM * WGN * 64;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int MI = WM / MS, NI = WN / MS;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm0 = (wave / WGN) * WM;
+  const int wn0 = (wave % WGN) * WN;
+  const int li = lane % MS;
+  const int lk = lane / MS;
+  // acc[mi][ni][4q + j] is C[m0 + wm0 + mi*MS + li][n0 + wn0 + ni*MS + q*8 + lk*4 + j]
+  // (MS = 32; for MS = 16 the single group is at lk*4 + j).
+  constexpr int NG = MfmaI8<MS>::kAcc / 4;
+  const bool vec_ok = (g.ldc & 3) == 0;
+  __shared__ i8 table[EPI == 1 ? 256 : 1];
+  if (EPI == 1) {                 // the K loop ended with a barrier: LDS is free
+    for (int i = tid; i < 256; i += NT) table[i] = g.aux[i];
+    __syncthreads();
+  }
+  auto finish = [&](i8 code, i8 res) -> i8 {
+    if (EPI == 1) return table[(int)code + 128];
+    if (EPI == 2) {
+      const float v = (float)res * g.res_mult + (float)code * g.acc_mult;
+      return (i8)(int)fminf(fmaxf(rintf(v), -127.0f), 127.0f);
+    }
+    return code;
+  };
+#pragma unroll
+  for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+      const int col = n0 + wn0 + ni * MS + q * 8 + lk * 4;
+      if (col >= g.N) continue;
+      const intx4 bv = *reinterpret_cast<const intx4*>(g.bias + col);
+      const floatx4 mv = *reinterpret_cast<const floatx4*>(g.mult + col);
+      const bool full = vec_ok && col + 4 <= g.N;
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi) {
+        const int row = m0 + wm0 + mi * MS + li;
+        if (row >= g.M) continue;
+        if (OUT == 1) {
+          float* cp = static_cast<float*>(g.C) + (size_t)row * g.ldc + col;
+          float o[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[j] = (float)(acc[mi][ni][4 * q + j] + bv[j]) * mv[j];
+          if (full) {
+            *reinterpret_cast<float4*>(cp) = make_float4(o[0], o[1], o[2], o[3]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (col + j < g.N) cp[j] = o[j];
+          }
+        } else {
+          const size_t off = (size_t)row * g.ldc + col;
+          i8* cp = static_cast<i8*>(g.C) + off;
+          union { int w; i8 b[4]; } o, r;
+          r.w = 0;
+          if (EPI == 2) {
+            if (full) {
+              r.w = *reinterpret_cast<const int*>(g.aux + off);
+            } else {
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                if (col + j < g.N) r.b[j] = g.aux[off + j];
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            o.b[j] = finish(requant(acc[mi][ni][4 * q + j] + bv[j], mv[j], (float)LO), r.b[j]);
+          if (full) {
+            *reinterpret_cast<int*>(cp) = o.w;
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (col + j < g.N) cp[j] = o.b[j];
+          }
+        }
+      }
+    }
+}
+
 // C[m][n] = q(sum_k A[m][k] * B[n][k] + bias[n]).
 //
 // AMODE 0: dense A [M][lda] (lda % 16 == 0).
@@ -293,76 +379,7 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
     }
   }
 
-  // ---- epilogue ---------------------------------------------------------------
-  // acc[mi][ni][4q + j] is C[m0 + wm0 + mi*MS + li][n0 + wn0 + ni*MS + q*8 + lk*4 + j]
-  // (MS = 32; for MS = 16 the single group is at lk*4 + j).
-  constexpr int NG = MfmaI8<MS>::kAcc / 4;
-  const bool vec_ok = (g.ldc & 3) == 0;
-  __shared__ i8 table[EPI == 1 ? 256 : 1];
-  if (EPI == 1) {                 // the K loop ended with a barrier: LDS is free
-    for (int i = tid; i < 256; i += NT) table[i] = g.aux[i];
-    __syncthreads();
-  }
-  auto finish = [&](i8 code, i8 res) -> i8 {
-    if (EPI == 1) return table[(int)code + 128];
-    if (EPI == 2) {
-      const float v = (float)res * g.res_mult + (float)code * g.acc_mult;
-      return (i8)(int)fminf(fmaxf(rintf(v), -127.0f), 127.0f);
-    }
-    return code;
-  };
-#pragma unroll
-  for (int ni = 0; ni < NI; ++ni)
-#pragma unroll
-    for (int q = 0; q < NG; ++q) {
-      const int col = n0 + wn0 + ni * MS + q * 8 + lk * 4;
-      if (col >= g.N) continue;
-      const intx4 bv = *reinterpret_cast<const intx4*>(g.bias + col);
-      const floatx4 mv = *reinterpret_cast<const floatx4*>(g.mult + col);
-      const bool full = vec_ok && col + 4 <= g.N;
-#pragma unroll
-      for (int mi = 0; mi < MI; ++mi) {
-        const int row = m0 + wm0 + mi * MS + li;
-        if (row >= g.M) continue;
-        if (OUT == 1) {
-          float* cp = static_cast<float*>(g.C) + (size_t)row * g.ldc + col;
-          float o[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) o[j] = (float)(acc[mi][ni][4 * q + j] + bv[j]) * mv[j];
-          if (full) {
-            *reinterpret_cast<float4*>(cp) = make_float4(o[0], o[1], o[2], o[3]);
-          } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              if (col + j < g.N) cp[j] = o[j];
-          }
-        } else {
-          const size_t off = (size_t)row * g.ldc + col;
-          i8* cp = static_cast<i8*>(g.C) + off;
-          union { int w; i8 b[4]; } o, r;
-          r.w = 0;
-          if (EPI == 2) {
-            if (full) {
-              r.w = *reinterpret_cast<const int*>(g.aux + off);
-            } else {
-#pragma unroll
-              for (int j = 0; j < 4; ++j)
-                if (col + j < g.N) r.b[j] = g.aux[off + j];
-            }
-          }
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            o.b[j] = finish(requant(acc[mi][ni][4 * q + j] + bv[j], mv[j], (float)LO), r.b[j]);
-          if (full) {
-            *reinterpret_cast<int*>(cp) = o.w;
-          } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              if (col + j < g.N) cp[j] = o.b[j];
-          }
-        }
-      }
-    }
+  qgemm_epilogue<BM, BN, WGM, WGN, MS, OUT, LO, EPI>(g, acc, m0, n0);
 }
 
 // Depthwise conv over NHWC int8 (one input channel per output channel),
