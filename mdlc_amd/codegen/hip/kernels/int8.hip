@@ -182,8 +182,8 @@ __device__ __forceinline__ void qgemm_epilogue(const QGemmArgs& g, Acc& acc, int
 // The MFMA takes the B tile as its row operand: a lane then holds four
 // consecutive output columns per accumulator group, stored as one 32-bit
 // (int8) or 128-bit (float) write.
-template <int BM, int BN, int BK, int WGM, int WGN, int MS, int AMODE, int GV, int CIN, int OUT, int LO,
-          int EPI, int DWG, class Win>
+template <int BM, int BN, int BK, int WGM, int WGN, int MS, bool DB, int AMODE, int GV, int CIN, int OUT,
+          int LO, int EPI, int DWG, class Win>
 __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   constexpr int NT = WGM * WGN * 64;
   constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -200,8 +200,9 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   static_assert(DWG == 0 || (AMODE == 1 && CIN == BN), "depthwise tiles span one channel block");
   typedef typename MfmaI8<MS>::acc_t acc_t;
 
-  __shared__ __attribute__((aligned(16))) i8 As[2][BM * LDS_ROW];
-  __shared__ __attribute__((aligned(16))) i8 Bs[2][BN * LDS_ROW];
+  constexpr int NBUF = DB ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) i8 As[NBUF][BM * LDS_ROW];
+  __shared__ __attribute__((aligned(16))) i8 Bs[NBUF][BN * LDS_ROW];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -344,7 +345,7 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   // operands, and land in a buffer nobody reads), so each iteration is one
   // basic block the scheduler can interleave with the MFMAs. The waves raise
   // their issue priority while they feed the matrix cores.
-  constexpr bool kTwoSets = MfmaI8<MS>::kAcc * MI * NI + 8 * (A_PT + B_PT) <= 192;
+  constexpr bool kTwoSets = DB && MfmaI8<MS>::kAcc * MI * NI + 8 * (A_PT + B_PT) <= 192;
   intx4 ra0[A_PT], rb0[B_PT], ra1[kTwoSets ? A_PT : 1], rb1[kTwoSets ? B_PT : 1];
   const int nk = (g.K + BK - 1) / BK;
   if constexpr (kTwoSets) {
@@ -365,7 +366,7 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
       step(kt, ra0, rb0, ra1, rb1);
       if (kt + 1 < nk) step(kt + 1, ra1, rb1, ra0, rb0);
     }
-  } else {
+  } else if constexpr (DB) {
     load_tiles(0, ra0, rb0);
     store_tiles(0, ra0, rb0);
     __syncthreads();
@@ -375,6 +376,19 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
       compute(kt & 1);
       __builtin_amdgcn_s_setprio(0);
       store_tiles((kt + 1) & 1, ra0, rb0);
+      __syncthreads();
+    }
+  } else {
+    // one LDS buffer (half the LDS, e.g. for 256-byte K tiles): the next
+    // tile waits in registers while the current one is consumed
+    load_tiles(0, ra0, rb0);
+    for (int kt = 0; kt < nk; ++kt) {
+      store_tiles(0, ra0, rb0);
+      __syncthreads();
+      load_tiles((kt + 1) * BK, ra0, rb0);
+      __builtin_amdgcn_s_setprio(1);
+      compute(0);
+      __builtin_amdgcn_s_setprio(0);
       __syncthreads();
     }
   }

@@ -377,7 +377,8 @@ def qgemm_kernel(name: str, sched: MfmaSchedule, *, amode: int, out_f32: bool, l
     s = sched
     winty = "mdlc::NoWin" if win is None else "mdlc::ConvWin<%d, %d, %d, %d, %d, %d, %d, %d>" % tuple(win)
     nt = s.threads_per_block()
-    tmpl = (f"mdlc::qgemm_i8_mfma<{s.BM}, {s.BN}, {s.BK}, {s.WGM}, {s.WGN}, {s.MS}, {amode}, "
+    tmpl = (f"mdlc::qgemm_i8_mfma<{s.BM}, {s.BN}, {s.BK}, {s.WGM}, {s.WGN}, {s.MS}, "
+            f"{'true' if s.DB else 'false'}, {amode}, "
             f"{gv}, {cin}, {1 if out_f32 else 0}, {int(lo)}, {epi}, {1 if depthwise else 0}, {winty}>")
     return name, (
         f'extern "C" __global__ __launch_bounds__({nt}) void {name}(\n'

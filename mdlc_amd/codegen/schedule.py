@@ -156,7 +156,8 @@ def default_schedule(M: int, N: int, K: int) -> MfmaSchedule:
 # ----- int8 schedules ---------------------------------------------------------
 # The same MfmaSchedule fields describe the int8 kernel, with BK counted in
 # bytes: MS = 32 selects v_mfma_i32_32x32x32_i8 (32 k per instruction), MS = 16
-# v_mfma_i32_16x16x64_i8 (64 k); LDS rows are BK + 16 bytes, double buffered.
+# v_mfma_i32_16x16x64_i8 (64 k); LDS rows are BK + 16 bytes, double buffered
+# (DB) or single buffered.
 
 def qsched_valid(s: MfmaSchedule) -> bool:
     if s.MS not in (16, 32) or s.SK != 1:
@@ -170,7 +171,7 @@ def qsched_valid(s: MfmaSchedule) -> bool:
     nt = s.threads_per_block()
     if nt > 1024 or nt % (s.BK // 16):
         return False
-    if 2 * (s.BM + s.BN) * (s.BK + 16) > LDS_LIMIT or s.acc_regs() > MAX_QACC_REGS:
+    if (2 if s.DB else 1) * (s.BM + s.BN) * (s.BK + 16) > LDS_LIMIT or s.acc_regs() > MAX_QACC_REGS:
         return False
     return True
 
@@ -215,9 +216,10 @@ def qdw_search_space():
 def qgemm_search_space():
     for bm in (32, 64, 128, 256):
         for bn in (32, 64, 128, 256):
-            for bk in (64, 128):
+            for bk in (64, 128, 256):
                 for wgm, wgn in ((1, 1), (2, 1), (1, 2), (2, 2), (4, 1), (1, 4), (4, 2), (2, 4)):
                     for ms in (32, 16):
-                        s = MfmaSchedule(bm, bn, bk, wgm, wgn, ms, True, 1)
-                        if qsched_valid(s):
-                            yield s
+                        for db in (True, False):
+                            s = MfmaSchedule(bm, bn, bk, wgm, wgn, ms, db, 1)
+                            if qsched_valid(s):
+                                yield s

@@ -95,7 +95,8 @@ class _Fixed:
 QSCHEDULES = [MfmaSchedule(256, 256, 128, 4, 2, 32, True),   # two register sets in flight
               MfmaSchedule(256, 256, 64, 2, 2, 32, True),    # 256 accumulators, one set
               MfmaSchedule(128, 64, 128, 2, 1, 16, True),
-              MfmaSchedule(32, 32, 64, 1, 1, 32, True)]
+              MfmaSchedule(32, 32, 64, 1, 1, 32, True),
+              MfmaSchedule(128, 128, 256, 2, 2, 16, False)]  # single LDS buffer, 256-byte K tiles
 
 
 @pytest.mark.parametrize("sched", QSCHEDULES, ids=lambda s: s.key())
