@@ -273,8 +273,12 @@ class HipCodegen(Int8LoweringMixin):
         kname = self._kernel(sig, lambda i: T.gemm_kernel(
             f"{tag}_{sched.key()}_SK_{i}", sched, with_bias=False, bmode=bmode, vec_a=vec_a,
             win=win))
+        # the partial kernel reads the operands and writes every slice's sums;
+        # bias, residual and the output belong to the reduce launch
+        extra_bytes = 4 * (M * N * (1 + len(extra)) + (M if epi["bias_mode"] == "row" else N) * len(bias))
         self.plan.append(Launch(kind, kname, list(operands), [ws], (tiles * slices, 1, 1), block,
-                                dict(meta, partial=True)))
+                                dict(meta, partial=True,
+                                     bytes=meta["bytes"] - extra_bytes + 4 * slices * M * N)))
         rsig = ("splitk_reduce", bool(bias), epi["bias_mode"], epi["act_sig"], epi["alpha"], epi["beta"],
                 residual)
         rname = self._kernel(rsig, lambda i: T.splitk_reduce_kernel(
