@@ -16,7 +16,7 @@ import numpy as np
 from mdlc_amd.codegen.hip import templates as T
 from mdlc_amd.codegen.hip.plan import Launch, round16
 from mdlc_amd.codegen.schedule import (
-    default_qdw_schedule, default_qschedule, qdw_valid, qsched_valid,
+    default_qdw_schedule, default_qschedule, qdw_valid, qmlp_layout, qsched_valid,
 )
 from mdlc_amd.passes.shape_inference import conv_geometry
 
@@ -196,6 +196,63 @@ class Int8LoweringMixin:
                 "depthwise_ops": 2 * P * C * KH * KW}
         self._emit_qgemm(node, sched, x, wdev, b, m, y, meta, amode=1, out_f32=False, lo=lo, win=win,
                          gv=16, depthwise=True)
+
+    def _padded_vector(self, g, name, n, dtype):
+        """A constant per-channel vector packed zero padded to a multiple of 16."""
+        n16 = round16(n)
+        out = np.zeros(n16, dtype)
+        out[:n] = np.asarray(g.initializers[name], dtype).ravel()
+        return self._pack_raw(f"{name}__dev{n16}", out)
+
+    def _lower_qmlp(self, g, node):
+        """The fused channel mixer: h = T[q1(x W1^T + b1)], y = qadd(x, q2(h W2^T + b2)),
+        both GEMMs over the NHWC rows of x in one launch (``qmlp_i8``)."""
+        x, w1, b1, m1, tab, w2, b2, m2 = node.inputs
+        if self.layout.get(x) != "NHWC":
+            raise NotImplementedError("HIP codegen: QMlp input must come from the int8 path")
+        n, C, H, W = self._shape(g, x)
+        M = n * H * W
+        W1 = np.asarray(g.initializers[w1], np.int8)
+        W2 = np.asarray(g.initializers[w2], np.int8)
+        E = W1.shape[0]
+        if W1.reshape(E, -1).shape[1] != C or W2.reshape(W2.shape[0], -1).shape != (C, E):
+            raise ValueError("QMlp weights do not match the input's channels")
+        if np.asarray(g.initializers[tab]).size != 256:
+            raise NotImplementedError("HIP codegen: QMlp needs a constant 256-entry table")
+        lay = self._qmlp_layout(node, C, E, M)
+        if lay is None:
+            raise NotImplementedError(f"HIP codegen: no fused MLP tiling for C={C}, E={E}")
+        if M * C >= 2 ** 31 - 2 ** 20:
+            raise NotImplementedError("HIP codegen: int8 MLP operand of 2 GiB or more")
+        self._check_dtype(g, x, "int8")
+        y = node.outputs[0]
+        self._check_dtype(g, y, "int8")
+        self.layout[y] = "NHWC"
+        CP, EP = -(-C // 64) * 64, -(-E // 64) * 64
+        w1p = np.zeros((E, CP), np.int8)
+        w1p[:, :C] = W1.reshape(E, C)
+        w2p = np.zeros((C, EP), np.int8)
+        w2p[:, :E] = W2.reshape(C, E)
+        ins = [x, self._pack_raw(f"{w1}__dev_mlp{CP}", w1p), self._padded_vector(g, b1, E, np.int32),
+               self._padded_vector(g, m1, E, np.float32), tab,
+               self._pack_raw(f"{w2}__dev_mlp{EP}", w2p), self._padded_vector(g, b2, C, np.int32),
+               self._padded_vector(g, m2, C, np.float32)]
+        lo1 = 0 if node.attrs.get("activation1") == "Relu" else -127
+        lo2 = 0 if node.attrs.get("activation2") == "Relu" else -127
+        kname = self._kernel(("qmlp", C, E, lay, lo1, lo2), lambda i: T.qmlp_kernel(
+            f"qmlp_c{C}_e{E}_{lay.key()}_{i}", C, E, lay, lo1=lo1, lo2=lo2))
+        self.plan.append(Launch(
+            "qmlp", kname, ins, [y], (-(-M // lay.BM), 1, 1), (256, 1, 1),
+            {"M": M, "C": C, "E": E, "layout": lay, "node": node,
+             "res_mult": float(node.attrs["res_mult"]), "acc_mult": float(node.attrs["acc_mult"]),
+             "ops": 4 * M * C * E,
+             # algorithmic HBM bytes: x once, y once, both weights, bias and mult
+             "bytes": 2 * M * C + 2 * C * E + 8 * (C + E) + 256}))
+
+    def _qmlp_layout(self, node, C, E, M):
+        fn = getattr(self.schedule_fn, "qmlp_layout", None)
+        lay = fn(C, E, M) if fn is not None else None
+        return lay if lay is not None else qmlp_layout(C, E, M)
 
     def _lower_qgemm(self, g, node):
         x, w, b, m = node.inputs[:4]

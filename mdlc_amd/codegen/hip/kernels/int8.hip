@@ -522,6 +522,153 @@ __device__ __forceinline__ void qgap_nhwc(const i8* __restrict__ x, i8* __restri
   y[i] = requant(s, m, -127.0f);
 }
 
+// Fused int8 channel mixer over channels-last rows:
+//
+//   h = table[q1(X W1^T + b1)]          [M][E], kept in LDS
+//   Y = qadd(X, q2(h W2^T + b2))        [M][C]
+//
+// with q1/q2 the requantization of a QConv (lower clamps LO1/LO2) and qadd
+// the residual add (res_mult on X, acc_mult on the codes), i.e. two 1x1
+// QConvs with their fused lookup and residual epilogues in one launch: the
+// hidden tensor never goes to HBM and X is read once (the residual comes
+// from the LDS copy). Weights are [E][CP] and [C][EP], K zero padded to a
+// multiple of 64 (CP, EP), so whatever sits in the padded K columns of the
+// LDS tiles is multiplied by zero.
+//
+// A workgroup of 4 waves owns BM rows. Each GEMM puts its waves on a
+// WGM x WGN grid: a wave owns BM/WGM rows and, per column chunk, NI blocks
+// of 16 columns; the chunks step over the output columns. A fragments come
+// from the LDS tiles, B fragments (weight rows, 16 contiguous K bytes per
+// lane) straight from global memory: the weights are small and L2 resident.
+// MFMA v_mfma_i32_16x16x64_i8 with the weight fragment as the row operand,
+// so a lane ends with 4 consecutive output columns of one row.
+struct QMlpArgs {
+  const i8* __restrict__ X;        // [M][C]
+  const i8* __restrict__ W1;       // [E][CP]
+  const int* __restrict__ b1;      // [E]
+  const float* __restrict__ m1;    // [E]
+  const i8* __restrict__ table;    // [256]
+  const i8* __restrict__ W2;       // [C][EP]
+  const int* __restrict__ b2;      // [C]
+  const float* __restrict__ m2;    // [C]
+  i8* __restrict__ Y;              // [M][C]
+  int M;
+  float res_mult, acc_mult;
+};
+
+template <int NK, int LDB, int NI>
+struct QMlpFrags {                   // B fragments of one column chunk, whole K
+  intx4 f[NK / 64][NI];
+  __device__ __forceinline__ void load(const i8* __restrict__ Bg, int col0) {
+    const int lane = threadIdx.x & 63;
+    const int li = lane & 15, lk = lane >> 4;
+#pragma unroll
+    for (int s = 0; s < NK / 64; ++s)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+        f[s][ni] = *reinterpret_cast<const intx4*>(Bg + (size_t)(col0 + ni * 16 + li) * LDB + s * 64 + lk * 16);
+  }
+};
+
+template <int WGN, int NI>
+__device__ __forceinline__ int qmlp_col0(int c0) { return c0 + ((threadIdx.x >> 6) % WGN) * NI * 16; }
+
+template <int NK, int LDA, int LDB, int NCOLS, int BM, int WGM, int WGN, int NI, class Epi, class Hook>
+__device__ __forceinline__ void qmlp_gemm(const i8* __restrict__ As, const i8* __restrict__ Bg,
+                                          const QMlpFrags<NK, LDB, NI>& first, Epi epi, Hook hook) {
+  constexpr int MI = BM / WGM / 16;
+  constexpr int CHUNK = WGN * NI * 16;
+  static_assert(NCOLS % CHUNK == 0 && (BM / WGM) % 16 == 0, "column chunks must tile the output");
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15, lk = lane >> 4;
+  const int r0 = (wave / WGN) * (BM / WGM);
+#pragma unroll
+  for (int c0 = 0; c0 < NCOLS; c0 += CHUNK) {
+    const int col0 = qmlp_col0<WGN, NI>(c0);
+    QMlpFrags<NK, LDB, NI> fr;
+    if (c0 == 0) fr = first; else fr.load(Bg, col0);
+    intx4 acc[MI][NI];
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = intx4{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < NK / 64; ++s) {
+      intx4 af[MI];
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+        af[mi] = *reinterpret_cast<const intx4*>(As + (r0 + mi * 16 + li) * LDA + s * 64 + lk * 16);
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni)
+          acc[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fr.f[s][ni], af[mi], acc[mi][ni], 0, 0, 0);
+    }
+    if (c0 + CHUNK >= NCOLS) hook();
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi) epi(r0 + mi * 16 + li, col0 + ni * 16 + lk * 4, acc[mi][ni]);
+  }
+}
+
+template <int C, int E, int BM, int WGM1, int WGN1, int NI1, int WGM2, int WGN2, int NI2, int LO1,
+          int LO2>
+__device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
+  constexpr int CP = (C + 63) / 64 * 64, EP = (E + 63) / 64 * 64;
+  constexpr int XS = CP + 16, HS = EP + 16;    // LDS row strides (bytes)
+  constexpr int NT = 256;
+  static_assert(C % 16 == 0 && E % 16 == 0, "channel counts must be multiples of 16");
+  __shared__ __attribute__((aligned(16))) i8 Xs[BM * XS];
+  __shared__ __attribute__((aligned(16))) i8 Hs[BM * HS];
+  __shared__ i8 tab[256];
+  const int tid = threadIdx.x;
+  const int m0 = blockIdx.x * BM;
+
+  // the first weight chunk is fetched while the X tile comes in
+  QMlpFrags<CP, CP, NI1> w1f;
+  w1f.load(g.W1, qmlp_col0<WGN1, NI1>(0));
+  const __amdgpu_buffer_rsrc_t rX = buffer_over(g.X, g.M * C);
+  constexpr int CPR = CP / 16;
+#pragma unroll
+  for (int i = tid; i < BM * CPR; i += NT) {
+    const int r = i / CPR, j = i - (i / CPR) * CPR;
+    const int off = (m0 + r < g.M && j * 16 < C) ? (m0 + r) * C + j * 16 : kOutside;
+    *reinterpret_cast<intx4*>(&Xs[r * XS + j * 16]) =
+        __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rX, off, 0, 0));
+  }
+  tab[tid] = g.table[tid];
+  __syncthreads();
+
+  QMlpFrags<EP, EP, NI2> w2f;
+  qmlp_gemm<CP, XS, CP, E, BM, WGM1, WGN1, NI1>(Xs, g.W1, w1f, [&](int r, int n, const intx4& acc) {
+    const intx4 bv = *reinterpret_cast<const intx4*>(g.b1 + n);
+    const floatx4 mv = *reinterpret_cast<const floatx4*>(g.m1 + n);
+    union { int w; i8 b[4]; } o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.b[j] = tab[(int)requant(acc[j] + bv[j], mv[j], (float)LO1) + 128];
+    *reinterpret_cast<int*>(&Hs[r * HS + n]) = o.w;
+  }, [&]() { w2f.load(g.W2, qmlp_col0<WGN2, NI2>(0)); });
+  __syncthreads();
+
+  qmlp_gemm<EP, HS, EP, C, BM, WGM2, WGN2, NI2>(Hs, g.W2, w2f, [&](int r, int n, const intx4& acc) {
+    const int m = m0 + r;
+    if (m >= g.M) return;
+    const intx4 bv = *reinterpret_cast<const intx4*>(g.b2 + n);
+    const floatx4 mv = *reinterpret_cast<const floatx4*>(g.m2 + n);
+    union { int w; i8 b[4]; } x, o;
+    x.w = *reinterpret_cast<const int*>(&Xs[r * XS + n]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const i8 code = requant(acc[j] + bv[j], mv[j], (float)LO2);
+      const float v = (float)x.b[j] * g.res_mult + (float)code * g.acc_mult;
+      o.b[j] = (i8)(int)fminf(fmaxf(rintf(v), -127.0f), 127.0f);
+    }
+    *reinterpret_cast<int*>(g.Y + (size_t)m * C + n) = o.w;
+  }, [] {});
+}
+
 // Dequantize: float(q) * s; an NHWC 4-D input is written back as NCHW.
 __device__ __forceinline__ void dequantize_i8(const i8* __restrict__ x, float* __restrict__ y,
                                               long long n, int C, int HW, float s) {

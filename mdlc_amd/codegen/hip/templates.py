@@ -392,6 +392,23 @@ def qgemm_kernel(name: str, sched: MfmaSchedule, *, amode: int, out_f32: bool, l
         f"  {tmpl}(g);\n}}\n")
 
 
+def qmlp_kernel(name: str, C: int, E: int, layout, *, lo1: int, lo2: int) -> tuple:
+    """Fused int8 channel mixer (two 1x1 QConvs, lookup, residual add) over
+    channels-last rows; ``layout`` is a ``QMlpLayout``.
+    ABI: (X, W1, b1, m1, table, W2, b2, m2, Y, int M, float res_mult,
+    float acc_mult)."""
+    args = (C, E, layout.BM) + tuple(layout.g1) + tuple(layout.g2) + (int(lo1), int(lo2))
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const signed char* __restrict__ X, const signed char* __restrict__ W1,\n"
+        "    const int* __restrict__ b1, const float* __restrict__ m1,\n"
+        "    const signed char* __restrict__ table, const signed char* __restrict__ W2,\n"
+        "    const int* __restrict__ b2, const float* __restrict__ m2, signed char* __restrict__ Y,\n"
+        "    int M, float res_mult, float acc_mult) {\n"
+        "  mdlc::QMlpArgs g{X, W1, b1, m1, table, W2, b2, m2, Y, M, res_mult, acc_mult};\n"
+        f"  mdlc::qmlp_i8<{', '.join(str(v) for v in args)}>(g);\n}}\n")
+
+
 def qdwconv_kernel(name: str, win: tuple, *, cv: int, lo: int) -> tuple:
     """int8 depthwise conv over NHWC. ``win`` = (KH, KW, SH, SW, DH, DW).
     ABI: (x, w, bias, mult, y, int N, int C, int H, int W, int OH, int OW, int PT, int PL)."""

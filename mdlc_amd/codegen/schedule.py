@@ -21,7 +21,7 @@ cross product of a few proven values, as in the reference.
 from __future__ import annotations
 
 from dataclasses import asdict, dataclass
-from typing import Iterator
+from typing import Iterator, Optional
 
 LDS_LIMIT = 160 * 1024         # bytes one workgroup may allocate (gfx950: 160 KB per CU)
 MAX_ACC_REGS = 128             # fp32 accumulator registers per lane we allow
@@ -223,3 +223,64 @@ def qgemm_search_space():
                             s = MfmaSchedule(bm, bn, bk, wgm, wgn, ms, db, 1)
                             if qsched_valid(s):
                                 yield s
+
+
+# ----- the fused int8 channel-mixer kernel (QMlp) -------------------------------
+
+@dataclass(frozen=True)
+class QMlpLayout:
+    """Tiling of the fused int8 MLP kernel: BM rows per 4-wave workgroup and,
+    for each of its two GEMMs, a (WGM, WGN) wave grid with NI blocks of 16
+    columns per wave per column chunk (g1: the hidden E columns, g2: the C
+    output columns)."""
+    BM: int
+    g1: tuple
+    g2: tuple
+
+    def key(self) -> str:
+        return "BM%d_%dx%dn%d_%dx%dn%d" % ((self.BM,) + tuple(self.g1) + tuple(self.g2))
+
+
+def _round64(n: int) -> int:
+    return -(-int(n) // 64) * 64
+
+
+def qmlp_grid(ncols: int, k: int, bm: int) -> Optional[tuple]:
+    """(WGM, WGN, NI) for one GEMM of the fused MLP: the widest wave grid
+    along the columns that tiles (ncols, bm), then the largest NI whose B
+    fragments for the whole K (16 bytes per lane per 64 K) stay within 96
+    registers, with at most 12 accumulator blocks per wave."""
+    ks = _round64(k) // 64
+    for wgn in (4, 2, 1):
+        wgm = 4 // wgn
+        if ncols % (16 * wgn) or bm % (16 * wgm):
+            continue
+        blocks = ncols // (16 * wgn)
+        mi = bm // wgm // 16
+        for ni in range(blocks, 0, -1):
+            if blocks % ni == 0 and ni * ks * 4 <= 96 and mi * ni <= 12:
+                return (wgm, wgn, ni)
+    return None
+
+
+def qmlp_lds_bytes(C: int, E: int, bm: int) -> int:
+    return bm * (_round64(C) + 16 + _round64(E) + 16) + 256
+
+
+def qmlp_layout(C: int, E: int, M: int, bm: Optional[int] = None) -> Optional[QMlpLayout]:
+    """The default tiling: 64-row workgroups when that still gives one per
+    CU, else 32 rows when that gives 128, else 16 — or the next larger row
+    count that tiles both GEMMs; ``bm`` forces one. None when the channel
+    counts admit no tiling (C and E must be multiples of 16)."""
+    if C % 16 or E % 16:
+        return None
+    if bm is None:
+        first = 64 if M >= 64 * CUS else (32 if M >= 32 * 128 else 16)
+        rows = [r for r in (16, 32, 64) if r >= first]
+    else:
+        rows = [bm]
+    for r in rows:
+        g1, g2 = qmlp_grid(E, C, r), qmlp_grid(C, E, r)
+        if g1 is not None and g2 is not None and qmlp_lds_bytes(C, E, r) <= LDS_LIMIT:
+            return QMlpLayout(r, g1, g2)
+    return None

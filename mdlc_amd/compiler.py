@@ -18,6 +18,7 @@ from mdlc_amd.ir import Graph, verify_graph
 from mdlc_amd.passes import default_pipeline
 from mdlc_amd.passes.base import PassManager
 from mdlc_amd.passes.fuse_quant_epilogue import FuseQuantEpilogue
+from mdlc_amd.passes.fuse_quant_mlp import FuseQuantMlp
 from mdlc_amd.passes.fuse_residual import FuseResidualEpilogue
 from mdlc_amd.passes.shape_inference import infer_shapes, make_dummy_feeds
 from mdlc_amd.runtime.memory_planner import MemoryPlan, plan_memory
@@ -56,24 +57,29 @@ def _structural_verifier(extra: Optional[Callable]) -> Callable:
 def compile_graph(graph: Graph, *, batch: int = 1, feeds: Optional[dict] = None,
                   schedule_fn=None, verify: Optional[Callable] = None,
                   conv_mode: str = "implicit", fuse_int8_epilogues: bool = True,
-                  int8_depthwise: str = "mfma", fuse_residual: bool = True) -> Compiled:
+                  int8_depthwise: str = "mfma", fuse_residual: bool = True,
+                  fuse_int8_mlp=True) -> Compiled:
     """Optimize, plan and lower ``graph``. The reference pipeline runs first,
     unchanged. Then backend epilogue folds: ``fuse_int8_epilogues`` folds a
     QLut or QAdd into the QConv that feeds it; ``fuse_residual`` folds a
     float residual add (and the pointwise ops after it) into the conv that
-    feeds it. ``int8_depthwise`` picks the int8 depthwise kernel ("mfma" or
-    "vector")."""
+    feeds it; ``fuse_int8_mlp`` (with the int8 folds) turns a 1x1 QConv +
+    lookup followed by a 1x1 QConv + residual add of the first's input into
+    one ``QMlp`` node where that pays ("always": wherever the kernel tiles). ``int8_depthwise`` picks the int8 depthwise kernel
+    ("mfma" or "vector")."""
     original = graph.clone()
     if feeds is None:
         feeds = make_dummy_feeds(graph, batch=batch)
     pm = default_pipeline(verify=_structural_verifier(verify))
-    if fuse_int8_epilogues and any(n.op_type == "QConv" for n in graph.nodes):
+    quant = fuse_int8_epilogues and any(n.op_type == "QConv" for n in graph.nodes)
+    if quant:
         pm.add(FuseQuantEpilogue())
     graph = pm.run(graph)
     infer_shapes(graph, feeds)
-    if fuse_residual:
-        PassManager([FuseResidualEpilogue()], verify=_structural_verifier(verify),
-                    history=pm.history).run(graph)
+    post = ([FuseResidualEpilogue()] if fuse_residual else []) + \
+        ([FuseQuantMlp(always=fuse_int8_mlp == "always")] if quant and fuse_int8_mlp else [])
+    if post:
+        PassManager(post, verify=_structural_verifier(verify), history=pm.history).run(graph)
     mem_plan = plan_memory(graph)
     module = emit_hip_module(graph, schedule_fn, conv_mode=conv_mode, int8_depthwise=int8_depthwise)
     return Compiled(original, graph, module, mem_plan, pm, feeds)

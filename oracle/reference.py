@@ -198,6 +198,16 @@ class ReferenceExecutor:
             if a.get("epilogue") == "add":
                 return [quant.qadd(ins[4], q, a["res_mult"], a["acc_mult"])]
             return [q]
+        if op == "QMlp":
+            # the composition it folds: QConv 1x1 + lookup, then QConv 1x1 +
+            # residual add of the first conv's input
+            one = dict(strides=[1, 1], pads=[0, 0, 0, 0], dilations=[1, 1], group=1)
+            lo1 = 0 if a.get("activation1") == "Relu" else quant.QMIN
+            lo2 = 0 if a.get("activation2") == "Relu" else quant.QMIN
+            h = quant.lut(quant.requant(quant.conv_acc(ins[0], ins[1], ins[2], **one),
+                                        ins[3].reshape(1, -1, 1, 1), lo1), ins[4])
+            q = quant.requant(quant.conv_acc(h, ins[5], ins[6], **one), ins[7].reshape(1, -1, 1, 1), lo2)
+            return [quant.qadd(ins[0], q, a["res_mult"], a["acc_mult"])]
         if op == "QGemm":
             acc = quant.gemm_acc(ins[0], ins[1], opt(2))
             if a.get("out_dtype", "int8") == "float32":

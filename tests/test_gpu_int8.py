@@ -161,28 +161,99 @@ def test_qadd_qlut_qgap(hip_ctx):
     assert np.mean(np.abs(got["s"].astype(int)) == 127) > 0.01          # clamp path exercised
 
 
-@pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
+@pytest.mark.parametrize("mode", ["mlp", "epilogues", "unfused"])
 @pytest.mark.parametrize("batch", [2, 32])
-def test_repvit_int8_every_tensor_bit_exact(batch, fused, hip_ctx):
+def test_repvit_int8_every_tensor_bit_exact(batch, mode, hip_ctx):
     """Every int8 tensor the module materializes, and the logits, equal the
-    oracle's — with the GELU lookups and residual adds folded into the conv
-    epilogues and the depthwise convs on the matrix cores, and with neither
-    (separate lookup/add launches, vector depthwise kernel)."""
+    oracle's — with the channel mixers as fused MLP launches, with the GELU
+    lookups and residual adds folded into the conv epilogues, and with
+    neither (separate lookup/add launches, vector depthwise kernel)."""
     g = build_repvit_int8(batch=batch)
     feeds = {"input": make_input(batch)}
-    c, got, want = device_run(g, feeds, ctx=hip_ctx, all_tensors=True, fuse_int8_epilogues=fused,
-                              int8_depthwise="mfma" if fused else "vector")
+    c, got, want = device_run(g, feeds, ctx=hip_ctx, all_tensors=True,
+                              fuse_int8_epilogues=mode != "unfused", fuse_int8_mlp=mode == "mlp",
+                              int8_depthwise="vector" if mode == "unfused" else "mfma")
     assert c.module.fallbacks() == []
+    nq = sum(l.kind == "qmlp" for l in c.module.plan)
+    assert nq == ({2: 6, 32: 21}[batch] if mode == "mlp" else 0)
     epis = [l.meta.get("epilogue", 0) for l in c.module.plan if l.kind == "qgemm"]
-    assert (epis.count(1), epis.count(2)) == ((24, 23) if fused else (0, 0))
+    want_epis = (0, 0) if mode == "unfused" else (24 - nq, 23 - nq)
+    assert (epis.count(1), epis.count(2)) == want_epis
     n = 0
     for name, v in got.items():
         w = want[name]
         if w.dtype == np.int8:
             np.testing.assert_array_equal(v, w, err_msg=name)
             n += 1
-    assert n >= (70 if fused else 120)
+    assert n >= {"mlp": 50, "epilogues": 70, "unfused": 120}[mode]
     np.testing.assert_array_equal(got["logits"], want["logits"])
+
+
+def _mlp_graph(n, c, e, hw, *, relu1=False, relu2=False, seed=3):
+    """Quantize -> 1x1 QConv c->e -> QLut -> 1x1 QConv e->c -> QAdd(xq, .):
+    a RepViT channel mixer with random weights, table and multipliers sized
+    to keep the codes away from the clamps."""
+    rng = np.random.default_rng(seed)
+    b = GraphBuilder("mlp")
+    b.input("x", (n, c, hw, hw))
+    b.node("QuantizeLinear", ["x"], "xq", inv_scale=20.0)
+    b.const("w1", rng.integers(-127, 128, (e, c, 1, 1)).astype(np.int8))
+    b.const("b1", rng.integers(-3000, 3000, e).astype(np.int32))
+    b.const("m1", (rng.uniform(0.5, 1.5, e) * 0.01 / np.sqrt(c)).astype(np.float32))
+    b.const("t", rng.integers(-127, 128, 256).astype(np.int8))
+    b.const("w2", rng.integers(-127, 128, (c, e, 1, 1)).astype(np.int8))
+    b.const("b2", rng.integers(-3000, 3000, c).astype(np.int32))
+    b.const("m2", (rng.uniform(0.5, 1.5, c) * 0.0075 / np.sqrt(e)).astype(np.float32))
+    one = dict(kernel_shape=[1, 1], strides=[1, 1], pads=[0] * 4)
+    b.node("QConv", ["xq", "w1", "b1", "m1"], "h0", **one, **({"activation": "Relu"} if relu1 else {}))
+    b.node("QLut", ["h0", "t"], "h")
+    b.node("QConv", ["h", "w2", "b2", "m2"], "y0", **one, **({"activation": "Relu"} if relu2 else {}))
+    b.node("QAdd", ["xq", "y0"], "y", ma=0.6, mb=0.35)
+    b.output("y")
+    return b.graph(), {"x": (rng.standard_normal((n, c, hw, hw)) * 3).astype(np.float32)}
+
+
+class _MlpRows:
+    """A schedule source that forces the fused MLP kernel's rows per workgroup."""
+
+    def __init__(self, bm):
+        self.bm = bm
+
+    def qmlp_layout(self, C, E, M):
+        from mdlc_amd.codegen.schedule import qmlp_layout
+        return qmlp_layout(C, E, M, bm=self.bm)
+
+    def __call__(self, node, mnk):
+        from mdlc_amd.codegen.schedule import default_qschedule
+        return default_qschedule(*mnk)
+
+
+@pytest.mark.parametrize("bm", [None, 16, 32, 64])
+@pytest.mark.parametrize("case", [(2, 48, 96, 14, False, False), (2, 96, 192, 9, False, False),
+                                  (1, 192, 384, 7, False, False), (2, 384, 768, 7, False, False),
+                                  (1, 32, 64, 5, True, False), (3, 48, 160, 5, False, True),
+                                  (2, 64, 128, 6, True, True)],
+                         ids=lambda c: "n{}c{}e{}hw{}{}{}".format(*c[:4], "_relu1" if c[4] else "",
+                                                               "_relu2" if c[5] else ""))
+def test_qmlp_bit_exact(case, bm, hip_ctx):
+    """The fused channel mixer equals the oracle and the two-conv launches it
+    replaces bit for bit: RepViT's four stage widths, K padding on either
+    GEMM (C = 32, E = 160), ReLU clamps, row tails, each row tiling."""
+    from mdlc_amd.codegen.schedule import qmlp_layout
+
+    n, c, e, hw, r1, r2 = case
+    if bm is not None and qmlp_layout(c, e, n * hw * hw, bm=bm) is None:
+        pytest.skip(f"no {bm}-row tiling for C={c}, E={e}")
+    g, feeds = _mlp_graph(n, c, e, hw, relu1=r1, relu2=r2)
+    fn = None if bm is None else _MlpRows(bm)
+    cmod, got, want = device_run(g, feeds, ctx=hip_ctx, schedule_fn=fn, fuse_int8_mlp="always")
+    assert [l.kind for l in cmod.module.plan] == ["quantize", "qmlp"]
+    np.testing.assert_array_equal(got["y"], want["y"])
+    v = want["y"].astype(int)
+    assert v.std() > 3 and np.mean(np.abs(v) == 127) < 0.5
+    g2, _ = _mlp_graph(n, c, e, hw, relu1=r1, relu2=r2)
+    _, got2, _ = device_run(g2, feeds, ctx=hip_ctx, fuse_int8_mlp=False)
+    np.testing.assert_array_equal(got["y"], got2["y"])
 
 
 def _qconv_epilogue_graph(n, c, hw, oc, k, epilogue, *, res_first, seed=5):

@@ -9,6 +9,8 @@ import numpy as np
 from mdlc_amd.compiler import compile_graph
 from mdlc_amd.ir import verify_graph
 from mdlc_amd.passes.fuse_quant_epilogue import FuseQuantEpilogue
+from mdlc_amd.passes.fuse_quant_mlp import FuseQuantMlp
+from mdlc_amd.passes.shape_inference import infer_shapes
 from mdlc_amd.tools.build_repvit_int8 import build_repvit_int8, make_input
 from mdlc_amd.tools.graph_builder import GraphBuilder
 from oracle.reference import run_reference
@@ -23,7 +25,7 @@ def test_repvit_lookups_and_adds_fold_into_convs():
     ops = [n.op_type for n in g.nodes]
     n_lut, n_add = ops.count("QLut"), ops.count("QAdd")
     assert (n_lut, n_add) == (24, 23)
-    c = compile_graph(g, feeds={"input": make_input(1)})
+    c = compile_graph(g, feeds={"input": make_input(1)}, fuse_int8_mlp=False)
     hist = c.graph.op_histogram()
     assert "QLut" not in hist and "QAdd" not in hist
     epis = [n.attrs.get("epilogue") for n in c.graph.nodes if n.op_type == "QConv"]
@@ -102,3 +104,82 @@ def test_add_multipliers_follow_operand_order():
     (conv,) = [n for n in g.nodes if n.op_type == "QConv"]
     assert conv.inputs[4] == "xq"
     assert conv.attrs["res_mult"] == 0.25 and conv.attrs["acc_mult"] == 0.75
+
+
+# ----- the channel-mixer fold (QConv+lut, QConv+add -> QMlp) -------------------
+
+def test_repvit_channel_mixers_fold_into_qmlp():
+    """At batch 32 the 21 channel mixers of stages 1-3 become one QMlp each;
+    stage 4's two, whose weights are large next to their 1568 rows, keep
+    their fused-epilogue convs; forced, all 23 fold."""
+    c = compile_graph(build_repvit_int8(batch=32), feeds={"input": make_input(32)})
+    hist = c.graph.op_histogram()
+    assert hist["QMlp"] == 21 and "QLut" not in hist and "QAdd" not in hist
+    epis = [n.attrs.get("epilogue") for n in c.graph.nodes if n.op_type == "QConv"]
+    assert epis.count("lut") == 3 and epis.count("add") == 2
+    ca = compile_graph(build_repvit_int8(batch=1), feeds={"input": make_input(1)},
+                       fuse_int8_mlp="always")
+    assert ca.graph.op_histogram()["QMlp"] == 23
+    for n in c.graph.nodes:
+        if n.op_type == "QMlp":
+            assert c.graph.info(n.outputs[0]).shape == c.graph.info(n.inputs[0]).shape
+            assert n.attrs["hidden"] not in {e for m in c.graph.nodes for e in m.inputs}
+    verify_graph(c.graph)
+
+
+def test_mlp_fold_equals_unfolded_everywhere():
+    feeds = {"input": make_input(2, image=64)}
+    cm = compile_graph(_small_repvit(), feeds=feeds)
+    ce = compile_graph(_small_repvit(), feeds=feeds, fuse_int8_mlp=False)
+    assert cm.graph.op_histogram()["QMlp"] == 3            # stages 1-2 at this size
+    a = run_reference(cm.graph, feeds, return_all=True)
+    b = run_reference(ce.graph, feeds, return_all=True)
+    common = [k for k in a if k in b and k not in cm.graph.initializers]
+    assert len(common) > 20 and "logits" in common
+    for k in common:
+        np.testing.assert_array_equal(a[k], b[k], err_msg=k)
+
+
+def _mlp(*, k1=1, hidden_use=False, other_residual=False, c=16, e=32):
+    """Quantize -> QConv(1x1, c->e) -> QLut -> QConv(1x1, e->c) -> QAdd(xq, .)."""
+    rng = np.random.default_rng(1)
+    b = GraphBuilder("mlp")
+    b.input("x", (1, c, 5, 5))
+    b.node("QuantizeLinear", ["x"], "xq", inv_scale=10.0)
+    b.node("QuantizeLinear", ["x"], "xr", inv_scale=12.0)
+    b.const("w1", rng.integers(-127, 128, (e, c, k1, k1)).astype(np.int8))
+    b.const("b1", rng.integers(-100, 100, e).astype(np.int32))
+    b.const("m1", np.full(e, 0.01, np.float32))
+    b.const("t", np.arange(-128, 128).clip(-127, 127)[::-1].copy().astype(np.int8))
+    b.const("w2", rng.integers(-127, 128, (c, e, 1, 1)).astype(np.int8))
+    b.const("b2", rng.integers(-100, 100, c).astype(np.int32))
+    b.const("m2", np.full(c, 0.005, np.float32))
+    p = (k1 - 1) // 2
+    b.node("QConv", ["xq", "w1", "b1", "m1"], "h0", kernel_shape=[k1, k1], strides=[1, 1], pads=[p] * 4)
+    b.node("QLut", ["h0", "t"], "h")
+    b.node("QConv", ["h", "w2", "b2", "m2"], "y0", kernel_shape=[1, 1], strides=[1, 1], pads=[0] * 4)
+    b.node("QAdd", ["xr" if other_residual else "xq", "y0"], "y", ma=0.5, mb=0.25)
+    b.output("y")
+    if hidden_use:
+        b.node("QLut", ["h", "t"], "h2")
+        b.output("h2")
+    g = b.graph()
+    FuseQuantEpilogue().run(g)
+    infer_shapes(g)
+    return g
+
+
+def test_mlp_fold_conditions():
+    g = _mlp()
+    assert FuseQuantMlp().run(g)
+    (node,) = [n for n in g.nodes if n.op_type == "QMlp"]
+    assert node.inputs == ["xq", "w1", "b1", "m1", "t", "w2", "b2", "m2"]
+    assert (node.attrs["res_mult"], node.attrs["acc_mult"]) == (0.5, 0.25)
+    x = np.random.default_rng(2).standard_normal((1, 16, 5, 5)).astype(np.float32) * 4
+    np.testing.assert_array_equal(run_reference(g, {"x": x})["y"], run_reference(_mlp(), {"x": x})["y"])
+    for kw in (dict(k1=3), dict(hidden_use=True), dict(other_residual=True), dict(c=24, e=40)):
+        g = _mlp(**kw)
+        assert not FuseQuantMlp().run(g), kw
+    # 25 rows against 2 * 64 * 128 weight bytes: only when forced
+    assert not FuseQuantMlp().run(_mlp(c=64, e=128))
+    assert FuseQuantMlp(always=True).run(_mlp(c=64, e=128))
