@@ -206,8 +206,10 @@ class Int8LoweringMixin:
 
     def _lower_qmlp(self, g, node):
         """The fused channel mixer: h = T[q1(x W1^T + b1)], y = qadd(x, q2(h W2^T + b2)),
-        both GEMMs over the NHWC rows of x in one launch (``qmlp_i8``)."""
-        x, w1, b1, m1, tab, w2, b2, m2 = node.inputs
+        both GEMMs over the NHWC rows of x in one launch (``qmlp_i8``); with a
+        token mixer, x = qdw(z) is computed in the same launch."""
+        mixer = node.attrs.get("mixer")
+        x, w1, b1, m1, tab, w2, b2, m2 = [node.inputs[0]] + list(node.inputs[4 if mixer else 1:])
         if self.layout.get(x) != "NHWC":
             raise NotImplementedError("HIP codegen: QMlp input must come from the int8 path")
         n, C, H, W = self._shape(g, x)
@@ -239,15 +241,36 @@ class Int8LoweringMixin:
                self._padded_vector(g, m2, C, np.float32)]
         lo1 = 0 if node.attrs.get("activation1") == "Relu" else -127
         lo2 = 0 if node.attrs.get("activation2") == "Relu" else -127
-        kname = self._kernel(("qmlp", C, E, lay, lo1, lo2), lambda i: T.qmlp_kernel(
-            f"qmlp_c{C}_e{E}_{lay.key()}_{i}", C, E, lay, lo1=lo1, lo2=lo2))
+        mix, ops, wbytes = None, 4 * M * C * E, 0
+        if mixer:
+            wd, bd, md = node.inputs[1:4]
+            kh, kw = mixer["kernel_shape"]
+            wdarr = np.asarray(g.initializers[wd], np.int8)
+            if wdarr.shape != (C, 1, kh, kw) or C % 16:
+                raise NotImplementedError("HIP codegen: QMlp token mixer must be depthwise over C % 16 == 0")
+            mix = (kh, kw, mixer["pads"][0], mixer["pads"][1],
+                   0 if mixer.get("activation") == "Relu" else -127)
+            # block-diagonal [C][KD]: k = (tap, channel within its 16-channel block)
+            taps = kh * kw
+            kd = -(-taps * 16 // 64) * 64
+            wbd = np.zeros((C, kd), np.int8)
+            ch = np.arange(C)
+            for t in range(taps):
+                wbd[ch, t * 16 + ch % 16] = wdarr.reshape(C, taps)[:, t]
+            ins[1:1] = [self._pack_raw(f"{wd}__dev_blockdiag{kd}", wbd),
+                        self._padded_vector(g, bd, C, np.int32), self._padded_vector(g, md, C, np.float32)]
+            ops += 2 * M * C * kh * kw
+            wbytes = C * (kh * kw + 8)
+        kname = self._kernel(("qmlp", C, E, lay, lo1, lo2, mix), lambda i: T.qmlp_kernel(
+            f"qmlp_c{C}_e{E}_{lay.key()}{'_dw%dx%d' % mix[:2] if mix else ''}_{i}", C, E, lay,
+            lo1=lo1, lo2=lo2, mixer=mix))
         self.plan.append(Launch(
             "qmlp", kname, ins, [y], (-(-M // lay.BM), 1, 1), (256, 1, 1),
-            {"M": M, "C": C, "E": E, "layout": lay, "node": node,
+            {"M": M, "C": C, "E": E, "H": H, "W": W, "layout": lay, "node": node, "mixer": bool(mix),
              "res_mult": float(node.attrs["res_mult"]), "acc_mult": float(node.attrs["acc_mult"]),
-             "ops": 4 * M * C * E,
-             # algorithmic HBM bytes: x once, y once, both weights, bias and mult
-             "bytes": 2 * M * C + 2 * C * E + 8 * (C + E) + 256}))
+             "ops": ops,
+             # algorithmic HBM bytes: x (or z) once, y once, the weights, bias and mult
+             "bytes": 2 * M * C + 2 * C * E + 8 * (C + E) + 256 + wbytes}))
 
     def _qmlp_layout(self, node, C, E, M):
         fn = getattr(self.schedule_fn, "qmlp_layout", None)

@@ -147,8 +147,11 @@ class HipExecutor:
             args += [I(m[f]) for f in ("M", "N", "K", "lda", "ldb", "ldc", "Cin", "H", "W", "OH", "OW")]
             args += [Arg.f32(m.get("res_mult", 0.0)), Arg.f32(m.get("acc_mult", 0.0))]
         elif k == "qmlp":
-            args = [P(e) for e in l.inputs] + [P(l.outputs[0]), I(m["M"]),
-                                               Arg.f32(m["res_mult"]), Arg.f32(m["acc_mult"])]
+            args = [P(e) for e in l.inputs]
+            if not m["mixer"]:                     # no token mixer: null Wd, bd, md
+                args[1:1] = [Arg.ptr(0)] * 3
+            args += [P(l.outputs[0]), I(m["M"]), I(m["H"]), I(m["W"]), Arg.f32(m["res_mult"]),
+                     Arg.f32(m["acc_mult"])]
         elif k == "qdwconv":
             args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
             args += [I(m[f]) for f in ("N", "C", "H", "W", "OH", "OW", "PT", "PL")]

@@ -533,7 +533,10 @@ __device__ __forceinline__ void qgap_nhwc(const i8* __restrict__ x, i8* __restri
 // hidden tensor never goes to HBM and X is read once (the residual comes
 // from the LDS copy). Weights are [E][CP] and [C][EP], K zero padded to a
 // multiple of 64 (CP, EP), so whatever sits in the padded K columns of the
-// LDS tiles is multiplied by zero.
+// LDS tiles is multiplied by zero. With MIX = 1 the X rows are themselves
+// computed in the prologue: a depthwise KHxKW stride-1 QConv (the block's
+// token mixer, lower clamp LOD) over the input Z, so X never goes to HBM
+// either.
 //
 // A workgroup of 4 waves owns BM rows. Each GEMM puts its waves on a
 // WGM x WGN grid: a wave owns BM/WGM rows and, per column chunk, NI blocks
@@ -543,7 +546,10 @@ __device__ __forceinline__ void qgap_nhwc(const i8* __restrict__ x, i8* __restri
 // MFMA v_mfma_i32_16x16x64_i8 with the weight fragment as the row operand,
 // so a lane ends with 4 consecutive output columns of one row.
 struct QMlpArgs {
-  const i8* __restrict__ X;        // [M][C]
+  const i8* __restrict__ X;        // [M][C]; with a token mixer its input Z [N][H][W][C]
+  const i8* __restrict__ Wd;       // token mixer: block-diagonal depthwise weights [C][KD]
+  const int* __restrict__ bd;      // [C]
+  const float* __restrict__ md;    // [C]
   const i8* __restrict__ W1;       // [E][CP]
   const int* __restrict__ b1;      // [E]
   const float* __restrict__ m1;    // [E]
@@ -552,9 +558,61 @@ struct QMlpArgs {
   const int* __restrict__ b2;      // [C]
   const float* __restrict__ m2;    // [C]
   i8* __restrict__ Y;              // [M][C]
-  int M;
+  int M, H, W;                     // rows; the token mixer's image size (stride 1, same size)
   float res_mult, acc_mult;
 };
+
+// Token mixer prologue: X rows [m0, m0 + BM) of a depthwise KHxKW stride-1
+// QConv over the NHWC input Z, requantized with (bd, md, LOD), written to the
+// LDS tile. It runs on the matrix cores as a block-diagonal GEMM per 16-row,
+// 16-channel tile: k = (tap, channel in the block), so a lane's 16-byte A
+// fragment is one tap's 16 channels of one pixel (loaded straight from Z,
+// zeros outside the image and past M) and Wd is packed [C][KD] with
+// Wd[n][tap*16 + n%16] = w[n][tap] and zeros elsewhere (KD = KH*KW*16
+// rounded up to 64). The int32 sums are exact, so this equals the unfused
+// depthwise conv bit for bit.
+template <int C, int BM, int XS, int KH, int KW, int PT, int PL, int LOD>
+__device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ Xs, int m0) {
+  constexpr int TAPS = KH * KW;
+  constexpr int KD = (TAPS * 16 + 63) / 64 * 64;
+  constexpr int CB = C / 16, TILES = (BM / 16) * CB;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15, lk = lane >> 4;
+  const int hw = g.H * g.W;
+  const __amdgpu_buffer_rsrc_t rZ = buffer_over(g.X, g.M * C);
+  for (int t = wave; t < TILES; t += 4) {
+    const int rb = t / CB, cb = t - (t / CB) * CB;
+    const int row = rb * 16 + li;
+    const int m = m0 + row;
+    int n = 0, oh = -(1 << 20), ow = 0;
+    if (m < g.M) {
+      n = m / hw;
+      const int s = m - n * hw;
+      oh = s / g.W;
+      ow = s - oh * g.W;
+    }
+    intx4 acc = intx4{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < KD / 64; ++s) {
+      const int tap = s * 4 + lk;
+      const int ih = oh - PT + tap / KW, iw = ow - PL + tap % KW;
+      const bool ok = tap < TAPS && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
+      const int off = ok ? ((n * g.H + ih) * g.W + iw) * C + cb * 16 : kOutside;
+      const intx4 a = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rZ, off, 0, 0));
+      const intx4 w = *reinterpret_cast<const intx4*>(g.Wd + (cb * 16 + li) * KD + s * 64 + lk * 16);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, a, acc, 0, 0, 0);
+    }
+    // acc[j]: row `row`, channel cb*16 + lk*4 + j
+    const int c = cb * 16 + lk * 4;
+    const intx4 bv = *reinterpret_cast<const intx4*>(g.bd + c);
+    const floatx4 mv = *reinterpret_cast<const floatx4*>(g.md + c);
+    union { int w; i8 b[4]; } o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.b[j] = requant(acc[j] + bv[j], mv[j], (float)LOD);
+    *reinterpret_cast<int*>(&Xs[row * XS + c]) = o.w;
+  }
+}
 
 template <int NK, int LDB, int NI>
 struct QMlpFrags {                   // B fragments of one column chunk, whole K
@@ -614,7 +672,7 @@ __device__ __forceinline__ void qmlp_gemm(const i8* __restrict__ As, const i8* _
 }
 
 template <int C, int E, int BM, int WGM1, int WGN1, int NI1, int WGM2, int WGN2, int NI2, int LO1,
-          int LO2>
+          int LO2, int MIX, int KH, int KW, int PT, int PL, int LOD>
 __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   constexpr int CP = (C + 63) / 64 * 64, EP = (E + 63) / 64 * 64;
   constexpr int XS = CP + 16, HS = EP + 16;    // LDS row strides (bytes)
@@ -629,14 +687,18 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   // the first weight chunk is fetched while the X tile comes in
   QMlpFrags<CP, CP, NI1> w1f;
   w1f.load(g.W1, qmlp_col0<WGN1, NI1>(0));
-  const __amdgpu_buffer_rsrc_t rX = buffer_over(g.X, g.M * C);
-  constexpr int CPR = CP / 16;
+  if constexpr (MIX) {
+    qmlp_mixer<C, BM, XS, KH, KW, PT, PL, LOD>(g, Xs, m0);
+  } else {
+    const __amdgpu_buffer_rsrc_t rX = buffer_over(g.X, g.M * C);
+    constexpr int CPR = CP / 16;
 #pragma unroll
-  for (int i = tid; i < BM * CPR; i += NT) {
-    const int r = i / CPR, j = i - (i / CPR) * CPR;
-    const int off = (m0 + r < g.M && j * 16 < C) ? (m0 + r) * C + j * 16 : kOutside;
-    *reinterpret_cast<intx4*>(&Xs[r * XS + j * 16]) =
-        __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rX, off, 0, 0));
+    for (int i = tid; i < BM * CPR; i += NT) {
+      const int r = i / CPR, j = i - (i / CPR) * CPR;
+      const int off = (m0 + r < g.M && j * 16 < C) ? (m0 + r) * C + j * 16 : kOutside;
+      *reinterpret_cast<intx4*>(&Xs[r * XS + j * 16]) =
+          __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rX, off, 0, 0));
+    }
   }
   tab[tid] = g.table[tid];
   __syncthreads();

@@ -392,20 +392,27 @@ def qgemm_kernel(name: str, sched: MfmaSchedule, *, amode: int, out_f32: bool, l
         f"  {tmpl}(g);\n}}\n")
 
 
-def qmlp_kernel(name: str, C: int, E: int, layout, *, lo1: int, lo2: int) -> tuple:
+def qmlp_kernel(name: str, C: int, E: int, layout, *, lo1: int, lo2: int,
+                mixer: Optional[tuple] = None) -> tuple:
     """Fused int8 channel mixer (two 1x1 QConvs, lookup, residual add) over
-    channels-last rows; ``layout`` is a ``QMlpLayout``.
-    ABI: (X, W1, b1, m1, table, W2, b2, m2, Y, int M, float res_mult,
-    float acc_mult)."""
-    args = (C, E, layout.BM) + tuple(layout.g1) + tuple(layout.g2) + (int(lo1), int(lo2))
+    channels-last rows; ``layout`` is a ``QMlpLayout``; ``mixer`` = (KH, KW,
+    PT, PL, LOD) adds the depthwise stride-1 token mixer that computes X
+    from the kernel's input.
+    ABI: (X or Z, Wd, bd, md, W1, b1, m1, table, W2, b2, m2, Y, int M,
+    int H, int W, float res_mult, float acc_mult)."""
+    mix = (1,) + tuple(int(v) for v in mixer) if mixer else (0, 1, 1, 0, 0, -127)
+    args = (C, E, layout.BM) + tuple(layout.g1) + tuple(layout.g2) + (int(lo1), int(lo2)) + mix
     return name, (
         f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
-        "    const signed char* __restrict__ X, const signed char* __restrict__ W1,\n"
-        "    const int* __restrict__ b1, const float* __restrict__ m1,\n"
-        "    const signed char* __restrict__ table, const signed char* __restrict__ W2,\n"
-        "    const int* __restrict__ b2, const float* __restrict__ m2, signed char* __restrict__ Y,\n"
-        "    int M, float res_mult, float acc_mult) {\n"
-        "  mdlc::QMlpArgs g{X, W1, b1, m1, table, W2, b2, m2, Y, M, res_mult, acc_mult};\n"
+        "    const signed char* __restrict__ X, const signed char* __restrict__ Wd,\n"
+        "    const int* __restrict__ bd, const float* __restrict__ md,\n"
+        "    const signed char* __restrict__ W1, const int* __restrict__ b1,\n"
+        "    const float* __restrict__ m1, const signed char* __restrict__ table,\n"
+        "    const signed char* __restrict__ W2, const int* __restrict__ b2,\n"
+        "    const float* __restrict__ m2, signed char* __restrict__ Y,\n"
+        "    int M, int H, int W, float res_mult, float acc_mult) {\n"
+        "  mdlc::QMlpArgs g{X, Wd, bd, md, W1, b1, m1, table, W2, b2, m2, Y, M, H, W, res_mult,\n"
+        "                   acc_mult};\n"
         f"  mdlc::qmlp_i8<{', '.join(str(v) for v in args)}>(g);\n}}\n")
 
 

@@ -96,4 +96,52 @@ class FuseQuantMlp(Pass):
         return changed
 
 
-__all__ = ["FuseQuantMlp"]
+class FuseQuantMixer(Pass):
+    """Fold a block's depthwise token mixer into the ``QMlp`` that consumes
+    it: ``x = QConv(z, Wd, bd, md)`` (depthwise, KxK odd, stride 1, same-size
+    padding, no epilogue) feeding only ``y = QMlp(x, ...)`` becomes
+    ``y = QMlp(z, Wd, bd, md, ...)`` with ``attrs["mixer"]`` holding the
+    conv's window (``kernel_shape``, ``pads``, ``activation``) and
+    ``attrs["mixed"]`` the name ``x`` had. The value is the composition, so it
+    is bit-identical; the device kernel computes ``x`` in its prologue and
+    keeps it on chip (it is also the residual). Runs after shape inference."""
+    name = "fuse_quant_mixer"
+
+    def run(self, graph: Graph) -> bool:
+        changed = False
+        prod = graph.producers()
+        for q in list(graph.nodes):
+            if q.op_type != "QMlp" or q.attrs.get("mixer"):
+                continue
+            x = q.inputs[0]
+            d = prod.get(x)
+            if d is None or d.op_type != "QConv" or d.attrs.get("epilogue"):
+                continue
+            if x in graph.outputs or graph.use_count().get(x, 0) != 1:
+                continue
+            if not all(graph.is_constant(e) for e in d.inputs[1:4]):
+                continue
+            zi, xi = graph.info(d.inputs[0]), graph.info(x)
+            if zi is None or xi is None or tuple(zi.shape) != tuple(xi.shape) or len(zi.shape) != 4:
+                continue
+            C = zi.shape[1]
+            w = graph.initializers[d.inputs[1]]
+            a = d.attrs
+            kh, kw = (list(a.get("kernel_shape") or w.shape[2:]) + [1, 1])[:2]
+            pads = [int(p) for p in a.get("pads", [0, 0, 0, 0])]
+            if (int(a.get("group", 1)) != C or w.shape[:2] != (C, 1) or kh % 2 == 0 or kw % 2 == 0
+                    or list(a.get("strides", [1, 1])) != [1, 1]
+                    or any(int(v) != 1 for v in a.get("dilations", [1, 1]))
+                    or pads != [kh // 2, kw // 2, kh // 2, kw // 2]):
+                continue
+            mixer = {"kernel_shape": [int(kh), int(kw)], "pads": pads, "activation": a.get("activation")}
+            fused = Node("QMlp", list(d.inputs[:4]) + list(q.inputs[1:]), list(q.outputs),
+                         dict(q.attrs, mixer=mixer, mixed=x), (d.name or "QConv") + "+" + (q.name or "mlp"),
+                         list(d.fused_from or ["QConv"]) + list(q.fused_from or ["QMlp"]))
+            graph.nodes[graph.nodes.index(d)] = fused
+            graph.remove_nodes([q])
+            changed = True
+        return changed
+
+
+__all__ = ["FuseQuantMlp", "FuseQuantMixer"]

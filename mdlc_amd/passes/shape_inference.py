@@ -106,8 +106,8 @@ def node_output_infos(node: Node, shape_of, dtype_of, const_of) -> list:
         g = conv_geometry(node, s0, shape_of(ins[1]))
         dt = DType.INT8 if op == "QConv" else d0
         return [((g["N"], g["OC"], g["OH"], g["OW"]), dt)]
-    if op == "QMlp":                 # two 1x1 QConvs, C -> E -> C, residual added
-        return [((s0[0], shape_of(ins[5])[0]) + tuple(s0[2:]), DType.INT8)]
+    if op == "QMlp":                 # [token mixer,] two 1x1 QConvs C -> E -> C, residual
+        return [((s0[0], shape_of(ins[-3])[0]) + tuple(s0[2:]), DType.INT8)]
     if op in ("Gemm", "FusedGemmAct", "QGemm"):
         sa, sb = shape_of(ins[0]), shape_of(ins[1])
         m = sa[1] if a.get("transA", 0) else sa[0]

@@ -199,8 +199,16 @@ class ReferenceExecutor:
                 return [quant.qadd(ins[4], q, a["res_mult"], a["acc_mult"])]
             return [q]
         if op == "QMlp":
-            # the composition it folds: QConv 1x1 + lookup, then QConv 1x1 +
-            # residual add of the first conv's input
+            # the composition it folds: [a depthwise stride-1 QConv token
+            # mixer,] QConv 1x1 + lookup, then QConv 1x1 + residual add of the
+            # first 1x1 conv's input
+            if a.get("mixer"):
+                mx = a["mixer"]
+                lod = 0 if mx.get("activation") == "Relu" else quant.QMIN
+                xm = quant.requant(quant.conv_acc(ins[0], ins[1], ins[2], strides=[1, 1], pads=mx["pads"],
+                                                  dilations=[1, 1], group=ins[0].shape[1]),
+                                   ins[3].reshape(1, -1, 1, 1), lod)
+                ins = [xm] + list(ins[4:])
             one = dict(strides=[1, 1], pads=[0, 0, 0, 0], dilations=[1, 1], group=1)
             lo1 = 0 if a.get("activation1") == "Relu" else quant.QMIN
             lo2 = 0 if a.get("activation2") == "Relu" else quant.QMIN

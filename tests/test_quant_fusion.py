@@ -9,7 +9,7 @@ import numpy as np
 from mdlc_amd.compiler import compile_graph
 from mdlc_amd.ir import verify_graph
 from mdlc_amd.passes.fuse_quant_epilogue import FuseQuantEpilogue
-from mdlc_amd.passes.fuse_quant_mlp import FuseQuantMlp
+from mdlc_amd.passes.fuse_quant_mlp import FuseQuantMixer, FuseQuantMlp
 from mdlc_amd.passes.shape_inference import infer_shapes
 from mdlc_amd.tools.build_repvit_int8 import build_repvit_int8, make_input
 from mdlc_amd.tools.graph_builder import GraphBuilder
@@ -115,6 +115,8 @@ def test_repvit_channel_mixers_fold_into_qmlp():
     c = compile_graph(build_repvit_int8(batch=32), feeds={"input": make_input(32)})
     hist = c.graph.op_histogram()
     assert hist["QMlp"] == 21 and "QLut" not in hist and "QAdd" not in hist
+    # the token mixers of the 19 blocks whose MLP input is a stride-1 depthwise conv
+    assert sum(1 for n in c.graph.nodes if n.op_type == "QMlp" and n.attrs.get("mixer")) == 19
     epis = [n.attrs.get("epilogue") for n in c.graph.nodes if n.op_type == "QConv"]
     assert epis.count("lut") == 3 and epis.count("add") == 2
     ca = compile_graph(build_repvit_int8(batch=1), feeds={"input": make_input(1)},
@@ -183,3 +185,56 @@ def test_mlp_fold_conditions():
     # 25 rows against 2 * 64 * 128 weight bytes: only when forced
     assert not FuseQuantMlp().run(_mlp(c=64, e=128))
     assert FuseQuantMlp(always=True).run(_mlp(c=64, e=128))
+
+
+def _mixed(*, stride=1, second_use=False, epilogue=False):
+    """Quantize -> depthwise 3x3 QConv -> the channel mixer of ``_mlp``."""
+    rng = np.random.default_rng(4)
+    b = GraphBuilder("mix")
+    c, e = 16, 32
+    b.input("x", (1, c, 6, 6))
+    b.node("QuantizeLinear", ["x"], "z", inv_scale=10.0)
+    b.const("wd", rng.integers(-127, 128, (c, 1, 3, 3)).astype(np.int8))
+    b.const("bd", np.zeros(c, np.int32))
+    b.const("md", np.full(c, 0.004, np.float32))
+    b.node("QConv", ["z", "wd", "bd", "md"], "xq", kernel_shape=[3, 3], strides=[stride, stride],
+           pads=[1, 1, 1, 1], group=c)
+    if epilogue:
+        b.const("t0", np.arange(-128, 128).clip(-127, 127).astype(np.int8))
+        b.node("QLut", ["xq", "t0"], "xl")
+    xin = "xl" if epilogue else "xq"
+    b.const("w1", rng.integers(-127, 128, (e, c, 1, 1)).astype(np.int8))
+    b.const("b1", np.zeros(e, np.int32))
+    b.const("m1", np.full(e, 0.002, np.float32))
+    b.const("t", np.arange(-128, 128).clip(-127, 127).astype(np.int8))
+    b.const("w2", rng.integers(-127, 128, (c, e, 1, 1)).astype(np.int8))
+    b.const("b2", np.zeros(c, np.int32))
+    b.const("m2", np.full(c, 0.002, np.float32))
+    one = dict(kernel_shape=[1, 1], strides=[1, 1], pads=[0] * 4)
+    b.node("QConv", [xin, "w1", "b1", "m1"], "h0", **one)
+    b.node("QLut", ["h0", "t"], "h")
+    b.node("QConv", ["h", "w2", "b2", "m2"], "y0", **one)
+    b.node("QAdd", [xin, "y0"], "y", ma=0.5, mb=0.5)
+    b.output("y")
+    if second_use:
+        b.output("xq")
+    g = b.graph()
+    FuseQuantEpilogue().run(g)
+    infer_shapes(g)
+    FuseQuantMlp(always=True).run(g)
+    return g
+
+
+def test_mixer_fold_conditions():
+    g = _mixed()
+    ref = run_reference(g, {"x": np.random.default_rng(5).standard_normal((1, 16, 6, 6)).astype(np.float32)})
+    assert FuseQuantMixer().run(g)
+    (node,) = [n for n in g.nodes if n.op_type == "QMlp"]
+    assert node.inputs[:4] == ["z", "wd", "bd", "md"] and node.attrs["mixed"] == "xq"
+    assert node.attrs["mixer"] == {"kernel_shape": [3, 3], "pads": [1, 1, 1, 1], "activation": None}
+    got = run_reference(g, {"x": np.random.default_rng(5).standard_normal((1, 16, 6, 6)).astype(np.float32)})
+    np.testing.assert_array_equal(got["y"], ref["y"])
+    # a strided mixer changes the size; an output that is seen elsewhere, or
+    # one that went through a fused lookup first, stays a separate conv
+    for kw in (dict(stride=2), dict(second_use=True), dict(epilogue=True)):
+        assert not FuseQuantMixer().run(_mixed(**kw)), kw
