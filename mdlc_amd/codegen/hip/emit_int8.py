@@ -101,7 +101,51 @@ class Int8LoweringMixin:
                                               "inv_s": float(node.attrs["inv_scale"]), "node": node,
                                               "bytes": 5 * total}))
 
+    def _lower_qconv_first(self, g, node):
+        """A QConv that quantizes its own float32 NCHW input (few channels):
+        one thread per output pixel, v_dot4 over the packed window."""
+        x, w, b, m = node.inputs[:4]
+        geo = conv_geometry(node, self._shape(g, x), self._shape(g, w))
+        OC, C, KH, KW = geo["OC"], geo["C"], geo["KH"], geo["KW"]
+        K = C * KH * KW
+        if geo["group"] != 1 or K > 64 or OC % 4 or OC > 64 or geo["DH"] != 1 or geo["DW"] != 1:
+            raise NotImplementedError("HIP codegen: fused input quantization needs a small "
+                                      "ungrouped conv (C*KH*KW <= 64, OC <= 64 and % 4 == 0, "
+                                      "no dilation)")
+        self._check_dtype(g, x, "float32")
+        y = node.outputs[0]
+        self.layout[y] = "NHWC"
+        kq = -(-K // 4)
+        wp = np.zeros((OC, kq * 4), np.int8)
+        wp[:, :K] = np.asarray(g.initializers[w], np.int8).reshape(OC, K)     # k = (c, kh, kw)
+        wdev = self._pack_raw(f"{w}__dev_dot4", wp.view(np.int32).copy())
+        epi, tab = 0, None
+        kind = node.attrs.get("epilogue")
+        if kind == "lut":
+            epi, tab = 1, node.inputs[4]
+            if not g.is_constant(tab) or np.asarray(g.initializers[tab]).size != 256:
+                raise NotImplementedError("HIP codegen: a fused lookup needs a constant 256-entry table")
+        elif kind:
+            raise NotImplementedError(f"HIP codegen: epilogue {kind!r} on a conv that quantizes its input")
+        lo = 0 if node.attrs.get("activation") == "Relu" else -127
+        win = (KH, KW, geo["SH"], geo["SW"], geo["PT"], geo["PL"])
+        kname = self._kernel(("qconv_first", C, win, OC, lo, epi), lambda i: T.qconv_first_kernel(
+            f"qconv_first_c{C}_{'x'.join(map(str, win))}_oc{OC}{'_lut' if epi else ''}_{i}", C, win, OC,
+            lo=lo, epi=epi))
+        P = geo["N"] * geo["OH"] * geo["OW"]
+        if P * OC >= 2 ** 31:
+            raise NotImplementedError("HIP codegen: int8 conv output of 2 GiB or more")
+        ins = [x, wdev, self._padded_vector(g, b, OC, np.int32), self._padded_vector(g, m, OC, np.float32)]
+        self.plan.append(Launch(
+            "qconv_first", kname, ins + ([tab] if tab else []), [y], (-(-P // 256), 1, 1), (256, 1, 1),
+            {**{k: geo[k] for k in ("N", "H", "W", "OH", "OW")}, "inv_s": float(node.attrs["quantize_input"]),
+             "node": node, "ops": 2 * P * OC * K,
+             "bytes": 4 * geo["N"] * C * geo["H"] * geo["W"] + P * OC + OC * (kq * 4 + 8)}))
+
     def _lower_qconv(self, g, node):
+        if node.attrs.get("quantize_input") is not None:
+            self._lower_qconv_first(g, node)
+            return
         x, w, b, m = node.inputs[:4]
         if self.layout.get(x) != "NHWC":
             raise NotImplementedError("HIP codegen: QConv input must come from the int8 path")

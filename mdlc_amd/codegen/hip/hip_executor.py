@@ -146,6 +146,10 @@ class HipExecutor:
             args += [P(l.inputs[4]) if len(l.inputs) > 4 else Arg.ptr(0)]
             args += [I(m[f]) for f in ("M", "N", "K", "lda", "ldb", "ldc", "Cin", "H", "W", "OH", "OW")]
             args += [Arg.f32(m.get("res_mult", 0.0)), Arg.f32(m.get("acc_mult", 0.0))]
+        elif k == "qconv_first":
+            args = [P(l.inputs[0]), Arg.f32(m["inv_s"])] + [P(e) for e in l.inputs[1:4]]
+            args += [P(l.inputs[4]) if len(l.inputs) > 4 else Arg.ptr(0), P(l.outputs[0])]
+            args += [I(m[f]) for f in ("N", "H", "W", "OH", "OW")]
         elif k == "qmlp":
             args = [P(e) for e in l.inputs]
             if not m["mixer"]:                     # no token mixer: null Wd, bd, md

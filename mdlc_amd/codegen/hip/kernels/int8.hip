@@ -451,6 +451,68 @@ __device__ __forceinline__ void qdwconv_nhwc(const i8* __restrict__ x, const i8*
   }
 }
 
+// First conv of an int8 network fused with its input quantization. x is the
+// float32 NCHW network input with few channels (K = C*KH*KW <= 64). One
+// thread per output pixel quantizes its receptive field with the
+// QuantizeLinear arithmetic (clamp(rint(x * inv_s), -127, 127); zeros where
+// the window leaves the image, as the conv pads the quantized tensor), packs
+// the codes four to a register in k = (c, kh, kw) order and forms every
+// output channel with v_dot4_i32_i8 against the weights, packed the same way
+// ([OC][KP/4], K zero padded to KP) and staged in LDS. Then the usual
+// requant (bias added to the exact int32 sum), an optional fused lookup, and
+// OC channels-last bytes per pixel.
+template <int C, int KH, int KW, int SH, int SW, int PT, int PL, int OC, int LO, int EPI>
+__device__ __forceinline__ void qconv_first(const float* __restrict__ x, float inv_s,
+                                            const int* __restrict__ w, const int* __restrict__ bias,
+                                            const float* __restrict__ mult,
+                                            const i8* __restrict__ table, i8* __restrict__ y,
+                                            int N, int H, int W, int OH, int OW) {
+  constexpr int K = C * KH * KW, KQ = (K + 3) / 4;
+  static_assert(K <= 64 && OC % 4 == 0 && OC <= 64, "small first-layer convs only");
+  __shared__ int ws[OC * KQ];
+  __shared__ int bs[OC];
+  __shared__ float ms[OC];
+  __shared__ i8 tab[256];
+  for (int i = threadIdx.x; i < OC * KQ; i += 256) ws[i] = w[i];
+  if (threadIdx.x < OC) {
+    bs[threadIdx.x] = bias[threadIdx.x];
+    ms[threadIdx.x] = mult[threadIdx.x];
+  }
+  if (EPI == 1) tab[threadIdx.x] = table[threadIdx.x];
+  __syncthreads();
+  const long long p = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (p >= (long long)N * OH * OW) return;
+  const int ow = (int)(p % OW);
+  const int oh = (int)((p / OW) % OH);
+  const int n = (int)(p / ((long long)OW * OH));
+  int q[KQ];
+#pragma unroll
+  for (int j = 0; j < KQ; ++j) q[j] = 0;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int c = k / (KH * KW), kh = (k / KW) % KH, kw = k % KW;
+    const int ih = oh * SH - PT + kh, iw = ow * SW - PL + kw;
+    int code = 0;
+    if ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W) {
+      const float r = rintf(x[(((size_t)n * C + c) * H + ih) * W + iw] * inv_s);
+      code = (int)fminf(fmaxf(r, -127.0f), 127.0f);
+    }
+    q[k / 4] |= (code & 0xff) << (8 * (k % 4));
+  }
+  union { int w[OC / 4]; i8 b[OC]; } out;
+#pragma unroll
+  for (int oc = 0; oc < OC; ++oc) {
+    int acc = 0;
+#pragma unroll
+    for (int j = 0; j < KQ; ++j) acc = __builtin_amdgcn_sdot4(q[j], ws[oc * KQ + j], acc, false);
+    const i8 code = requant(acc + bs[oc], ms[oc], (float)LO);
+    out.b[oc] = EPI == 1 ? tab[(int)code + 128] : code;
+  }
+  int* yp = reinterpret_cast<int*>(y + p * OC);
+#pragma unroll
+  for (int j = 0; j < OC / 4; ++j) yp[j] = out.w[j];
+}
+
 // Quantize float32 NCHW -> int8 NHWC: clamp(rint(x * inv_s), -127, 127).
 __device__ __forceinline__ void quantize_nchw_nhwc(const float* __restrict__ x, i8* __restrict__ y,
                                                    int N, int C, int HW, float inv_s) {

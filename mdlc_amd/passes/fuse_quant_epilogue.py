@@ -75,4 +75,46 @@ class FuseQuantEpilogue(Pass):
         return changed
 
 
-__all__ = ["FuseQuantEpilogue"]
+class FuseInputQuantize(Pass):
+    """Fold ``xq = QuantizeLinear(x)`` into the one QConv that reads it when
+    that conv is small enough to quantize its own window (the first layer of
+    an int8 network: float32 NCHW input, C*KH*KW <= 64, ungrouped, no
+    dilation, at most 64 output channels and a multiple of 4, no epilogue or
+    a lookup). The
+    conv then takes ``x`` itself and ``attrs["quantize_input"]`` = the
+    quantizer's ``inv_scale``; its value is the composition, bit for bit.
+    Runs after shape inference."""
+    name = "fuse_input_quantize"
+
+    def run(self, graph: Graph) -> bool:
+        changed = False
+        for qn in list(graph.nodes):
+            if qn.op_type != "QuantizeLinear":
+                continue
+            x, xq = qn.inputs[0], qn.outputs[0]
+            xi = graph.info(x)
+            if xi is None or len(xi.shape) != 4 or xi.dtype != "float32":
+                continue
+            if xq in graph.outputs or graph.use_count().get(xq, 0) != 1:
+                continue
+            (conv,) = graph.consumers()[xq]
+            a = conv.attrs
+            if conv.op_type != "QConv" or conv.inputs[0] != xq or a.get("epilogue") not in (None, "lut"):
+                continue
+            w = graph.initializers.get(conv.inputs[1])
+            if w is None or int(a.get("group", 1)) != 1 or w.shape[0] % 4 or w.shape[0] > 64 \
+                    or w[0].size > 64:
+                continue
+            if any(int(d) != 1 for d in a.get("dilations", [1, 1])):
+                continue
+            attrs = dict(a, quantize_input=float(qn.attrs["inv_scale"]))
+            fused = Node("QConv", [x] + list(conv.inputs[1:]), list(conv.outputs), attrs,
+                         "QuantizeLinear+" + (conv.name or "QConv"),
+                         ["QuantizeLinear"] + list(conv.fused_from or ["QConv"]))
+            graph.nodes[graph.nodes.index(conv)] = fused
+            graph.remove_nodes([qn])
+            changed = True
+        return changed
+
+
+__all__ = ["FuseQuantEpilogue", "FuseInputQuantize"]

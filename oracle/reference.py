@@ -187,6 +187,8 @@ class ReferenceExecutor:
         if op == "DequantizeLinear":
             return [quant.dequantize(ins[0], a["scale"])]
         if op == "QConv":
+            if a.get("quantize_input") is not None:      # a folded QuantizeLinear
+                ins = [quant.quantize(ins[0], a["quantize_input"])] + list(ins[1:])
             acc = quant.conv_acc(ins[0], ins[1], opt(2), strides=a.get("strides", [1, 1]),
                                  pads=a.get("pads"), dilations=a.get("dilations", [1, 1]),
                                  group=a.get("group", 1))

@@ -139,11 +139,13 @@ def test_repvit_int8_module_compiles_and_is_channels_last():
         c = compile_graph(build_repvit_int8(batch=2), feeds={"input": make_input(2)},
                           fuse_int8_epilogues=fused, int8_depthwise=dw)
         kinds = {l.kind for l in c.module.plan}
-        assert kinds >= {"quantize", "qgemm", "qgap"}
+        assert kinds >= {"qgemm", "qgap"}
+        assert ("quantize" in kinds) != fused and ("qconv_first" in kinds) == fused
         assert ("qlut" in kinds and "qadd" in kinds) != fused
         assert ("qdwconv" in kinds) == (dw == "vector")
+        assert ("qmlp" in kinds) == fused                   # stages 1-2 fold at batch 2
         assert c.module.fallbacks() == []
         assert all(c.module.device_layout.get(l.outputs[0]) == "NHWC"
-                   for l in c.module.plan if l.kind in ("qdwconv", "qlut", "qadd", "qgemm")
-                   and l.meta.get("OH"))
+                   for l in c.module.plan if (l.kind in ("qdwconv", "qlut", "qadd", "qgemm")
+                                              and l.meta.get("OH")) or l.kind in ("qmlp", "qconv_first"))
         R.compile_code_object(c.module.sources())

@@ -176,8 +176,10 @@ def test_repvit_int8_every_tensor_bit_exact(batch, mode, hip_ctx):
     assert c.module.fallbacks() == []
     nq = sum(l.kind == "qmlp" for l in c.module.plan)
     assert nq == ({2: 6, 32: 21}[batch] if mode == "mlp" else 0)
+    nf = sum(l.kind == "qconv_first" for l in c.module.plan)     # stem + its GELU + the quantize
+    assert nf == (0 if mode == "unfused" else 1)
     epis = [l.meta.get("epilogue", 0) for l in c.module.plan if l.kind == "qgemm"]
-    want_epis = (0, 0) if mode == "unfused" else (24 - nq, 23 - nq)
+    want_epis = (0, 0) if mode == "unfused" else (24 - nq - nf, 23 - nq)
     assert (epis.count(1), epis.count(2)) == want_epis
     n = 0
     for name, v in got.items():
@@ -365,3 +367,46 @@ def test_int8_gemm_4096_cube_rows_exact(hip_ctx):
     f = acc.astype(np.int32).astype(np.float32) * mult
     want = np.clip(np.rint(f), -127, 127).astype(np.int8)
     np.testing.assert_array_equal(y[rows], want)
+
+
+@pytest.mark.parametrize("case", [(2, 3, 31, 24, 3, 2, "lut"), (1, 3, 16, 24, 3, 2, None),
+                                  (2, 1, 9, 8, 5, 1, "lut"), (1, 4, 12, 16, 3, 1, "relu"),
+                                  (3, 2, 7, 12, 3, 2, None)],
+                         ids=lambda c: "n{}c{}hw{}oc{}k{}s{}_{}".format(*c))
+def test_first_conv_quantizes_its_input(case, hip_ctx):
+    """QuantizeLinear folded into a small first QConv (float NCHW in, one
+    thread per output pixel, dot4 over the packed window), with a fused
+    lookup, a ReLU or neither: equal to the oracle and to the separate
+    quantize + conv launches."""
+    n, c, hw, oc, k, s, post = case
+
+    def graph():
+        rng = np.random.default_rng(21)
+        b = GraphBuilder("first")
+        b.input("x", (n, c, hw, hw))
+        b.node("QuantizeLinear", ["x"], "xq", inv_scale=25.0)
+        b.const("w", rng.integers(-127, 128, (oc, c, k, k)).astype(np.int8))
+        b.const("b", rng.integers(-3000, 3000, oc).astype(np.int32))
+        b.const("m", (rng.uniform(0.5, 1.5, oc) * 0.01 / np.sqrt(c * k * k)).astype(np.float32))
+        attrs = dict(kernel_shape=[k, k], strides=[s, s], pads=[k // 2] * 4)
+        if post == "relu":
+            attrs["activation"] = "Relu"
+        b.node("QConv", ["xq", "w", "b", "m"], "y", **attrs)
+        out = "y"
+        if post == "lut":
+            b.const("t", rng.integers(-127, 128, 256).astype(np.int8))
+            b.node("QLut", ["y", "t"], "z")
+            out = "z"
+        b.output(out)
+        feeds = {"x": (rng.standard_normal((n, c, hw, hw)) * 2).astype(np.float32)}
+        return b.graph(), feeds, out
+
+    g, feeds, out = graph()
+    cmod, got, want = device_run(g, feeds, ctx=hip_ctx)
+    assert [l.kind for l in cmod.module.plan] == ["qconv_first"]
+    np.testing.assert_array_equal(got[out], want[out])
+    g2, _, _ = graph()
+    _, got2, want2 = device_run(g2, feeds, ctx=hip_ctx, fuse_int8_epilogues=False)
+    np.testing.assert_array_equal(got[out], got2[out])
+    v = want2["y"].astype(int) if "y" in want2 else want[out].astype(int)
+    assert v.std() > 3 and np.mean(np.abs(v) == 127) < 0.5
