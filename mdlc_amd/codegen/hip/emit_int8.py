@@ -377,9 +377,12 @@ class Int8LoweringMixin:
         n, c, h, w = self._shape(g, x)
         if self.layout.get(x) != "NHWC":
             raise NotImplementedError("HIP codegen: QGlobalAveragePool expects the int8 path")
-        self._kernel("qgap", lambda i: T.qgap_kernel("qgap"))
+        per_image = c % 4 == 0 and c <= 1024
+        kname = "qgap_wg" if per_image else "qgap"
+        self._kernel(kname, lambda i: T.qgap_kernel(kname, per_image))
         self.layout[node.outputs[0]] = "NHWC"
-        self.plan.append(Launch("qgap", "qgap", [x], [node.outputs[0]], (-(-(n * c) // 256), 1, 1),
+        grid = n if per_image else -(-(n * c) // 256)
+        self.plan.append(Launch("qgap", kname, [x], [node.outputs[0]], (grid, 1, 1),
                                 (256, 1, 1), {"N": n, "C": c, "HW": h * w,
                                               "m": float(node.attrs["mult"]), "node": node,
                                               "bytes": n * c * (h * w + 1)}))

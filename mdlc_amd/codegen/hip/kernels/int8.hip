@@ -793,6 +793,38 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   }, [] {});
 }
 
+// The same pool with one workgroup per image for C % 4 == 0, C <= 1024:
+// thread t sums channels [4g, 4g+4) (g = t % (C/4)) over the pixels
+// p = t / (C/4) (mod R), R = 256 / (C/4), with 32-bit loads coalesced along
+// the channels; the R partial sums of each channel meet in LDS. Integer
+// sums are exact, so the result equals qgap_nhwc's.
+__device__ __forceinline__ void qgap_nhwc_wg(const i8* __restrict__ x, i8* __restrict__ y, int C,
+                                             int HW, float m) {
+  __shared__ int part[1024];
+  const int n = blockIdx.x;
+  const int G = C / 4, R = 256 / G;
+  const int t = threadIdx.x, gi = t % G, r = t / G;
+  int s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+  if (r < R) {
+    const i8* xp = x + (size_t)n * HW * C + 4 * gi;
+    for (int p = r; p < HW; p += R) {
+      union { int w; i8 b[4]; } v;
+      v.w = *reinterpret_cast<const int*>(xp + (size_t)p * C);
+      s0 += v.b[0]; s1 += v.b[1]; s2 += v.b[2]; s3 += v.b[3];
+    }
+  }
+  for (int c = t; c < C; c += 256) part[c] = 0;
+  __syncthreads();
+  if (r < R) {
+    atomicAdd(&part[4 * gi], s0);
+    atomicAdd(&part[4 * gi + 1], s1);
+    atomicAdd(&part[4 * gi + 2], s2);
+    atomicAdd(&part[4 * gi + 3], s3);
+  }
+  __syncthreads();
+  for (int c = t; c < C; c += 256) y[(size_t)n * C + c] = requant(part[c], m, -127.0f);
+}
+
 // Dequantize: float(q) * s; an NHWC 4-D input is written back as NCHW.
 __device__ __forceinline__ void dequantize_i8(const i8* __restrict__ x, float* __restrict__ y,
                                               long long n, int C, int HW, float s) {

@@ -466,11 +466,14 @@ def qlut_kernel(name: str = "qlut") -> tuple:
         "  mdlc::qlut_i8(x, table, y, n);\n}\n")
 
 
-def qgap_kernel(name: str = "qgap") -> tuple:
+def qgap_kernel(name: str = "qgap", per_image: bool = False) -> tuple:
+    """int8 global average pool; ``per_image``: one workgroup per image (C % 4 == 0).
+    ABI: (x, y, int N, int C, int HW, float m)."""
+    body = "mdlc::qgap_nhwc_wg(x, y, C, HW, m);" if per_image else "mdlc::qgap_nhwc(x, y, N, C, HW, m);"
     return name, (
         f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
         "    const signed char* __restrict__ x, signed char* __restrict__ y, int N, int C, int HW, float m) {\n"
-        "  mdlc::qgap_nhwc(x, y, N, C, HW, m);\n}\n")
+        f"  {body}\n}}\n")
 
 
 def dequantize_kernel(name: str = "dequantize") -> tuple:

@@ -17,6 +17,7 @@ from mdlc_amd.codegen.hip.emit import HipModule, emit_hip_module
 from mdlc_amd.ir import Graph, verify_graph
 from mdlc_amd.passes import default_pipeline
 from mdlc_amd.passes.base import PassManager
+from mdlc_amd.passes.fold_flatten import FoldPoolFlatten
 from mdlc_amd.passes.fuse_quant_epilogue import FuseInputQuantize, FuseQuantEpilogue
 from mdlc_amd.passes.fuse_quant_mlp import FuseQuantMixer, FuseQuantMlp
 from mdlc_amd.passes.fuse_residual import FuseResidualEpilogue
@@ -67,7 +68,9 @@ def compile_graph(graph: Graph, *, batch: int = 1, feeds: Optional[dict] = None,
     lookup followed by a 1x1 QConv + residual add of the first's input into
     one ``QMlp`` node where that pays ("always": wherever the kernel tiles),
     and folds the depthwise token mixer that feeds it into the same node; the
-    int8 folds also let a small first conv quantize its own float input. ``int8_depthwise`` picks the int8 depthwise kernel
+    int8 folds also let a small first conv quantize its own float input.
+    With ``fuse_residual`` a global average pool also writes the flattened
+    output of a Flatten that follows it. ``int8_depthwise`` picks the int8 depthwise kernel
     ("mfma" or "vector")."""
     original = graph.clone()
     if feeds is None:
@@ -81,7 +84,7 @@ def compile_graph(graph: Graph, *, batch: int = 1, feeds: Optional[dict] = None,
     post = ([FuseResidualEpilogue()] if fuse_residual else []) + \
         ([FuseQuantMlp(always=fuse_int8_mlp == "always"), FuseQuantMixer()]
          if quant and fuse_int8_mlp else []) + \
-        ([FuseInputQuantize()] if quant else [])
+        ([FuseInputQuantize()] if quant else []) + ([FoldPoolFlatten()] if fuse_residual else [])
     if post:
         PassManager(post, verify=_structural_verifier(verify), history=pm.history).run(graph)
     mem_plan = plan_memory(graph)

@@ -75,12 +75,18 @@ class FuseQuantEpilogue(Pass):
         return changed
 
 
+# With this few input channels the channels-last byte gather of the int8
+# conv kernels is at its least efficient; wider inputs keep the quantize
+# launch and the GEMM conv.
+MAX_FIRST_CIN = 4
+
+
 class FuseInputQuantize(Pass):
     """Fold ``xq = QuantizeLinear(x)`` into the one QConv that reads it when
     that conv is small enough to quantize its own window (the first layer of
-    an int8 network: float32 NCHW input, C*KH*KW <= 64, ungrouped, no
-    dilation, at most 64 output channels and a multiple of 4, no epilogue or
-    a lookup). The
+    an int8 network: float32 NCHW input with at most ``MAX_FIRST_CIN``
+    channels, C*KH*KW <= 64, ungrouped, no dilation, at most 64 output
+    channels and a multiple of 4, no epilogue or a lookup). The
     conv then takes ``x`` itself and ``attrs["quantize_input"]`` = the
     quantizer's ``inv_scale``; its value is the composition, bit for bit.
     Runs after shape inference."""
@@ -103,7 +109,7 @@ class FuseInputQuantize(Pass):
                 continue
             w = graph.initializers.get(conv.inputs[1])
             if w is None or int(a.get("group", 1)) != 1 or w.shape[0] % 4 or w.shape[0] > 64 \
-                    or w[0].size > 64:
+                    or w.shape[1] > MAX_FIRST_CIN or w[0].size > 64:
                 continue
             if any(int(d) != 1 for d in a.get("dilations", [1, 1])):
                 continue

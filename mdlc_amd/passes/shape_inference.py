@@ -123,6 +123,8 @@ def node_output_infos(node: Node, shape_of, dtype_of, const_of) -> list:
     if op == "AveragePool":
         return [(_pool_shape(node, s0, dil=False), d0)]
     if op in ("GlobalAveragePool", "QGlobalAveragePool"):
+        if a.get("flatten"):                 # a folded Flatten(axis=1)
+            return [(tuple(s0[:2]), d0)]
         return [(tuple(s0[:2]) + (1,) * (len(s0) - 2), d0)]
     if op in ("BatchNormalization", "Relu", "Sigmoid", "Tanh", "HardSwish", "HardSigmoid",
               "LeakyRelu", "Clip", "Softmax", "Identity", "QLut"):

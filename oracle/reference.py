@@ -129,7 +129,8 @@ class ReferenceExecutor:
                                     count_include_pad=a.get("count_include_pad", 0),
                                     ceil_mode=a.get("ceil_mode", 0))]
         if op == "GlobalAveragePool":
-            return [ops.global_average_pool(ins[0])]
+            y = ops.global_average_pool(ins[0])
+            return [y.reshape(y.shape[:2]) if a.get("flatten") else y]
         if op in ("Relu", "Sigmoid", "Tanh", "HardSwish"):
             return [act(op, ins[0], a)]
         if op == "Clip":
@@ -229,7 +230,8 @@ class ReferenceExecutor:
         if op == "QLut":
             return [quant.lut(ins[0], ins[1])]
         if op == "QGlobalAveragePool":
-            return [quant.global_avg_pool(ins[0], a["mult"])]
+            y = quant.global_avg_pool(ins[0], a["mult"])
+            return [y.reshape(y.shape[:2]) if a.get("flatten") else y]
 
         raise NotImplementedError(f"reference executor: op {op!r} not implemented")
 
