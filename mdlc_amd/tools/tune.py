@@ -39,6 +39,8 @@ def model_problems(model: str, batch: int, conv_mode: str) -> list:
 
     if model == "int8_gemm":          # the square int8 GEMM benchmark, M = N = K = batch
         return [{"kind": "qgemm", "M": batch, "N": batch, "K": batch, "out_f32": False}]
+    if model == "fp32_gemm":          # a square dense fp32 GEMM, M = N = K = batch
+        return [{"kind": "gemm", "M": batch, "N": batch, "K": batch}]
     if model == "resnet18":
         from mdlc_amd.tools.build_resnet18 import build_resnet18
         graph = build_resnet18(batch=batch, calibrate=False)
