@@ -13,8 +13,8 @@ extended because nothing runs on the host here:
   im2col      batched column matrix for the explicit conv path
   dwconv      direct depthwise convolution + epilogue
   splitk_reduce  sums split-K partial slices in order + epilogue
-  quantize, qgemm, qconv, qdwconv, qadd, qlut, qgap, dequantize  (INT8 path,
-              int8 activations channels-last on the device)
+  quantize, qgemm, qconv, qdwconv, qadd, qlut, qgap, dequantize, qmlp,
+  qconv_first (INT8 path, int8 activations channels-last on the device)
   elementwise fused pointwise chain (also single pointwise ops)
   maxpool, gap, copy (reshaping views: Flatten/Reshape/Identity/...)
 
