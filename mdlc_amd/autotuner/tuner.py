@@ -32,7 +32,7 @@ MFMA_FLOPS_PER_CU_CLK = 256          # fp32 MFMA, dense
 CLOCK_GHZ = 2.4
 HBM_GBS = 8000.0
 LAUNCH_US = 2.0
-SPLITS = (1, 2, 4, 8)
+SPLITS = (1, 2, 3, 4, 5, 6, 8)
 
 
 def analytical_cost(sched: MfmaSchedule, M: int, N: int, K: int) -> float:

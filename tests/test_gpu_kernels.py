@@ -124,7 +124,7 @@ def test_conv_matches_oracle(case, mode, hip_ctx):
 
 
 @pytest.mark.parametrize("mode", ["implicit", "im2col"])
-@pytest.mark.parametrize("sk", [2, 4])
+@pytest.mark.parametrize("sk", [2, 4, 5])
 @pytest.mark.parametrize("case", [CONV_CASES[2], CONV_CASES[4], CONV_CASES[6]],
                          ids=lambda c: "x".join(map(str, c)))
 def test_conv_split_k(case, sk, mode, hip_ctx):
