@@ -158,14 +158,15 @@ def network(args, name: str) -> dict:
         from mdlc_amd.tools.build_repvit_int8 import build_repvit_int8 as build, make_input
     x = make_input(B)
     t0 = time.perf_counter()
+    folds = dict(fuse_residual=False, fuse_int8_epilogues=False) if args.no_fold else {}
     c = compile_graph(build(batch=B), feeds={"input": x}, conv_mode=args.conv_mode,
-                      schedule_fn=schedule_source(args))
+                      schedule_fn=schedule_source(args), **folds)
     log(f"{name} b={B}: compiled in {time.perf_counter() - t0:.1f} s, {len(c.module.plan)} launches")
     ms, host_s, prof, arena = time_module(c, {"input": x}, args.steps, args.warmup,
                                           args.profile_iters, args.graph)
     value = B * 1000.0 / ms
     log(f"{ms:.3f} ms/step, {value:.1f} images/s (arena {arena / 2**20:.1f} MiB)")
-    traffic = TRAFFIC_JSON if (name == "resnet18" and B == 32) else ""
+    traffic = TRAFFIC_JSON if (name == "resnet18" and B == 32 and not args.no_fold) else ""
     roof, _ = roofline(prof, traffic_json=traffic)
     int8 = name == "repvit_int8"
     work = sum(l.meta.get("ops" if int8 else "flops", 0) for l in c.module.plan)
@@ -183,6 +184,7 @@ def network(args, name: str) -> dict:
         "vs_baseline": None, "dtype": "i8" if int8 else "f32", "data": data,
         "config": {"workload": f"{name}_{'int8' if int8 else 'fp32'}_b{B}", "batch": B,
                    "image": [3, 224, 224], "conv_mode": args.conv_mode,
+                   "backend_folds": not args.no_fold,
                    "launches": len(c.module.plan), "gop_per_step": work / 1e9,
                    ("network_tops" if int8 else "network_tflops"): work / (ms * 1e-3) / 1e12,
                    "host_buffer_images_per_s": B / host_s},
@@ -277,6 +279,8 @@ def main(argv=None) -> int:
     ap.add_argument("--schedules", default="", help="tuner JSON cache to use instead of the "
                     "shipped mdlc_amd/autotuner/tuned_gfx950.json")
     ap.add_argument("--graph", action="store_true", help="replay the plan as a hipGraph")
+    ap.add_argument("--no-fold", action="store_true",
+                    help="the reference's fused groups only (no residual / int8 / pool folds)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-iters", type=int, default=3)
     args = ap.parse_args(argv)

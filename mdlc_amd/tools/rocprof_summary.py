@@ -4,6 +4,9 @@
     python -m mdlc_amd.tools.rocprof_summary pmc.db --counter FETCH_SIZE
     python -m mdlc_amd.tools.rocprof_summary --traffic fetch.db write.db \
         copy_fetch.db copy_write.db --copy-mib 256 --out traffic.json
+    python -m mdlc_amd.tools.rocprof_summary trace.db --rates traffic.json
+    python -m mdlc_amd.tools.rocprof_summary trace.db --per-launch KERNEL 8 \
+        --traffic fetch.db write.db copy_fetch.db copy_write.db
 
 The first form lists, per kernel name, the dispatch count, total and average
 duration and share of device time (the ``--kernel-trace --stats`` view). The
@@ -11,7 +14,10 @@ second lists the average value of one PMC counter per dispatch of each
 kernel (``--pmc`` runs). The third turns a FETCH_SIZE run and a WRITE_SIZE
 run of a workload, plus the same two counters read for a plain copy of
 ``--copy-mib`` MiB, into HBM bytes per dispatch for every kernel: each
-counter is scaled by (true copy bytes / counter reading for the copy).
+counter is scaled by (true copy bytes / counter reading for the copy). The
+fourth divides those bytes by each kernel's average traced duration (HBM
+GB/s against the 8 TB/s peak). ``--counter MfmaUtil`` (a derived counter of
+``rocprofv3 --pmc MfmaUtil``) gives the matrix-core busy percentage.
 """
 
 from __future__ import annotations
@@ -41,6 +47,26 @@ def counter_stats(path: str, counter: str) -> list:
     return rows
 
 
+def per_position(path: str, kernel: str, period: int, counter: str = "") -> list:
+    """Average duration (trace db) or counter value (pmc db) of ``kernel``'s
+    dispatches by position within each run of ``period`` consecutive ones
+    (e.g. the 8 launches one forward makes of a shared kernel)."""
+    con = sqlite3.connect(path)
+    if counter:
+        rows = con.execute(
+            "select p.counter_value from pmc_events p join kernels k on k.dispatch_id = p.dispatch_id "
+            "where k.name = ? and p.counter_name = ? order by k.dispatch_id", (kernel, counter)).fetchall()
+    else:
+        rows = con.execute("select duration from kernels where name = ? order by dispatch_id",
+                           (kernel,)).fetchall()
+    con.close()
+    sums, counts = [0.0] * period, [0] * period
+    for i, (v,) in enumerate(rows):
+        sums[i % period] += v
+        counts[i % period] += 1
+    return [s / max(c, 1) for s, c in zip(sums, counts)]
+
+
 def traffic(fetch_db, write_db, copy_fetch_db, copy_write_db, copy_mib) -> dict:
     true_kib = copy_mib * 1024.0
     cf = dict((n, v) for n, _, v in counter_stats(copy_fetch_db, "FETCH_SIZE"))["copy_bytes"]
@@ -61,7 +87,36 @@ def main(argv=None) -> int:
     ap.add_argument("--traffic", nargs=4, metavar=("FETCH_DB", "WRITE_DB", "COPY_FETCH_DB", "COPY_WRITE_DB"))
     ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--out", default="")
+    ap.add_argument("--rates", metavar="TRAFFIC_JSON", default="",
+                    help="with a kernel-trace db: HBM GB/s per kernel from a --traffic JSON")
+    ap.add_argument("--per-launch", nargs=2, metavar=("KERNEL", "PERIOD"),
+                    help="with a trace db and --traffic: HBM GB/s of each of a kernel's PERIOD "
+                         "launches per forward")
     args = ap.parse_args(argv)
+    if args.per_launch and args.traffic:
+        kernel, period = args.per_launch[0], int(args.per_launch[1])
+        true_kib = args.copy_mib * 1024.0
+        cf = dict((n, v) for n, _, v in counter_stats(args.traffic[2], "FETCH_SIZE"))["copy_bytes"]
+        cw = dict((n, v) for n, _, v in counter_stats(args.traffic[3], "WRITE_SIZE"))["copy_bytes"]
+        dur = per_position(args.db, kernel, period)
+        fet = per_position(args.traffic[0], kernel, period, "FETCH_SIZE")
+        wri = per_position(args.traffic[1], kernel, period, "WRITE_SIZE")
+        print(f"{'launch':>6s} {'avg_us':>8s} {'HBM_MB':>8s} {'GB/s':>7s} {'of 8 TB/s':>9s}")
+        for i in range(period):
+            b = (fet[i] * true_kib / cf + wri[i] * true_kib / cw) * 1024
+            gbs = b / (dur[i] * 1e-9) / 1e9
+            print(f"{i:6d} {dur[i] / 1e3:8.2f} {b / 1e6:8.2f} {gbs:7.0f} {gbs / 8000.0:9.1%}")
+        return 0
+    if args.rates:
+        with open(args.rates) as f:
+            t = json.load(f)["kernels"]
+        print(f"{'kernel':64s} {'avg_us':>9s} {'HBM_MB':>9s} {'GB/s':>8s} {'of 8 TB/s':>9s}")
+        for name, n, tot, avg, mn, mx in kernel_stats(args.db):
+            if name in t:
+                gbs = t[name]["traffic_bytes"] / (avg * 1e-9) / 1e9
+                print(f"{name[:64]:64s} {avg / 1e3:9.2f} {t[name]['traffic_bytes'] / 1e6:9.2f} "
+                      f"{gbs:8.0f} {gbs / 8000.0:9.1%}")
+        return 0
     if args.traffic:
         t = traffic(*args.traffic, args.copy_mib)
         text = json.dumps(t, indent=1, sort_keys=True)
