@@ -100,6 +100,32 @@ def test_resnet18_batch32_rows_match_single_images(hip_ctx):
         assert_close(f"oracle logits[{i}]", y32[i:i + 1], want, FP32_NETWORK)
 
 
+def test_mobilenetv2_batch32_rows_match_single_images(hip_ctx):
+    """MobileNetV2 at batch 32 (its own tuned schedules and kernels): every
+    image's logits equal the device's batch-1 run of that image within the
+    network tolerance, and two of them the oracle's."""
+    from mdlc_amd.tools.build_mobilenetv2 import make_input as mb_input
+
+    x = mb_input(32, seed=5)
+    c32 = compile_graph(build_mobilenetv2(batch=32), feeds={"input": x})
+    ex = HipExecutor(c32.module, hip_ctx)
+    try:
+        y32 = ex.run({"input": x})["outputs"]["logits"]
+    finally:
+        ex.close()
+    c1 = compile_graph(build_mobilenetv2(batch=1), feeds={"input": x[:1]})
+    ex1 = HipExecutor(c1.module, hip_ctx)
+    try:
+        for i in range(32):
+            yi = ex1.run({"input": x[i:i + 1]})["outputs"]["logits"]
+            assert_close(f"logits[{i}]", y32[i:i + 1], yi, FP32_NETWORK)
+    finally:
+        ex1.close()
+    for i in (0, 31):
+        want = run_reference(c1.graph, {"input": x[i:i + 1]})["logits"]
+        assert_close(f"oracle logits[{i}]", y32[i:i + 1], want, FP32_NETWORK)
+
+
 @pytest.mark.parametrize("fold", [True, False], ids=["residual_folded", "reference_groups"])
 def test_mobilenetv2_every_group(fold, hip_ctx):
     g = build_mobilenetv2(batch=1)
