@@ -46,6 +46,7 @@ from mdlc_amd.passes.shape_inference import conv_geometry
 ScheduleFn = Callable[[Optional[Node], tuple], MfmaSchedule]
 
 VIEW_OPS = {"Flatten", "Reshape", "Identity", "Squeeze", "Unsqueeze"}
+REDUCE_VEC = 4        # outputs per thread of the split-K reduce where the layout allows (else 1)
 
 
 class HipCodegen(Int8LoweringMixin):
@@ -279,14 +280,17 @@ class HipCodegen(Int8LoweringMixin):
         self.plan.append(Launch(kind, kname, list(operands), [ws], (tiles * slices, 1, 1), block,
                                 dict(meta, partial=True,
                                      bytes=meta["bytes"] - extra_bytes + 4 * slices * M * N)))
+        # four contiguous, 16-byte aligned outputs per thread when the layout allows
+        vec = REDUCE_VEC if N % 4 == 0 and (epi["hw"] % 4 == 0 if epi["hw"] else epi["ldc"] % 4 == 0) \
+            else 1
         rsig = ("splitk_reduce", bool(bias), epi["bias_mode"], epi["act_sig"], epi["alpha"], epi["beta"],
-                residual)
+                residual, vec)
         rname = self._kernel(rsig, lambda i: T.splitk_reduce_kernel(
-            f"splitk_reduce_{act or 'none'}_{epi['bias_mode']}{rtag}_{i}", with_bias=bool(bias),
-            bias_mode=epi["bias_mode"], activation=act, attrs=epi["attrs"], alpha=epi["alpha"],
-            beta=epi["beta"], residual=residual))
+            f"splitk_reduce{'4' if vec == 4 else ''}_{act or 'none'}_{epi['bias_mode']}{rtag}_{i}",
+            with_bias=bool(bias), bias_mode=epi["bias_mode"], activation=act, attrs=epi["attrs"],
+            alpha=epi["alpha"], beta=epi["beta"], residual=residual, vec=vec))
         self.plan.append(Launch(
-            "splitk_reduce", rname, [ws] + bias + extra, [out], (-(-(M * N) // 256), 1, 1),
+            "splitk_reduce", rname, [ws] + bias + extra, [out], (-(-(M * N) // (256 * vec)), 1, 1),
             (256, 1, 1),
             {"S": slices, "M": M, "N": N, "ldc": epi["ldc"], "hw": epi["hw"],
              "node": meta["node"], "bytes": 4 * (slices + 1 + len(extra)) * M * N}))

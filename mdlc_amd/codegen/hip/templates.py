@@ -180,8 +180,9 @@ def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: s
 
 def splitk_reduce_kernel(name: str, *, with_bias: bool, bias_mode: str,
                          activation: Optional[str], attrs: dict, alpha: float = 1.0,
-                         beta: float = 1.0, residual: Optional[str] = None) -> tuple:
-    """Split-K epilogue. ABI: (ws, [bias], [res], C, int S, int M, int N, int ldc, int hw)."""
+                         beta: float = 1.0, residual: Optional[str] = None, vec: int = 1) -> tuple:
+    """Split-K epilogue, ``vec`` (1 or 4) outputs per thread.
+    ABI: (ws, [bias], [res], C, int S, int M, int N, int ldc, int hw)."""
     epi = f"{name}_epi"
     src = epilogue_struct(epi, bias_mode=bias_mode if with_bias else None, activation=activation,
                           attrs=attrs, alpha=alpha, beta=beta, residual=residual)
@@ -191,7 +192,7 @@ def splitk_reduce_kernel(name: str, *, with_bias: bool, bias_mode: str,
         f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
         f"    const float* __restrict__ ws, {bias_arg}{res_arg}float* __restrict__ C, int S, int M,\n"
         "    int N, int ldc, int hw) {\n"
-        f"  mdlc::splitk_reduce_f32<{epi}>(ws, {'bias' if with_bias else 'nullptr'}, "
+        f"  mdlc::splitk_reduce_f32<{epi}, {int(vec)}>(ws, {'bias' if with_bias else 'nullptr'}, "
         f"{'res' if residual else 'nullptr'}, C, S, M, N, ldc, hw);\n}}\n")
 
 

@@ -223,6 +223,26 @@ def test_conv_residual_epilogue(post, res_first, sk, mode, hip_ctx):
     np.testing.assert_array_equal(got["z"], got2["z"])
 
 
+@pytest.mark.parametrize("case", [(2, 16, 16, 16, 32, 3, 1, 1), (1, 64, 14, 14, 128, 3, 1, 1)],
+                         ids=lambda c: "x".join(map(str, c)))
+def test_splitk_reduce_vector_and_scalar_forms_agree(case, hip_ctx, monkeypatch):
+    """The split-K reduce with four outputs per thread (here hw = 256, 196)
+    and with one give the same bits, and match the oracle."""
+    from mdlc_amd.codegen.hip import emit
+
+    sched = MfmaSchedule(64, 64, 16, 2, 2, 32, True, 5)
+    g, feeds = _conv_graph(*case)
+    c, got, want = device_run(g, feeds, ctx=hip_ctx, schedule_fn=lambda n, mnk: sched)
+    (red,) = [l for l in c.module.plan if l.kind == "splitk_reduce"]
+    assert red.kernel_name.startswith("splitk_reduce4_")
+    assert_close("y", got["y"], want["y"])
+    monkeypatch.setattr(emit, "REDUCE_VEC", 1)
+    g2, _ = _conv_graph(*case)
+    c2, got2, _ = device_run(g2, feeds, ctx=hip_ctx, schedule_fn=lambda n, mnk: sched)
+    assert not any(l.kernel_name.startswith("splitk_reduce4_") for l in c2.module.plan)
+    np.testing.assert_array_equal(got["y"], got2["y"])
+
+
 @pytest.mark.parametrize("n", [1, 2, 8])
 def test_conv_no_bias_no_act(n, hip_ctx):
     g, feeds = _conv_graph(n, 5, 11, 11, 6, 3, 1, 1, act=None, bias=False, seed=4)
