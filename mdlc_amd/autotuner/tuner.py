@@ -165,10 +165,11 @@ def is_implicit_conv(problem: dict) -> bool:
 
 
 def candidates(M: int, N: int, K: int, *, budget: int = 24, seed: int = 0, extra_random: int = 4,
-               conv: bool = False) -> list:
+               conv: bool = False, stream_k: int = 4) -> list:
     """The ``budget`` best schedules by the cost model, a seeded random few
-    more, and the shape-aware default (``conv``: implicit-GEMM convolution
-    schedules only)."""
+    more, the shape-aware default (``conv``: implicit-GEMM convolution
+    schedules only), and the stream-K form of the ``stream_k`` best unsplit
+    ones whose tile count is above the CU count and not a multiple of it."""
     space = list(gemm_search_space(SPLITS))
     space = [s for s in space if split_slices(K, s)[0] == s.SK or s.SK == 1]
     if conv:
@@ -181,7 +182,13 @@ def candidates(M: int, N: int, K: int, *, budget: int = 24, seed: int = 0, extra
     d = default_schedule(M, N, K)
     if d not in pick:
         pick.append(d)
+    uneven = [s for s in pick if s.SK == 1 and _tiles(s, M, N) > CUS and _tiles(s, M, N) % CUS]
+    pick += [s.with_stream_k() for s in uneven[:stream_k]]
     return pick
+
+
+def _tiles(s: MfmaSchedule, M: int, N: int) -> int:
+    return -(-M // s.BM) * -(-N // s.BN)
 
 
 def qcandidates(M: int, N: int, K: int, *, budget: int = 24, seed: int = 0,

@@ -13,6 +13,7 @@ extended because nothing runs on the host here:
   im2col      batched column matrix for the explicit conv path
   dwconv      direct depthwise convolution + epilogue
   splitk_reduce  sums split-K partial slices in order + epilogue
+  streamk_fixup  finishes the stream-K remainder tiles (pieces in K order + epilogue)
   quantize, qgemm, qconv, qdwconv, qadd, qlut, qgap, dequantize, qmlp,
   qconv_first (INT8 path, int8 activations channels-last on the device)
   elementwise fused pointwise chain (also single pointwise ops)
@@ -47,6 +48,7 @@ ScheduleFn = Callable[[Optional[Node], tuple], MfmaSchedule]
 
 VIEW_OPS = {"Flatten", "Reshape", "Identity", "Squeeze", "Unsqueeze"}
 REDUCE_VEC = 4        # outputs per thread of the split-K reduce where the layout allows (else 1)
+STREAM_K_WGS = 256    # stream-K workgroups: one per CU
 
 
 class HipCodegen(Int8LoweringMixin):
@@ -258,6 +260,10 @@ class HipCodegen(Int8LoweringMixin):
                epi["alpha"], epi["beta"], win, residual)
         meta = dict(meta, ksplit=slices, kchunk=chunk, ldc=epi["ldc"], hw=epi["hw"])
         meta.setdefault("ldb", 0)
+        if sched.ST and tiles % STREAM_K_WGS:
+            self._emit_stream_k(kind, sched, operands, bias, out, meta, epi, bmode=bmode,
+                                vec_a=vec_a, out_nchw=out_nchw, win=win, tiles=tiles)
+            return
         if slices == 1:
             kname = self._kernel(sig, lambda i: T.gemm_kernel(
                 f"{tag}_{sched.key()}_{act or 'none'}_{epi['bias_mode']}{rtag}_{i}", sched,
@@ -294,6 +300,45 @@ class HipCodegen(Int8LoweringMixin):
             (256, 1, 1),
             {"S": slices, "M": M, "N": N, "ldc": epi["ldc"], "hw": epi["hw"],
              "node": meta["node"], "bytes": 4 * (slices + 1 + len(extra)) * M * N}))
+
+    def _emit_stream_k(self, kind, sched, operands, bias, out, meta, epi, *, bmode, vec_a, out_nchw,
+                       win, tiles) -> None:
+        """Stream-K: the first ``full`` tiles (a multiple of the CU count) one
+        per workgroup, the remaining ones cut into equal K-step ranges over
+        STREAM_K_WGS more workgroups, whose pieces the fix-up launch adds."""
+        M, N, K = meta["M"], meta["N"], meta["K"]
+        full = tiles - tiles % STREAM_K_WGS
+        act = epi["act"]
+        tag = "conv" if kind == "conv" else "gemm"
+        residual, res = epi.get("residual"), epi.get("res_input")
+        extra = [res] if res else []
+        rtag = "_res" if residual else ""
+        ws = out + "__streamk"
+        self.scratch[ws] = (2 * STREAM_K_WGS * sched.BM, sched.BN)
+        self.scratch_class[ws] = "splitk"
+        sig = (kind, sched, bool(bias), epi["bias_mode"], epi["act_sig"], bmode, out_nchw, vec_a,
+               epi["alpha"], epi["beta"], win, residual, "streamk")
+        kname = self._kernel(sig, lambda i: T.gemm_kernel(
+            f"{tag}_{sched.key()}_ST_{act or 'none'}_{epi['bias_mode']}{rtag}_{i}", sched,
+            with_bias=bool(bias), bias_mode=epi["bias_mode"], activation=act,
+            attrs=epi["attrs"], alpha=epi["alpha"], beta=epi["beta"], bmode=bmode,
+            out_nchw=out_nchw, vec_a=vec_a, win=win, residual=residual, stream_k=STREAM_K_WGS))
+        self.plan.append(Launch(kind, kname, operands + bias + extra + [ws], [out],
+                                (full + STREAM_K_WGS, 1, 1), (sched.threads_per_block(), 1, 1),
+                                dict(meta, ksplit=full, kchunk=K, stream_k=True)))
+        fsig = ("streamk_fixup", sched.BM, sched.BN, sched.BK, bool(bias), epi["bias_mode"],
+                epi["act_sig"], epi["alpha"], epi["beta"], residual)
+        fname = self._kernel(fsig, lambda i: T.streamk_fixup_kernel(
+            f"streamk_fixup_{act or 'none'}_{epi['bias_mode']}{rtag}_{i}", sched, STREAM_K_WGS,
+            with_bias=bool(bias), bias_mode=epi["bias_mode"], activation=act, attrs=epi["attrs"],
+            alpha=epi["alpha"], beta=epi["beta"], residual=residual))
+        rest = tiles - full
+        self.plan.append(Launch(
+            "streamk_fixup", fname, [ws] + bias + extra, [out],
+            (rest * (sched.BM * sched.BN // 1024), 1, 1), (256, 1, 1),
+            {"M": M, "N": N, "K": K, "full": full, "ldc": epi["ldc"], "hw": epi["hw"],
+             "node": meta["node"],
+             "bytes": 4 * rest * sched.BM * sched.BN * (2 + len(extra))}))
 
     def _lower_dwconv(self, g: Graph, node: Node, geo: dict, has_bias: bool) -> None:
         if geo["ICG"] != 1 or geo["OC"] % geo["C"] != 0:

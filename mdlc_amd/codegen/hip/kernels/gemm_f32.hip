@@ -69,16 +69,22 @@ struct GemmArgs {
   float* __restrict__ C;
   int M, N, K, lda, ldb, ldc, hw;
   int Cin, H, W, OH, OW;         // conv input / output geometry (BMODE >= 2)
-  int ksplit, kchunk;            // K slices (grid = tiles * ksplit) and slice depth
+  int ksplit, kchunk;            // K slices (grid = tiles * ksplit) and slice depth; with
+                                 // stream-K, ksplit = the tiles done whole (see gemm_f32_mfma)
+  float* __restrict__ ws;        // stream-K partial-tile workspace [2 * SKW][BM * BN]
 };
 
 __device__ __forceinline__ float pick(const float4& v, int q) {
   return q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w;
 }
 
+// One output tile [m0, m0+BM) x [n0, n0+BN) over K range [kbeg, kend). slot < 0:
+// the epilogue for OUT (slice ks of a split-K workspace for OUT == 2); slot
+// >= 0: raw sums into the stream-K workspace, tile-local rows of BN.
 template <int BM, int BN, int BK, int WGM, int WGN, int MS, bool DB, bool VA, int BMODE, int OUT,
           class Epi, class Win>
-__device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
+__device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0, int kbeg, int kend,
+                                              int ks, int slot) {
   constexpr int NT = WGM * WGN * 64;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int MI = WM / MS, NI = WN / MS;
@@ -105,18 +111,6 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
   const int li = lane % MS;
   const int lk = lane / MS;
 
-  const int tiles_m = (g.M + BM - 1) / BM;
-  const int tiles_n = (g.N + BN - 1) / BN;
-  const int tiles = tiles_m * tiles_n;
-  // Logical order (slice, n-block, m-block), m fastest: workgroups sharing a
-  // B slab are consecutive and land on the same XCD.
-  const int t = xcd_remap(blockIdx.x, tiles * g.ksplit);
-  const int ks = t / tiles;
-  const int tt = t - ks * tiles;
-  const int m0 = (tt % tiles_m) * BM;
-  const int n0 = (tt / tiles_m) * BN;
-  const int kbeg = ks * g.kchunk;
-  const int kend = min(g.K, kbeg + g.kchunk);
 
   // ---- A staging: addresses fixed per thread, advanced by k0 --------------
   constexpr int A_ELEMS = VA ? BM * BK / 4 : BM * BK;
@@ -341,6 +335,19 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
   }
 
   // ---- epilogue: bias + activation, scatter to the output layout ---------
+  if (slot >= 0) {                     // stream-K piece: raw sums, tile-local
+    float* wp = g.ws + (size_t)slot * BM * BN;
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) {
+      const int c = wn0 + ni * MS + li;
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int r = 0; r < Mfma<MS>::kAcc; ++r)
+          wp[(wm0 + mi * MS + (r / 4) * 8 + lk * 4 + (r % 4)) * BN + c] = acc[mi][ni][r];
+    }
+    return;
+  }
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
     const int col = n0 + wn0 + ni * MS + li;
@@ -377,6 +384,137 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
           }
         }
       }
+  }
+}
+
+// Entry. Without stream-K (SKW == 0) workgroup b owns one (K slice, tile):
+// logical order (slice, n-block, m-block), m fastest, so workgroups sharing a
+// B slab are consecutive and land on the same XCD.
+//
+// With stream-K (SKW > 0 workgroups): the first ksplit tiles (a multiple of
+// the CU count) are done whole, one per workgroup; the remaining R tiles'
+// R * KT K steps (KT = ceil(K / BK)) are cut into SKW equal contiguous
+// ranges, one per extra workgroup, so every CU gets the same amount of work
+// instead of some CUs one tile more than others. R < SKW, so a range covers
+// at most two (partial) tiles; piece p of workgroup j writes its raw sums
+// to workspace slot 2j + p and streamk_fixup_f32 adds each tile's pieces in
+// K order and applies the epilogue.
+template <int BM, int BN, int BK, int WGM, int WGN, int MS, bool DB, bool VA, int BMODE, int OUT,
+          class Epi, class Win, int SKW = 0>
+__device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
+  const int tiles_m = (g.M + BM - 1) / BM;
+  const int tiles_n = (g.N + BN - 1) / BN;
+  const int tiles = tiles_m * tiles_n;
+  if (SKW == 0) {
+    const int t = xcd_remap(blockIdx.x, tiles * g.ksplit);
+    const int ks = t / tiles;
+    const int tt = t - ks * tiles;
+    const int kbeg = ks * g.kchunk;
+    gemm_f32_tile<BM, BN, BK, WGM, WGN, MS, DB, VA, BMODE, OUT, Epi, Win>(
+        g, (tt % tiles_m) * BM, (tt / tiles_m) * BN, kbeg, min(g.K, kbeg + g.kchunk), ks, -1);
+    return;
+  }
+  // One call site for whole tiles and pieces, so that the tile body is
+  // inlined once: a whole tile is the step range [tt*KT, (tt+1)*KT).
+  const int full = g.ksplit;
+  const int b = blockIdx.x;
+  const int KT = (g.K + BK - 1) / BK;
+  long long it, it1;
+  int slot = -1;
+  if (b < full) {
+    it = (long long)xcd_remap(b, full) * KT;
+    it1 = it + KT;
+  } else {
+    const int j = b - full;
+    const long long total = (long long)(tiles - full) * KT;
+    it = (long long)full * KT + j * total / SKW;
+    it1 = (long long)full * KT + (j + 1) * total / SKW;
+    slot = 2 * j;
+  }
+  while (it < it1) {
+    const int tt = (int)(it / KT);
+    const int k0 = (int)(it - (long long)tt * KT);
+    const int k1 = (int)min((long long)KT, k0 + (it1 - it));
+    gemm_f32_tile<BM, BN, BK, WGM, WGN, MS, DB, VA, BMODE, OUT, Epi, Win>(
+        g, (tt % tiles_m) * BM, (tt / tiles_m) * BN, k0 * BK, min(g.K, k1 * BK), 0, slot);
+    it += k1 - k0;
+    if (slot >= 0) ++slot;
+  }
+}
+
+// Stream-K fix-up: ``BM * BN / 1024`` workgroups per partially computed tile
+// (the tiles after the first ``full``), four tile elements per thread. The
+// pieces of tile u came from the consecutive workgroups whose K-step ranges
+// overlap [u*KT, (u+1)*KT); up to eight of them are loaded at once and added
+// in that (K) order, then bias, activation and the folded residual, and the
+// elements are scattered like the main epilogue (row-major or NCHW).
+template <class Epi, int BM, int BN, int BK, int SKW>
+__device__ __forceinline__ void streamk_fixup_f32(const float* __restrict__ ws,
+                                                  const float* __restrict__ bias,
+                                                  const float* __restrict__ res,
+                                                  float* __restrict__ C, int M, int N, int K,
+                                                  int full, int ldc, int hw) {
+  constexpr int CHUNKS = BM * BN / 1024;
+  static_assert(BM * BN % 1024 == 0, "fix-up tile split");
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles = tiles_m * ((N + BN - 1) / BN);
+  const int KT = (K + BK - 1) / BK;
+  const long long total = (long long)(tiles - full) * KT;
+  const int u = blockIdx.x / CHUNKS;
+  const int e = ((blockIdx.x - u * CHUNKS) * 256 + threadIdx.x) * 4;
+  const int tt = full + u;
+  const int m0 = (tt % tiles_m) * BM, n0 = (tt / tiles_m) * BN;
+  const long long lo = (long long)u * KT, hi = lo + KT;
+  // contributors j0 .. j1 - 1: the workgroups whose ranges meet [lo, hi)
+  int j0 = (int)(lo * SKW / total);
+  while (j0 > 0 && j0 * total / SKW > lo) --j0;
+  while ((j0 + 1) * total / SKW <= lo) ++j0;
+  int j1 = (int)((hi - 1) * SKW / total) + 1;
+  while (j1 < SKW && j1 * total / SKW < hi) ++j1;
+  while (j1 - 1 > j0 && (j1 - 1) * total / SKW >= hi) --j1;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  bool first = true;
+  for (int jb = j0; jb < j1; jb += 8) {
+    float4 p[8];
+    bool has[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {                        // issue the batch's loads together
+      const int j = jb + q;
+      const long long a = j * total / SKW, z = (j + 1) * total / SKW;
+      has[q] = j < j1 && z > a;                          // skip empty ranges
+      const int piece = (a >= lo) ? 0 : 1;               // which of j's pieces covers tile u
+      if (has[q]) p[q] = ld4(ws + (size_t)(2 * j + piece) * BM * BN + e);
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      if (!has[q]) continue;
+      if (first) {
+        v = p[q];
+      } else {
+        v.x += p[q].x; v.y += p[q].y; v.z += p[q].z; v.w += p[q].w;
+      }
+      first = false;
+    }
+  }
+  const int r = e / BN, c = e - (e / BN) * BN;
+  const int row = m0 + r;
+  if (row >= M) return;
+  const float vs[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int col = n0 + c + i;
+    if (col >= N) break;
+    const float b = Epi::bias == 1 ? bias[row] : (Epi::bias == 2 ? bias[col] : 0.f);
+    float x = Epi::apply(vs[i], b);
+    size_t o;
+    if (hw > 0) {
+      const int n = col / hw;
+      o = ((size_t)n * M + row) * hw + (col - n * hw);
+    } else {
+      o = (size_t)row * ldc + col;
+    }
+    if (Epi::residual) x = Epi::post(x, res[o]);
+    C[o] = x;
   }
 }
 

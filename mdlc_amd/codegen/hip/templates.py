@@ -123,7 +123,7 @@ def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: s
                 activation: Optional[str] = None, attrs: Optional[dict] = None,
                 alpha: float = 1.0, beta: float = 1.0, bmode: int = 0, out_nchw: bool = False,
                 vec_a: bool = True, win: Optional[tuple] = None,
-                residual: Optional[str] = None) -> tuple:
+                residual: Optional[str] = None, stream_k: int = 0) -> tuple:
     """(name, source) of one GEMM instantiation.
 
     Kernel ABI (the reference's gemm ABI plus trailing layout arguments):
@@ -136,7 +136,10 @@ def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: s
     body of the epilogue's ``post``). With ``sched.SK > 1`` the kernel writes
     raw partial sums of each K slice to its C argument (the split-K
     workspace) and takes no bias or residual; the epilogue then lives in
-    ``splitk_reduce_kernel``.
+    ``splitk_reduce_kernel``. With ``stream_k`` = SKW > 0 a workspace pointer
+    ``ws`` precedes the output, ``ksplit`` is the number of tiles done whole
+    and the last SKW workgroups compute the remaining tiles in pieces
+    (``streamk_fixup_kernel`` finishes them).
     """
     attrs = attrs or {}
     s = sched
@@ -155,25 +158,27 @@ def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: s
     out = 2 if split else (1 if out_nchw else 0)
     tmpl = (f"mdlc::gemm_f32_mfma<{s.BM}, {s.BN}, {s.BK}, {s.WGM}, {s.WGN}, {s.MS}, "
             f"{'true' if s.DB else 'false'}, {'true' if vec_a else 'false'}, {bmode}, "
-            f"{out}, {epi}, {winty}>")
+            f"{out}, {epi}, {winty}, {int(stream_k)}>")
     nt = s.threads_per_block()
+    ws_arg = "float* __restrict__ ws, " if stream_k else ""
+    ws_val = ", ws" if stream_k else ""
     if bmode >= 2:
         src.append(
             f'extern "C" __global__ __launch_bounds__({nt}) void {name}(\n'
-            f"    const float* __restrict__ A, const float* __restrict__ x, {bias_arg}"
+            f"    const float* __restrict__ A, const float* __restrict__ x, {bias_arg}{ws_arg}"
             f"float* __restrict__ y,\n    int M, int N, int K, int lda, int Cin, int H, int W, "
             f"int OH, int OW, int ksplit, int kchunk) {{\n"
             f"  mdlc::GemmArgs g{{A, x, {bias_val}, y, M, N, K, lda, 0, 0, OH * OW, Cin, H, W, OH, OW, "
-            f"ksplit, kchunk}};\n"
+            f"ksplit, kchunk{ws_val}}};\n"
             f"  {tmpl}(g);\n}}\n")
     else:
         src.append(
             f'extern "C" __global__ __launch_bounds__({nt}) void {name}(\n'
-            f"    const float* __restrict__ A, const float* __restrict__ B, {bias_arg}"
+            f"    const float* __restrict__ A, const float* __restrict__ B, {bias_arg}{ws_arg}"
             f"float* __restrict__ C,\n    int M, int N, int K, int lda, int ldb, int ldc, int hw, "
             f"int ksplit, int kchunk) {{\n"
             f"  mdlc::GemmArgs g{{A, B, {bias_val}, C, M, N, K, lda, ldb, ldc, hw, 0, 0, 0, 0, 0, "
-            f"ksplit, kchunk}};\n"
+            f"ksplit, kchunk{ws_val}}};\n"
             f"  {tmpl}(g);\n}}\n")
     return name, "\n".join(src)
 
@@ -194,6 +199,28 @@ def splitk_reduce_kernel(name: str, *, with_bias: bool, bias_mode: str,
         "    int N, int ldc, int hw) {\n"
         f"  mdlc::splitk_reduce_f32<{epi}, {int(vec)}>(ws, {'bias' if with_bias else 'nullptr'}, "
         f"{'res' if residual else 'nullptr'}, C, S, M, N, ldc, hw);\n}}\n")
+
+
+def streamk_fixup_kernel(name: str, sched: MfmaSchedule, skw: int, *, with_bias: bool,
+                         bias_mode: str, activation: Optional[str], attrs: dict,
+                         alpha: float = 1.0, beta: float = 1.0,
+                         residual: Optional[str] = None) -> tuple:
+    """Stream-K fix-up: sums the pieces of each remainder tile and applies
+    the epilogue. ABI: (ws, [bias], [res], C, int M, int N, int K, int full,
+    int ldc, int hw); BM * BN / 1024 workgroups of 256 threads per
+    remainder tile, four elements per thread."""
+    epi = f"{name}_epi"
+    src = epilogue_struct(epi, bias_mode=bias_mode if with_bias else None, activation=activation,
+                          attrs=attrs, alpha=alpha, beta=beta, residual=residual)
+    bias_arg = "const float* __restrict__ bias, " if with_bias else ""
+    res_arg = "const float* __restrict__ res, " if residual else ""
+    return name, src + (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        f"    const float* __restrict__ ws, {bias_arg}{res_arg}float* __restrict__ C, int M, int N,\n"
+        "    int K, int full, int ldc, int hw) {\n"
+        f"  mdlc::streamk_fixup_f32<{epi}, {sched.BM}, {sched.BN}, {sched.BK}, {int(skw)}>(ws, "
+        f"{'bias' if with_bias else 'nullptr'}, {'res' if residual else 'nullptr'}, C, M, N, K, full, "
+        "ldc, hw);\n}\n")
 
 
 def im2col_kernel(name: str = "im2col") -> tuple:

@@ -38,6 +38,7 @@ class MfmaSchedule:
     MS: int = 32
     DB: bool = True
     SK: int = 1
+    ST: bool = False        # stream-K remainder (fp32 GEMM/conv, SK == 1): see gemm_f32_mfma
 
     def threads_per_block(self) -> int:
         return 64 * self.WGM * self.WGN
@@ -58,6 +59,8 @@ class MfmaSchedule:
 
     def is_valid(self) -> bool:
         if min(self.BM, self.BN, self.BK, self.WGM, self.WGN, self.SK) <= 0 or self.MS not in (16, 32):
+            return False
+        if self.ST and self.SK != 1:
             return False
         wm, wn = self.wave_tile()
         if self.BM % self.WGM or self.BN % self.WGN:
@@ -89,10 +92,13 @@ class MfmaSchedule:
                 f"_M{self.MS}{'_DB' if self.DB else ''}")
 
     def key_full(self) -> str:
-        return self.key() + (f"_SK{self.SK}" if self.SK > 1 else "")
+        return self.key() + (f"_SK{self.SK}" if self.SK > 1 else "") + ("_ST" if self.ST else "")
 
     def with_split(self, sk: int) -> "MfmaSchedule":
         return MfmaSchedule(self.BM, self.BN, self.BK, self.WGM, self.WGN, self.MS, self.DB, sk)
+
+    def with_stream_k(self) -> "MfmaSchedule":
+        return MfmaSchedule(self.BM, self.BN, self.BK, self.WGM, self.WGN, self.MS, self.DB, 1, True)
 
     def as_dict(self) -> dict:
         return asdict(self)

@@ -31,6 +31,8 @@ SCHEDULES = [
     MfmaSchedule(256, 128, 16, 4, 2, 32, True),
     MfmaSchedule(64, 64, 16, 2, 2, 32, True, 3),       # split-K, ragged last slice
     MfmaSchedule(32, 32, 16, 1, 1, 16, True, 2),       # split-K with 16x16x4
+    MfmaSchedule(32, 32, 16, 1, 1, 16, True, 1, True),  # stream-K: every tile in pieces
+    MfmaSchedule(64, 64, 16, 2, 2, 32, False, 1, True),
 ]
 
 
@@ -202,14 +204,15 @@ def _conv_residual_graph(post, res_first, seed=9):
 
 
 @pytest.mark.parametrize("mode", ["implicit", "im2col"])
-@pytest.mark.parametrize("sk", [1, 3])
+@pytest.mark.parametrize("sk", [1, 3, "stream"])
 @pytest.mark.parametrize("post,res_first", [("relu", False), ("relu", True), ("clip", False),
                                             ("none", True)])
 def test_conv_residual_epilogue(post, res_first, sk, mode, hip_ctx):
     """A residual add (+ Relu / Clip / nothing) folded into the conv epilogue
-    (or the split-K reduce) matches the oracle and equals the unfused
-    device result bit for bit."""
-    sched = MfmaSchedule(64, 64, 16, 2, 2, 32, True, sk)
+    (or the split-K reduce, or the stream-K fix-up) matches the oracle and
+    equals the unfused device result bit for bit."""
+    sched = (MfmaSchedule(64, 64, 16, 2, 2, 32, True).with_stream_k() if sk == "stream"
+             else MfmaSchedule(64, 64, 16, 2, 2, 32, True, sk))
     g, feeds = _conv_residual_graph(post, res_first)
     c, got, want = device_run(g, feeds, conv_mode=mode, ctx=hip_ctx,
                               schedule_fn=lambda n, mnk: sched)
@@ -221,6 +224,39 @@ def test_conv_residual_epilogue(post, res_first, sk, mode, hip_ctx):
                              schedule_fn=lambda n, mnk: sched, fuse_residual=False)
     assert not any(n.attrs.get("residual_subgraph") for n in c2.graph.nodes)
     np.testing.assert_array_equal(got["z"], got2["z"])
+
+
+@pytest.mark.parametrize("mode", ["implicit", "im2col"])
+@pytest.mark.parametrize("case", [(2, 16, 14, 14, 32, 3, 1, 1), (5, 16, 64, 64, 64, 3, 1, 1),
+                                  (1, 64, 7, 7, 128, 3, 1, 1), (3, 24, 33, 33, 40, 3, 2, 1)],
+                         ids=lambda c: "x".join(map(str, c)))
+def test_conv_stream_k(case, mode, hip_ctx):
+    """Stream-K: with fewer tiles than CUs every tile is assembled from
+    pieces (some one K step long); with 320 tiles the first 256 are done whole
+    and the other 64 in pieces. Correct on the first run and on a repeat with
+    another input in between (the workspace is rewritten every run), and the
+    same bits every time (pieces are added in K order)."""
+    from mdlc_amd.codegen.hip.hip_executor import HipExecutor
+    from mdlc_amd.compiler import compile_graph
+    from oracle.reference import run_reference
+
+    sched = MfmaSchedule(64, 64, 16, 2, 2, 32, True).with_stream_k()
+    g, feeds = _conv_graph(*case)
+    c = compile_graph(g, feeds=feeds, conv_mode=mode, schedule_fn=lambda n, mnk: sched)
+    kinds = [l.kind for l in c.module.plan]
+    assert kinds[-1] == "streamk_fixup"
+    main = c.module.plan[-2]
+    assert main.meta["stream_k"] and main.grid[0] == main.meta["ksplit"] + 256
+    ex = HipExecutor(c.module, hip_ctx)
+    try:
+        y1 = ex.run(feeds)["outputs"]["y"]
+        ex.run({"x": (feeds["x"][::-1] * 0.5).copy()})
+        y2 = ex.run(feeds)["outputs"]["y"]
+    finally:
+        ex.close()
+    want = run_reference(c.graph, feeds)["y"]
+    assert_close("y", y1, want)
+    np.testing.assert_array_equal(y1, y2)
 
 
 @pytest.mark.parametrize("case", [(2, 16, 16, 16, 32, 3, 1, 1), (1, 64, 14, 14, 128, 3, 1, 1)],
