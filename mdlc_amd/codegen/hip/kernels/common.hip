@@ -20,4 +20,17 @@ __device__ __forceinline__ int xcd_remap(int b, int total) {
   return x * q + (x < r ? x : r) + j;
 }
 
+// Logical tile t -> (m tile, n tile), down M in groups of GM rows of tiles:
+// the tiles one XCD runs together then share GM row blocks of A and a few
+// column blocks of B instead of every row block of A. With tiles_m <= GM this
+// is plain column order. A bijection onto the tile grid.
+template <int GM>
+__device__ __forceinline__ void grouped_tile(int t, int tiles_m, int tiles_n, int& mt, int& nt) {
+  const int grp = t / (GM * tiles_n);
+  const int gsz = min(tiles_m - grp * GM, GM);
+  const int tg = t - grp * GM * tiles_n;
+  mt = grp * GM + tg % gsz;
+  nt = tg / gsz;
+}
+
 }  // namespace mdlc

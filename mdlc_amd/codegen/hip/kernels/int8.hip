@@ -214,9 +214,10 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
 
   const int tiles_m = (g.M + BM - 1) / BM;
   const int tiles_n = (g.N + BN - 1) / BN;
-  const int t = xcd_remap(blockIdx.x, tiles_m * tiles_n);
-  const int m0 = (t % tiles_m) * BM;
-  const int n0 = (t / tiles_m) * BN;
+  int mt, nt;
+  grouped_tile<16>(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, mt, nt);
+  const int m0 = mt * BM;
+  const int n0 = nt * BN;
 
   const int kc = tid % CPR;
   const int r0 = tid / CPR;
