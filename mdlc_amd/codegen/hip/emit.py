@@ -10,6 +10,8 @@ extended because nothing runs on the host here:
 
   gemm        dense GEMM + epilogue (Gemm/MatMul, and conv after im2col)
   conv        implicit-GEMM convolution (no column buffer)
+  conv_smallc direct convolution for few input channels (stems): input patch
+              in LDS, weights in registers, matrix cores
   im2col      batched column matrix for the explicit conv path
   dwconv      direct depthwise convolution + epilogue
   splitk_reduce  sums split-K partial slices in order + epilogue
@@ -39,7 +41,8 @@ import numpy as np
 from mdlc_amd.codegen.hip import templates as T
 from mdlc_amd.codegen.hip.emit_int8 import Int8LoweringMixin
 from mdlc_amd.codegen.hip.plan import LIBRARY_PARTS, QUANT_OPS, HipModule, Launch, round4, round16  # noqa: F401
-from mdlc_amd.codegen.schedule import MfmaSchedule, default_schedule, split_slices
+from mdlc_amd.codegen.schedule import (MfmaSchedule, default_schedule, smallc_fits, smallc_pairs,
+                                      smallc_tile, split_slices)
 from mdlc_amd.ir import Graph, Node
 from mdlc_amd.passes.fuse_elementwise import ELEMENTWISE
 from mdlc_amd.passes.shape_inference import conv_geometry
@@ -49,14 +52,16 @@ ScheduleFn = Callable[[Optional[Node], tuple], MfmaSchedule]
 VIEW_OPS = {"Flatten", "Reshape", "Identity", "Squeeze", "Unsqueeze"}
 REDUCE_VEC = 4        # outputs per thread of the split-K reduce where the layout allows (else 1)
 STREAM_K_WGS = 256    # stream-K workgroups: one per CU
+SMALLC_WGS = 512      # workgroups stepping through the blocks of the small-channel conv
 
 
 class HipCodegen(Int8LoweringMixin):
     def __init__(self, schedule_fn: Optional[ScheduleFn] = None, *, conv_mode: str = "implicit",
-                 int8_depthwise: str = "mfma") -> None:
+                 int8_depthwise: str = "mfma", small_conv: bool = True) -> None:
         """``int8_depthwise``: "mfma" runs 16-channel-aligned int8 depthwise
         convs as block-diagonal GEMMs on the matrix cores, "vector" keeps
-        them on the per-pixel vector kernel."""
+        them on the per-pixel vector kernel. ``small_conv``: convs with few
+        input channels take the direct kernel (implicit mode)."""
         if conv_mode not in ("implicit", "im2col"):
             raise ValueError(f"conv_mode must be 'implicit' or 'im2col', not {conv_mode!r}")
         if int8_depthwise not in ("mfma", "vector"):
@@ -68,6 +73,7 @@ class HipCodegen(Int8LoweringMixin):
             schedule_fn = tuned_schedules()
         self.schedule_fn = schedule_fn
         self.conv_mode = conv_mode
+        self.small_conv = small_conv
         self.kernels: dict = {}
         self.plan: list = []
         self.scratch: dict = {}
@@ -175,6 +181,10 @@ class HipCodegen(Int8LoweringMixin):
         if geo["group"] != 1:
             self._lower_dwconv(g, node, geo, has_bias)
             return
+        if self.conv_mode == "implicit" and self.small_conv and smallc_fits(geo["C"], geo["KH"], geo["KW"], geo["DH"],
+                                                        geo["DW"]):
+            self._lower_conv_smallc(g, node, geo, has_bias)
+            return
         OC, K = geo["OC"], geo["C"] * geo["KH"] * geo["KW"]
         OH, OW, N = geo["OH"], geo["OW"], geo["N"]
         P = N * OH * OW
@@ -227,6 +237,44 @@ class HipCodegen(Int8LoweringMixin):
         meta.update({"ldb": ldc})
         self._emit_gemm("gemm", sched, [wdev, cols], bias, y, meta, epi, bmode=0, vec_a=True,
                         out_nchw=True)
+
+    def _lower_conv_smallc(self, g: Graph, node: Node, geo: dict, has_bias: bool) -> None:
+        """A conv with few input channels (a network's stem): the direct
+        matrix-core kernel, input patch in LDS and weights in registers. The
+        weights are packed here as [channel block][pair i][lane], lane =
+        (k % 2) * 32 + oc % 32, k = 2i + k % 2 in (c, kh, kw) order with kw
+        padded to even (zero weights)."""
+        C, KH, KW = geo["C"], geo["KH"], geo["KW"]
+        OC, OH, OW, N = geo["OC"], geo["OH"], geo["OW"], geo["N"]
+        x, w, y = node.inputs[0], node.inputs[1], node.outputs[0]
+        a = node.attrs
+        TR, TC, OCW = smallc_tile(N, OC, OH, OW)
+        kwp = KW + (KW & 1)
+        npair = smallc_pairs(C, KH, KW)
+        nblk = -(-OC // (32 * OCW)) * OCW
+        wpad = np.zeros((nblk * 32, C, KH, kwp), np.float32)
+        wpad[:OC, :, :, :KW] = np.asarray(g.initializers[w], np.float32).reshape(OC, C, KH, KW)
+        packed = wpad.reshape(nblk, 32, npair, 2).transpose(0, 2, 3, 1).reshape(nblk, npair, 64)
+        wdev = self._pack(f"{w}__dev_smallc", packed)
+        bias = [node.inputs[2]] if has_bias else []
+        res = self._residual_epilogue(g, node)
+        extra = [res["res_input"]] if res["res_input"] else []
+        win = (C, KH, KW, geo["SH"], geo["SW"], geo["PT"], geo["PL"])
+        act = a.get("activation")
+        sig = ("conv_smallc", win, (TR, TC, OCW), has_bias, self._act_sig(a), res["residual"])
+        kname = self._kernel(sig, lambda i: T.conv_smallc_kernel(
+            f"conv_smallc_{KH}x{KW}s{geo['SH']}_{act or 'none'}{'_res' if extra else ''}_{i}", win,
+            (TR, TC, OCW), with_bias=has_bias, activation=act, attrs=self._act_attrs(a),
+            residual=res["residual"]))
+        P, K = N * OH * OW, C * KH * KW
+        grid = (min(N * -(-OH // TR) * -(-OW // TC), SMALLC_WGS), nblk // OCW, 1)
+        self.plan.append(Launch(
+            "conv_smallc", kname, [x, wdev] + bias + extra, [y], grid, (256, 1, 1),
+            {"M": OC, "N": P, "K": K, "batch": N, "H": geo["H"], "W": geo["W"], "OC": OC,
+             "OH": OH, "OW": OW,
+             "tile": (TR, TC, OCW), "node": node, "flops": 2 * OC * P * K,
+             "bytes": 4 * (N * C * geo["H"] * geo["W"] + OC * K + P * OC * (1 + len(extra))
+                           + (OC if has_bias else 0))}))
 
     def _residual_epilogue(self, g: Graph, node: Node) -> dict:
         """``residual`` (the epilogue's post() body) and ``res_input`` for a
@@ -515,5 +563,7 @@ class HipCodegen(Int8LoweringMixin):
 
 
 def emit_hip_module(graph: Graph, schedule_fn: Optional[ScheduleFn] = None, *,
-                    conv_mode: str = "implicit", int8_depthwise: str = "mfma") -> HipModule:
-    return HipCodegen(schedule_fn, conv_mode=conv_mode, int8_depthwise=int8_depthwise).lower(graph)
+                    conv_mode: str = "implicit", int8_depthwise: str = "mfma",
+                    small_conv: bool = True) -> HipModule:
+    return HipCodegen(schedule_fn, conv_mode=conv_mode, int8_depthwise=int8_depthwise,
+                      small_conv=small_conv).lower(graph)

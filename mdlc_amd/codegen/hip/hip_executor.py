@@ -118,6 +118,9 @@ class HipExecutor:
             args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
             args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["Cin"]), I(m["H"]),
                      I(m["W"]), I(m["OH"]), I(m["OW"]), I(m["ksplit"]), I(m["kchunk"])]
+        elif k == "conv_smallc":
+            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+            args += [I(m[f]) for f in ("batch", "H", "W", "OC", "OH", "OW")]
         elif k == "streamk_fixup":
             args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
             args += [I(m[f]) for f in ("M", "N", "K", "full", "ldc", "hw")]

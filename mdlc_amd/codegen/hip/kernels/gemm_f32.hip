@@ -348,42 +348,94 @@ __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0,
     }
     return;
   }
+  // Output offsets first, then every epilogue operand (bias, residual) is
+  // loaded before the first store: the stores go through a pointer the
+  // compiler cannot separate from the operands, so a load placed after a
+  // store would wait out a full memory round trip per output.
+  constexpr int KA = Mfma<MS>::kAcc;
+  size_t cofs[NI];
+  bool cok[NI];
+  int rstride;
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
     const int col = n0 + wn0 + ni * MS + li;
-    if (col >= g.N) continue;
-    size_t cofs;
-    int rstride;
+    cok[ni] = col < g.N;
     if (OUT == 2) {
-      cofs = (size_t)ks * g.M * g.N + col;
+      cofs[ni] = (size_t)ks * g.M * g.N + col;
       rstride = g.N;
     } else if (OUT == 1) {
-      int n = col / g.hw;
-      int s = col - n * g.hw;
-      cofs = (size_t)n * g.M * g.hw + s;
+      const int n = col / g.hw;
+      cofs[ni] = (size_t)n * g.M * g.hw + (col - n * g.hw);
       rstride = g.hw;
     } else {
-      cofs = col;
+      cofs[ni] = col;
       rstride = g.ldc;
     }
-    const float bcol = (OUT != 2 && Epi::bias == 2) ? g.bias[col] : 0.f;
+  }
+  float brow[MI][KA], bcol[NI], rv[NI][MI][KA];
+  if (OUT != 2) {
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-      for (int r = 0; r < Mfma<MS>::kAcc; ++r) {
+      for (int r = 0; r < KA; ++r) {
         const int row = m0 + wm0 + mi * MS + (r / 4) * 8 + lk * 4 + (r % 4);
-        if (row < g.M) {
-          if (OUT == 2) {
-            g.C[cofs + (size_t)row * rstride] = acc[mi][ni][r];
-          } else {
-            const float bv = (Epi::bias == 1) ? g.bias[row] : bcol;
-            const size_t o = cofs + (size_t)row * rstride;
-            float v = Epi::apply(acc[mi][ni][r], bv);
-            if (Epi::residual) v = Epi::post(v, g.R[o]);
-            g.C[o] = v;
+        brow[mi][r] = (Epi::bias == 1 && row < g.M) ? g.bias[row] : 0.f;
+      }
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+      bcol[ni] = (Epi::bias == 2 && cok[ni]) ? g.bias[n0 + wn0 + ni * MS + li] : 0.f;
+    if (Epi::residual) {
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+          for (int r = 0; r < KA; ++r) {
+            const int row = m0 + wm0 + mi * MS + (r / 4) * 8 + lk * 4 + (r % 4);
+            rv[ni][mi][r] = (cok[ni] && row < g.M) ? g.R[cofs[ni] + (size_t)row * rstride] : 0.f;
           }
+    }
+  }
+  // every output value is formed before the first store, and a tile that
+  // lies wholly inside M x N stores without per-element branches, so no
+  // store waits on an operand load or on the previous store
+  float outv[NI][MI][KA];
+#pragma unroll
+  for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int r = 0; r < KA; ++r) {
+        if (OUT == 2) {
+          outv[ni][mi][r] = acc[mi][ni][r];
+        } else {
+          float v = Epi::apply(acc[mi][ni][r], Epi::bias == 1 ? brow[mi][r] : bcol[ni]);
+          if (Epi::residual) v = Epi::post(v, rv[ni][mi][r]);
+          outv[ni][mi][r] = v;
         }
       }
+  if (m0 + BM <= g.M && n0 + BN <= g.N) {
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int r = 0; r < KA; ++r) {
+          const int row = m0 + wm0 + mi * MS + (r / 4) * 8 + lk * 4 + (r % 4);
+          g.C[cofs[ni] + (size_t)row * rstride] = outv[ni][mi][r];
+        }
+  } else {
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) {
+      if (!cok[ni]) continue;
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int r = 0; r < KA; ++r) {
+          const int row = m0 + wm0 + mi * MS + (r / 4) * 8 + lk * 4 + (r % 4);
+          if (row < g.M) g.C[cofs[ni] + (size_t)row * rstride] = outv[ni][mi][r];
+        }
+    }
   }
 }
 
@@ -500,21 +552,35 @@ __device__ __forceinline__ void streamk_fixup_f32(const float* __restrict__ ws,
   const int row = m0 + r;
   if (row >= M) return;
   const float vs[4] = {v.x, v.y, v.z, v.w};
+  // offsets and epilogue operands for all four elements before any store
+  size_t o[4];
+  float b[4], rs[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int col = n0 + c + i;
-    if (col >= N) break;
-    const float b = Epi::bias == 1 ? bias[row] : (Epi::bias == 2 ? bias[col] : 0.f);
-    float x = Epi::apply(vs[i], b);
-    size_t o;
+    const bool ok = col < N;
     if (hw > 0) {
       const int n = col / hw;
-      o = ((size_t)n * M + row) * hw + (col - n * hw);
+      o[i] = ((size_t)n * M + row) * hw + (col - n * hw);
     } else {
-      o = (size_t)row * ldc + col;
+      o[i] = (size_t)row * ldc + col;
     }
-    if (Epi::residual) x = Epi::post(x, res[o]);
-    C[o] = x;
+    b[i] = Epi::bias == 1 ? bias[row] : ((Epi::bias == 2 && ok) ? bias[col] : 0.f);
+    rs[i] = (Epi::residual && ok) ? res[o[i]] : 0.f;
+  }
+  float xs[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    xs[i] = Epi::apply(vs[i], b[i]);
+    if (Epi::residual) xs[i] = Epi::post(xs[i], rs[i]);
+  }
+  if (n0 + c + 3 < N) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) C[o[i]] = xs[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (n0 + c + i < N) C[o[i]] = xs[i];
   }
 }
 
@@ -579,6 +645,194 @@ __device__ __forceinline__ void splitk_reduce_f32(const float* __restrict__ ws,
   }
   if (Epi::residual) v = Epi::post(v, res[o]);
   C[o] = v;
+}
+
+// Convolution with few input channels (a network's stem, C <= 4) as a direct
+// convolution on the matrix cores. A 4-wave workgroup computes 32 * OCW output
+// channels of TR x TC blocks of one image's output pixels:
+//  * the input patch of a block ((TR-1)*SH + KH rows by (TC-1)*SW + KWP
+//    columns of every channel, zero outside the image) is staged in LDS;
+//  * each wave keeps its 32 channels' weights in registers for the whole K,
+//    packed as [channel block][pair i][lane]: lane l holds w[oc0 + l%32][k],
+//    k = 2i + l/32 in (c, kh, kw) order with kw padded to KWP (KW rounded up to
+//    even; zero weights in the padding), so both k of a pair share one patch row;
+//  * the K loop is v_mfma_f32_32x32x2f32 with the B operand read straight
+//    from the patch: lane l's pixel (l%32 of a 32-pixel block) and k sit at
+//    patch[c][SH*r + kh][SW*col + kw], a per-lane base plus a compile-time
+//    offset per pair, so the loop has no address arithmetic, global loads or
+//    barriers.
+// The workgroups step through the pixel blocks (x = block index, stride
+// gridDim.x; y = channel group), so the weights are loaded once per
+// workgroup, and the next block's patch is fetched into registers while the
+// current one is computed (two LDS patch buffers, one barrier per block).
+// LDS offset of pair i's first k = 2i = (c, kh, kw) in a C x PR x PC patch
+template <int C, int KH, int KWP, int PR, int PC>
+__device__ __forceinline__ constexpr int smallc_off(int i) {
+  return ((2 * i) / (KH * KWP) * PR + (2 * i) % (KH * KWP) / KWP) * PC + (2 * i) % KWP;
+}
+
+template <class Epi, int C, int KH, int KW, int SH, int SW, int PT, int PL, int TR, int TC, int OCW>
+__device__ __forceinline__ void conv_smallc_f32(const float* __restrict__ x,
+                                                const float* __restrict__ wp,
+                                                const float* __restrict__ bias,
+                                                const float* __restrict__ res,
+                                                float* __restrict__ y, int N, int H, int W, int OC,
+                                                int OH, int OW) {
+  constexpr int KWP = (KW + 1) & ~1;
+  constexpr int NPAIR = C * KH * KWP / 2;
+  constexpr int PR = (TR - 1) * SH + KH;
+  constexpr int PC = (TC - 1) * SW + KWP;
+  constexpr int PSZ = C * PR * PC;
+  constexpr int NPT = (PSZ + 255) / 256;        // patch elements per thread
+  constexpr int PXG = 4 / OCW;                  // wave groups along the pixels
+  constexpr int NB = TR * TC / 32 / PXG;        // 32-pixel blocks per wave
+  static_assert(4 % OCW == 0 && TR * TC == NB * 32 * PXG && NB >= 1, "tile split");
+  static_assert(PSZ * 4 <= 65536, "patch exceeds the LDS offset range");
+  __shared__ float patch[2][PSZ];
+
+  const int tiles_w = (OW + TC - 1) / TC;
+  const int tiles_h = (OH + TR - 1) / TR;
+  const int ntiles = N * tiles_h * tiles_w;
+  int t = blockIdx.x;
+  if (t >= ntiles) return;
+
+  auto load_patch = [&](int tile, float (&pr)[NPT]) {
+    const int tw = tile % tiles_w;
+    const int th = (tile / tiles_w) % tiles_h;
+    const int n = tile / (tiles_w * tiles_h);
+    const int ih0 = th * TR * SH - PT, iw0 = tw * TC * SW - PL;
+    const float* xn = x + (size_t)n * C * H * W;
+#pragma unroll
+    for (int q = 0; q < NPT; ++q) {
+      const int e = threadIdx.x + q * 256;
+      const int c = e / (PR * PC);
+      const int rem = e - c * (PR * PC);
+      const int r = rem / PC, col = rem - r * PC;
+      const int ih = ih0 + r, iw = iw0 + col;
+      pr[q] = (e < PSZ && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
+                  ? xn[((size_t)c * H + ih) * W + iw] : 0.f;
+    }
+  };
+  auto store_patch = [&](int buf, const float (&pr)[NPT]) {
+#pragma unroll
+    for (int q = 0; q < NPT; ++q) {
+      const int e = threadIdx.x + q * 256;
+      if (PSZ % 256 == 0 || e < PSZ) patch[buf][e] = pr[q];
+    }
+  };
+
+  float pr[NPT];
+  load_patch(t, pr);
+  store_patch(0, pr);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ocb = blockIdx.y * OCW + wave % OCW;
+  const int pg = wave / OCW;
+  float a[NPAIR];
+  const float* wl = wp + (size_t)ocb * NPAIR * 64 + lane;
+#pragma unroll
+  for (int i = 0; i < NPAIR; ++i) a[i] = wl[i * 64];
+
+  const int li = lane & 31, lk = lane >> 5;
+  int base[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int p = (pg * NB + j) * 32 + li;
+    const int r = p / TC, col = p - (p / TC) * TC;
+    base[j] = r * SH * PC + col * SW + lk;
+  }
+  // this lane's 16 output channels and their bias, fixed for the workgroup
+  float bsv[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int oc = ocb * 32 + (r / 4) * 8 + lk * 4 + (r % 4);
+    bsv[r] = (Epi::bias && oc < OC) ? bias[oc] : 0.f;
+  }
+  __syncthreads();
+
+  for (int cur = 0; t < ntiles; t += gridDim.x, cur ^= 1) {
+    const int tn = t + gridDim.x;
+    if (tn < ntiles) load_patch(tn, pr);
+    const float* pt = patch[cur];
+    floatx16 acc[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+    // B operands run DIST pairs ahead of the MFMAs (a ring of registers);
+    // the scheduling barriers keep the compiler from sinking each read next
+    // to its MFMA, which would expose the LDS latency on every pair
+    constexpr int DIST = 4;
+    float bv[DIST][NB];
+#pragma unroll
+    for (int i = 0; i < DIST && i < NPAIR; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) bv[i][j] = pt[base[j] + smallc_off<C, KH, KWP, PR, PC>(i)];
+#pragma unroll
+    for (int i = 0; i < NPAIR; ++i) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], bv[i % DIST][j], acc[j], 0, 0, 0);
+      if (i + DIST < NPAIR) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+          bv[i % DIST][j] = pt[base[j] + smallc_off<C, KH, KWP, PR, PC>(i + DIST)];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // lane l holds pixel l%32 of each block and channels (r/4)*8 + (l/32)*4 + r%4;
+    // residual operands are all loaded before the first store
+    const int tw = t % tiles_w;
+    const int th = (t / tiles_w) % tiles_h;
+    const int n = t / (tiles_w * tiles_h);
+    const size_t cs = (size_t)OH * OW;
+    size_t o0[NB];
+    bool pok[NB];
+    float rv[NB][16];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int p = (pg * NB + j) * 32 + li;
+      const int oh = th * TR + p / TC, ow = tw * TC + p % TC;
+      pok[j] = oh < OH && ow < OW;
+      o0[j] = (((size_t)n * OC + ocb * 32 + lk * 4) * OH + oh) * OW + ow;
+      if (Epi::residual) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int oc = ocb * 32 + (r / 4) * 8 + lk * 4 + (r % 4);
+          rv[j][r] = (pok[j] && oc < OC) ? res[o0[j] + ((r / 4) * 8 + (r % 4)) * cs] : 0.f;
+        }
+      }
+    }
+    float outv[NB][16];
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float v = Epi::apply(acc[j][r], bsv[r]);
+        if (Epi::residual) v = Epi::post(v, rv[j][r]);
+        outv[j][r] = v;
+      }
+    const bool full = (ocb + 1) * 32 <= OC && (th + 1) * TR <= OH && (tw + 1) * TC <= OW;
+    if (full) {                                  // no per-element branches
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) y[o0[j] + ((r / 4) * 8 + (r % 4)) * cs] = outv[j][r];
+    } else {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        if (!pok[j]) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int oc = ocb * 32 + (r / 4) * 8 + lk * 4 + (r % 4);
+          if (oc < OC) y[o0[j] + ((r / 4) * 8 + (r % 4)) * cs] = outv[j][r];
+        }
+      }
+    }
+    if (tn < ntiles) store_patch(cur ^ 1, pr);
+    __syncthreads();
+  }
 }
 
 }  // namespace mdlc

@@ -223,6 +223,29 @@ def streamk_fixup_kernel(name: str, sched: MfmaSchedule, skw: int, *, with_bias:
         "ldc, hw);\n}\n")
 
 
+def conv_smallc_kernel(name: str, win: tuple, tile: tuple, *, with_bias: bool,
+                       activation: Optional[str], attrs: dict,
+                       residual: Optional[str] = None) -> tuple:
+    """Direct convolution for few input channels on the matrix cores.
+    ``win`` = (C, KH, KW, SH, SW, PT, PL), ``tile`` = (TR, TC, OCW): a
+    workgroup computes 32 * OCW channels of a TR x TC output block.
+    ABI: (x, wp, [bias], [res], y, int N, int H, int W, int OC, int OH,
+    int OW) with ``wp`` the weights packed [channel block][pair][lane]; grid
+    x steps through the TR x TC blocks, y covers the channel groups."""
+    epi = f"{name}_epi"
+    src = epilogue_struct(epi, bias_mode="row" if with_bias else None, activation=activation,
+                          attrs=attrs, residual=residual)
+    bias_arg = "const float* __restrict__ bias, " if with_bias else ""
+    res_arg = "const float* __restrict__ res, " if residual else ""
+    targs = ", ".join(str(int(v)) for v in tuple(win) + tuple(tile))
+    return name, src + (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        f"    const float* __restrict__ x, const float* __restrict__ wp, {bias_arg}{res_arg}"
+        "float* __restrict__ y,\n    int N, int H, int W, int OC, int OH, int OW) {\n"
+        f"  mdlc::conv_smallc_f32<{epi}, {targs}>(x, wp, {'bias' if with_bias else 'nullptr'}, "
+        f"{'res' if residual else 'nullptr'}, y, N, H, W, OC, OH, OW);\n}}\n")
+
+
 def im2col_kernel(name: str = "im2col") -> tuple:
     """ABI: the reference's (x, cols, C, H, W, KH, KW, OH, OW, SH, SW, PH, PW,
     DH, DW) plus trailing (N, ldc) for the batched column matrix."""

@@ -290,3 +290,33 @@ def qmlp_layout(C: int, E: int, M: int, bm: Optional[int] = None) -> Optional[QM
         if g1 is not None and g2 is not None and qmlp_lds_bytes(C, E, r) <= LDS_LIMIT:
             return QMlpLayout(r, g1, g2)
     return None
+
+
+# ----- direct convolution for few input channels ---------------------------
+
+SMALLC_MAX_C = 4          # input channels up to which a conv takes the direct kernel
+SMALLC_MAX_PAIRS = 96     # weight registers per lane it may hold (C * KH * KW padded / 2)
+
+
+def smallc_pairs(C: int, KH: int, KW: int) -> int:
+    return C * KH * (KW + (KW & 1)) // 2
+
+
+def smallc_fits(C: int, KH: int, KW: int, DH: int, DW: int) -> bool:
+    return C <= SMALLC_MAX_C and DH == 1 and DW == 1 and smallc_pairs(C, KH, KW) <= SMALLC_MAX_PAIRS
+
+
+def smallc_tile(N: int, OC: int, OH: int, OW: int) -> tuple:
+    """(TR, TC, OCW) of the direct small-channel convolution: 8x16 output
+    blocks with two 32-channel blocks per workgroup, 4x16 blocks when that
+    leaves fewer than two workgroups per CU; one channel block for OC <= 32."""
+    ocw = 2 if OC > 32 else 1
+    if ocw == 1:
+        return 8, 16, 1
+    wgs = N * -(-OH // 8) * -(-OW // 16) * -(-OC // 64)
+    return (8, 16, 2) if wgs >= 2 * CUS else (4, 16, 2)
+
+
+def smallc_lds_bytes(C: int, KH: int, KW: int, SH: int, SW: int, TR: int, TC: int) -> int:
+    return 4 * C * ((TR - 1) * SH + KH) * ((TC - 1) * SW + KW + (KW & 1))
+

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 from gpu_util import assert_close, device_run
-from mdlc_amd.codegen.schedule import MfmaSchedule
+from mdlc_amd.codegen.schedule import MfmaSchedule, smallc_tile
 from mdlc_amd.ir import Node
 from mdlc_amd.testing import BITWISE, DEVICE_TENSOR
 from mdlc_amd.tools.graph_builder import GraphBuilder
@@ -116,13 +116,74 @@ CONV_CASES = [
 ]
 
 
-@pytest.mark.parametrize("mode", ["implicit", "im2col"])
+@pytest.mark.parametrize("mode", ["implicit", "im2col", "implicit-gemm"])
 @pytest.mark.parametrize("case", CONV_CASES, ids=lambda c: "x".join(map(str, c)))
 def test_conv_matches_oracle(case, mode, hip_ctx):
+    """Implicit mode takes the direct small-channel kernel for C <= 4;
+    "implicit-gemm" keeps those convs on the implicit-GEMM gather."""
     g, feeds = _conv_graph(*case)
-    c, got, want = device_run(g, feeds, conv_mode=mode, ctx=hip_ctx)
+    c, got, want = device_run(g, feeds, conv_mode=mode.split("-")[0], ctx=hip_ctx,
+                              small_conv=mode != "implicit-gemm")
     assert [n.op_type for n in c.graph.nodes] == ["FusedConvAct"]
+    kinds = [l.kind for l in c.module.plan]
+    assert ("conv_smallc" in kinds) == (mode == "implicit" and case[1] <= 4)
     assert_close("y", got["y"], want["y"])
+
+
+SMALLC_CASES = [
+    # n, c, h, w, oc, k, s, p, act, bias: every tile rule, ragged edges, OC not a multiple of 32
+    (2, 3, 30, 30, 64, 7, 2, 3, "Relu", True),
+    (1, 3, 17, 19, 32, 3, 2, 1, "Clip", True),
+    (2, 1, 9, 9, 40, 3, 1, 1, None, False),
+    (1, 4, 12, 20, 96, 5, 1, 2, "Relu", True),
+    (2, 2, 15, 15, 24, 4, 2, 1, "Sigmoid", True),
+    (3, 3, 40, 36, 70, 7, 2, 3, "Relu", False),
+    (64, 3, 16, 16, 256, 3, 1, 1, "Relu", True),       # 8x16 blocks (>= 512 workgroups)
+]
+
+
+@pytest.mark.parametrize("case", SMALLC_CASES, ids=lambda c: "x".join(map(str, c[:8])))
+def test_conv_small_channels_direct(case, hip_ctx):
+    """The direct small-channel kernel (input patch in LDS, weights in
+    registers, 32x32x2 MFMAs) against the oracle, and equal to a repeat run."""
+    from mdlc_amd.codegen.hip.hip_executor import HipExecutor
+    from mdlc_amd.compiler import compile_graph
+    from oracle.reference import run_reference
+
+    *geo, act, bias = case
+    g, feeds = _conv_graph(*geo, act=act, bias=bias)
+    c = compile_graph(g, feeds=feeds)
+    (launch,) = [l for l in c.module.plan if l.kind == "conv_smallc"]
+    m = launch.meta
+    assert m["tile"] == smallc_tile(geo[0], m["OC"], m["OH"], m["OW"])
+    ex = HipExecutor(c.module, hip_ctx)
+    try:
+        y1 = ex.run(feeds)["outputs"]["y"]
+        y2 = ex.run(feeds)["outputs"]["y"]
+    finally:
+        ex.close()
+    assert_close("y", y1, run_reference(c.graph, feeds)["y"])
+    np.testing.assert_array_equal(y1, y2)
+
+
+def test_conv_small_channels_residual(hip_ctx):
+    """A residual add folded into the direct small-channel conv's epilogue."""
+    rng = np.random.default_rng(11)
+    b = GraphBuilder("smallres")
+    b.input("x", (2, 3, 20, 20))
+    b.input("r", (2, 48, 10, 10))
+    b.const("w", (rng.standard_normal((48, 3, 7, 7)) * 0.1).astype(np.float32))
+    b.const("b", (rng.standard_normal(48) * 0.1).astype(np.float32))
+    b.node("Conv", ["x", "w", "b"], "c", kernel_shape=[7, 7], strides=[2, 2], pads=[3, 3, 3, 3])
+    b.node("Relu", ["c"], "y")
+    b.node("Add", ["y", "r"], "s")
+    b.node("Relu", ["s"], "z")
+    b.output("z")
+    feeds = {"x": rng.standard_normal((2, 3, 20, 20)).astype(np.float32),
+             "r": rng.standard_normal((2, 48, 10, 10)).astype(np.float32)}
+    c, got, want = device_run(b.graph(), feeds, ctx=hip_ctx)
+    assert [l.kind for l in c.module.plan] == ["conv_smallc"]
+    assert_close("z", got["z"], want["z"])
 
 
 @pytest.mark.parametrize("mode", ["implicit", "im2col"])
@@ -139,7 +200,8 @@ def test_conv_split_k(case, sk, mode, hip_ctx):
 
     sched = MfmaSchedule(64, 64, 16, 2, 2, 32, True, sk)
     g, feeds = _conv_graph(*case)
-    c = compile_graph(g, feeds=feeds, conv_mode=mode, schedule_fn=lambda n, mnk: sched)
+    c = compile_graph(g, feeds=feeds, conv_mode=mode, schedule_fn=lambda n, mnk: sched,
+                      small_conv=False)
     (launch,) = [l for l in c.module.plan if l.kind in ("conv", "gemm")]
     assert launch.meta["ksplit"] > 1 and launch.grid[0] % launch.meta["ksplit"] == 0
     assert [l.kind for l in c.module.plan][-1] == "splitk_reduce"
@@ -173,7 +235,7 @@ def test_conv_gather_schedules(case, sched, hip_ctx):
     assert sched.conv_valid()
     g, feeds = _conv_graph(*case)
     c, got, want = device_run(g, feeds, conv_mode="implicit", ctx=hip_ctx,
-                              schedule_fn=lambda n, mnk: sched)
+                              schedule_fn=lambda n, mnk: sched, small_conv=False)
     (launch,) = [l for l in c.module.plan if l.kind == "conv"]
     assert launch.meta["k_order"] == ("tap" if case[1] % sched.BK == 0 else "channel")
     assert_close("y", got["y"], want["y"])
