@@ -84,11 +84,20 @@ __device__ __forceinline__ void qgemm_epilogue(const QGemmArgs& g, Acc& acc, int
   // (MS = 32; for MS = 16 the single group is at lk*4 + j).
   constexpr int NG = MfmaI8<MS>::kAcc / 4;
   const bool vec_ok = (g.ldc & 3) == 0;
+  // The tile's bias and multipliers (and the lookup table) go through LDS:
+  // read from global memory between the output stores, each would wait for
+  // the store before it (the compiler cannot tell them apart from the output).
   __shared__ i8 table[EPI == 1 ? 256 : 1];
-  if (EPI == 1) {                 // the K loop ended with a barrier: LDS is free
-    for (int i = tid; i < 256; i += NT) table[i] = g.aux[i];
-    __syncthreads();
+  __shared__ int bias_s[BN];
+  __shared__ float mult_s[BN];
+  for (int i = tid; i < BN; i += NT) {        // the K loop ended with a barrier: LDS is free
+    const bool ok = n0 + i < g.N;
+    bias_s[i] = ok ? g.bias[n0 + i] : 0;
+    mult_s[i] = ok ? g.mult[n0 + i] : 0.f;
   }
+  if (EPI == 1)
+    for (int i = tid; i < 256; i += NT) table[i] = g.aux[i];
+  __syncthreads();
   auto finish = [&](i8 code, i8 res) -> i8 {
     if (EPI == 1) return table[(int)code + 128];
     if (EPI == 2) {
@@ -103,9 +112,19 @@ __device__ __forceinline__ void qgemm_epilogue(const QGemmArgs& g, Acc& acc, int
     for (int q = 0; q < NG; ++q) {
       const int col = n0 + wn0 + ni * MS + q * 8 + lk * 4;
       if (col >= g.N) continue;
-      const intx4 bv = *reinterpret_cast<const intx4*>(g.bias + col);
-      const floatx4 mv = *reinterpret_cast<const floatx4*>(g.mult + col);
+      const intx4 bv = *reinterpret_cast<const intx4*>(&bias_s[col - n0]);
+      const floatx4 mv = *reinterpret_cast<const floatx4*>(&mult_s[col - n0]);
       const bool full = vec_ok && col + 4 <= g.N;
+      // the residual words of all the group's rows before its first store
+      int rw[MI];
+      if (OUT == 0 && EPI == 2) {
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi) {
+          const int row = m0 + wm0 + mi * MS + li;
+          const size_t off = (size_t)row * g.ldc + col;
+          rw[mi] = (full && row < g.M) ? *reinterpret_cast<const int*>(g.aux + off) : 0;
+        }
+      }
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi) {
         const int row = m0 + wm0 + mi * MS + li;
@@ -129,7 +148,7 @@ __device__ __forceinline__ void qgemm_epilogue(const QGemmArgs& g, Acc& acc, int
           r.w = 0;
           if (EPI == 2) {
             if (full) {
-              r.w = *reinterpret_cast<const int*>(g.aux + off);
+              r.w = rw[mi];
             } else {
 #pragma unroll
               for (int j = 0; j < 4; ++j)
@@ -730,7 +749,8 @@ __device__ __forceinline__ void qmlp_gemm(const i8* __restrict__ As, const i8* _
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
-      for (int mi = 0; mi < MI; ++mi) epi(r0 + mi * 16 + li, col0 + ni * 16 + lk * 4, acc[mi][ni]);
+      for (int mi = 0; mi < MI; ++mi)
+        epi(r0 + mi * 16 + li, col0 + ni * 16 + lk * 4, acc[mi][ni], c0 / CHUNK, ni);
   }
 }
 
@@ -767,7 +787,8 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   __syncthreads();
 
   QMlpFrags<EP, EP, NI2> w2f;
-  qmlp_gemm<CP, XS, CP, E, BM, WGM1, WGN1, NI1>(Xs, g.W1, w1f, [&](int r, int n, const intx4& acc) {
+  qmlp_gemm<CP, XS, CP, E, BM, WGM1, WGN1, NI1>(Xs, g.W1, w1f, [&](int r, int n, const intx4& acc,
+                                                                    int, int) {
     const intx4 bv = *reinterpret_cast<const intx4*>(g.b1 + n);
     const floatx4 mv = *reinterpret_cast<const floatx4*>(g.m1 + n);
     union { int w; i8 b[4]; } o;
@@ -775,13 +796,27 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
     for (int j = 0; j < 4; ++j) o.b[j] = tab[(int)requant(acc[j] + bv[j], mv[j], (float)LO1) + 128];
     *reinterpret_cast<int*>(&Hs[r * HS + n]) = o.w;
   }, [&]() { w2f.load(g.W2, qmlp_col0<WGN2, NI2>(0)); });
+  // the second GEMM's bias and multipliers for this lane's columns, loaded
+  // before any output store (loads after a store to Y would wait for it)
+  constexpr int CH2 = WGN2 * NI2 * 16, NCH2 = C / CH2;
+  intx4 b2v[NCH2][NI2];
+  floatx4 m2v[NCH2][NI2];
+#pragma unroll
+  for (int ch = 0; ch < NCH2; ++ch)
+#pragma unroll
+    for (int ni = 0; ni < NI2; ++ni) {
+      const int n = qmlp_col0<WGN2, NI2>(ch * CH2) + ni * 16 + ((threadIdx.x & 63) >> 4) * 4;
+      b2v[ch][ni] = *reinterpret_cast<const intx4*>(g.b2 + n);
+      m2v[ch][ni] = *reinterpret_cast<const floatx4*>(g.m2 + n);
+    }
   __syncthreads();
 
-  qmlp_gemm<EP, HS, EP, C, BM, WGM2, WGN2, NI2>(Hs, g.W2, w2f, [&](int r, int n, const intx4& acc) {
+  qmlp_gemm<EP, HS, EP, C, BM, WGM2, WGN2, NI2>(Hs, g.W2, w2f, [&](int r, int n, const intx4& acc,
+                                                                   int ch, int ni) {
     const int m = m0 + r;
     if (m >= g.M) return;
-    const intx4 bv = *reinterpret_cast<const intx4*>(g.b2 + n);
-    const floatx4 mv = *reinterpret_cast<const floatx4*>(g.m2 + n);
+    const intx4 bv = b2v[ch][ni];
+    const floatx4 mv = m2v[ch][ni];
     union { int w; i8 b[4]; } x, o;
     x.w = *reinterpret_cast<const int*>(&Xs[r * XS + n]);
 #pragma unroll
