@@ -741,12 +741,12 @@ __device__ __forceinline__ void conv_smallc_f32(const float* __restrict__ x,
     const int r = p / TC, col = p - (p / TC) * TC;
     base[j] = r * SH * PC + col * SW + lk;
   }
-  // this lane's 16 output channels and their bias, fixed for the workgroup
-  float bsv[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int oc = ocb * 32 + (r / 4) * 8 + lk * 4 + (r % 4);
-    bsv[r] = (Epi::bias && oc < OC) ? bias[oc] : 0.f;
+  // the workgroup's bias values in LDS: read between output stores from
+  // global memory they would each wait for the store before them
+  __shared__ float bias_s[32 * OCW];
+  if (threadIdx.x < 32 * OCW) {
+    const int oc = blockIdx.y * OCW * 32 + threadIdx.x;
+    bias_s[threadIdx.x] = (Epi::bias && oc < OC) ? bias[oc] : 0.f;
   }
   __syncthreads();
 
@@ -804,21 +804,18 @@ __device__ __forceinline__ void conv_smallc_f32(const float* __restrict__ x,
         }
       }
     }
-    float outv[NB][16];
-#pragma unroll
-    for (int j = 0; j < NB; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float v = Epi::apply(acc[j][r], bsv[r]);
-        if (Epi::residual) v = Epi::post(v, rv[j][r]);
-        outv[j][r] = v;
-      }
+    const float* bl = bias_s + (wave % OCW) * 32 + lk * 4;
+    auto outval = [&](int j, int r) {
+      float v = Epi::apply(acc[j][r], bl[(r / 4) * 8 + (r % 4)]);
+      if (Epi::residual) v = Epi::post(v, rv[j][r]);
+      return v;
+    };
     const bool full = (ocb + 1) * 32 <= OC && (th + 1) * TR <= OH && (tw + 1) * TC <= OW;
     if (full) {                                  // no per-element branches
 #pragma unroll
       for (int j = 0; j < NB; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) y[o0[j] + ((r / 4) * 8 + (r % 4)) * cs] = outv[j][r];
+        for (int r = 0; r < 16; ++r) y[o0[j] + ((r / 4) * 8 + (r % 4)) * cs] = outval(j, r);
     } else {
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
@@ -826,7 +823,7 @@ __device__ __forceinline__ void conv_smallc_f32(const float* __restrict__ x,
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int oc = ocb * 32 + (r / 4) * 8 + lk * 4 + (r % 4);
-          if (oc < OC) y[o0[j] + ((r / 4) * 8 + (r % 4)) * cs] = outv[j][r];
+          if (oc < OC) y[o0[j] + ((r / 4) * 8 + (r % 4)) * cs] = outval(j, r);
         }
       }
     }

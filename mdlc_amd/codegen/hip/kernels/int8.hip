@@ -505,18 +505,26 @@ __device__ __forceinline__ void qconv_first(const float* __restrict__ x, float i
   const int ow = (int)(p % OW);
   const int oh = (int)((p / OW) % OH);
   const int n = (int)(p / ((long long)OW * OH));
+  // the whole window is loaded before any of it is used (a tap outside the
+  // image reads the image's first element and is then replaced by zero), so
+  // the K loads are in flight together instead of one after another
+  const float* xn = x + (size_t)n * C * H * W;
+  float xv[K];
+  bool ok[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int c = k / (KH * KW), kh = (k / KW) % KH, kw = k % KW;
+    const int ih = oh * SH - PT + kh, iw = ow * SW - PL + kw;
+    ok[k] = (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+    xv[k] = xn[ok[k] ? ((size_t)c * H + ih) * W + iw : 0];
+  }
   int q[KQ];
 #pragma unroll
   for (int j = 0; j < KQ; ++j) q[j] = 0;
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    const int c = k / (KH * KW), kh = (k / KW) % KH, kw = k % KW;
-    const int ih = oh * SH - PT + kh, iw = ow * SW - PL + kw;
-    int code = 0;
-    if ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W) {
-      const float r = rintf(x[(((size_t)n * C + c) * H + ih) * W + iw] * inv_s);
-      code = (int)fminf(fmaxf(r, -127.0f), 127.0f);
-    }
+    const float r = rintf(xv[k] * inv_s);
+    const int code = ok[k] ? (int)fminf(fmaxf(r, -127.0f), 127.0f) : 0;
     q[k / 4] |= (code & 0xff) << (8 * (k % 4));
   }
   union { int w[OC / 4]; i8 b[OC]; } out;
