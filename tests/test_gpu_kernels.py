@@ -166,6 +166,21 @@ def test_conv_small_channels_direct(case, hip_ctx):
     np.testing.assert_array_equal(y1, y2)
 
 
+@pytest.mark.parametrize("wgs", [1, 7])
+def test_conv_small_channels_blocks_per_workgroup(wgs, hip_ctx, monkeypatch):
+    """Fewer workgroups than output blocks: each steps through several blocks,
+    prefetching the next patch while it computes (1 workgroup: every block in
+    turn; 7: an uneven share, the last block partial)."""
+    from mdlc_amd.codegen.hip import emit as E
+
+    monkeypatch.setattr(E, "SMALLC_WGS", wgs)
+    g, feeds = _conv_graph(3, 3, 37, 45, 64, 7, 2, 3)
+    c, got, want = device_run(g, feeds, ctx=hip_ctx)
+    (launch,) = [l for l in c.module.plan if l.kind == "conv_smallc"]
+    assert launch.grid[0] == wgs
+    assert_close("y", got["y"], want["y"])
+
+
 def test_conv_small_channels_residual(hip_ctx):
     """A residual add folded into the direct small-channel conv's epilogue."""
     rng = np.random.default_rng(11)
