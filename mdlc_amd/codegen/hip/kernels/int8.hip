@@ -234,7 +234,7 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   const int tiles_m = (g.M + BM - 1) / BM;
   const int tiles_n = (g.N + BN - 1) / BN;
   int mt, nt;
-  grouped_tile<16>(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, mt, nt);
+  grouped_tile<8>(xcd_remap(blockIdx.x, tiles_m * tiles_n), tiles_m, tiles_n, mt, nt);
   const int m0 = mt * BM;
   const int n0 = nt * BN;
 
