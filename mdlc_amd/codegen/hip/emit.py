@@ -250,18 +250,17 @@ class HipCodegen(Int8LoweringMixin):
         """A conv with few input channels (a network's stem): the direct
         matrix-core kernel, input patch in LDS and weights in registers. The
         weights are packed here as [channel block][pair i][lane], lane =
-        (k % 2) * 32 + oc % 32, k = 2i + k % 2 in (c, kh, kw) order with kw
-        padded to even (zero weights)."""
+        (k % 2) * 32 + oc % 32, k = 2i + k % 2 in (c, kh, kw) order (a zero
+        weight pads an odd K)."""
         C, KH, KW = geo["C"], geo["KH"], geo["KW"]
         OC, OH, OW, N = geo["OC"], geo["OH"], geo["OW"], geo["N"]
         x, w, y = node.inputs[0], node.inputs[1], node.outputs[0]
         a = node.attrs
         TR, TC, OCW = smallc_tile(N, OC, OH, OW)
-        kwp = KW + (KW & 1)
         npair = smallc_pairs(C, KH, KW)
         nblk = -(-OC // (32 * OCW)) * OCW
-        wpad = np.zeros((nblk * 32, C, KH, kwp), np.float32)
-        wpad[:OC, :, :, :KW] = np.asarray(g.initializers[w], np.float32).reshape(OC, C, KH, KW)
+        wpad = np.zeros((nblk * 32, 2 * npair), np.float32)
+        wpad[:OC, :C * KH * KW] = np.asarray(g.initializers[w], np.float32).reshape(OC, -1)
         packed = wpad.reshape(nblk, 32, npair, 2).transpose(0, 2, 3, 1).reshape(nblk, npair, 64)
         wdev = self._pack(f"{w}__dev_smallc", packed)
         bias = [node.inputs[2]] if has_bias else []

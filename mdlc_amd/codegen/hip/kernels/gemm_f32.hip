@@ -650,25 +650,33 @@ __device__ __forceinline__ void splitk_reduce_f32(const float* __restrict__ ws,
 // Convolution with few input channels (a network's stem, C <= 4) as a direct
 // convolution on the matrix cores. A 4-wave workgroup computes 32 * OCW output
 // channels of TR x TC blocks of one image's output pixels:
-//  * the input patch of a block ((TR-1)*SH + KH rows by (TC-1)*SW + KWP
+//  * the input patch of a block ((TR-1)*SH + KH rows by (TC-1)*SW + KW
 //    columns of every channel, zero outside the image) is staged in LDS;
 //  * each wave keeps its 32 channels' weights in registers for the whole K,
 //    packed as [channel block][pair i][lane]: lane l holds w[oc0 + l%32][k],
-//    k = 2i + l/32 in (c, kh, kw) order with kw padded to KWP (KW rounded up to
-//    even; zero weights in the padding), so both k of a pair share one patch row;
+//    k = 2i + l/32 in (c, kh, kw) order (K = C*KH*KW, one zero weight pads an
+//    odd K);
 //  * the K loop is v_mfma_f32_32x32x2f32 with the B operand read straight
 //    from the patch: lane l's pixel (l%32 of a 32-pixel block) and k sit at
-//    patch[c][SH*r + kh][SW*col + kw], a per-lane base plus a compile-time
-//    offset per pair, so the loop has no address arithmetic, global loads or
-//    barriers.
+//    patch[c][SH*r + kh][SW*col + kw]. The second k of a pair is one column,
+//    one row step or one channel step after the first (or, for the padding,
+//    the same element), so each lane keeps one base address per step kind and
+//    every read is such a base plus a compile-time offset: the loop has no
+//    address arithmetic, global loads or barriers.
 // The workgroups step through the pixel blocks (x = block index, stride
 // gridDim.x; y = channel group), so the weights are loaded once per
 // workgroup, and the next block's patch is fetched into registers while the
 // current one is computed (two LDS patch buffers, one barrier per block).
-// LDS offset of pair i's first k = 2i = (c, kh, kw) in a C x PR x PC patch
-template <int C, int KH, int KWP, int PR, int PC>
-__device__ __forceinline__ constexpr int smallc_off(int i) {
-  return ((2 * i) / (KH * KWP) * PR + (2 * i) % (KH * KWP) / KWP) * PC + (2 * i) % KWP;
+// LDS offset of k = (c, kh, kw) in a C x PR x PC patch
+template <int KH, int KW, int PR, int PC>
+__device__ __forceinline__ constexpr int smallc_off(int k) {
+  return (k / (KH * KW) * PR + k % (KH * KW) / KW) * PC + k % KW;
+}
+// how the pair's second k = 2i + 1 follows its first: 0 next column, 1 next
+// row, 2 next channel, 3 padding past K (read the first k again)
+template <int C, int KH, int KW>
+__device__ __forceinline__ constexpr int smallc_step(int i) {
+  return 2 * i + 1 >= C * KH * KW ? 3 : (2 * i + 1) % KW ? 0 : (2 * i + 1) % (KH * KW) ? 1 : 2;
 }
 
 template <class Epi, int C, int KH, int KW, int SH, int SW, int PT, int PL, int TR, int TC, int OCW>
@@ -678,10 +686,9 @@ __device__ __forceinline__ void conv_smallc_f32(const float* __restrict__ x,
                                                 const float* __restrict__ res,
                                                 float* __restrict__ y, int N, int H, int W, int OC,
                                                 int OH, int OW) {
-  constexpr int KWP = (KW + 1) & ~1;
-  constexpr int NPAIR = C * KH * KWP / 2;
+  constexpr int NPAIR = (C * KH * KW + 1) / 2;
   constexpr int PR = (TR - 1) * SH + KH;
-  constexpr int PC = (TC - 1) * SW + KWP;
+  constexpr int PC = (TC - 1) * SW + KW;
   constexpr int PSZ = C * PR * PC;
   constexpr int NPT = (PSZ + 255) / 256;        // patch elements per thread
   constexpr int PXG = 4 / OCW;                  // wave groups along the pixels
@@ -734,12 +741,18 @@ __device__ __forceinline__ void conv_smallc_f32(const float* __restrict__ x,
   for (int i = 0; i < NPAIR; ++i) a[i] = wl[i * 64];
 
   const int li = lane & 31, lk = lane >> 5;
-  int base[NB];
+  // per block and step kind: the lane's pixel plus, for the upper half of the
+  // lanes (the pair's second k), one column / one row / one channel
+  int base[NB][4];
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
     const int p = (pg * NB + j) * 32 + li;
     const int r = p / TC, col = p - (p / TC) * TC;
-    base[j] = r * SH * PC + col * SW + lk;
+    const int b0 = r * SH * PC + col * SW;
+    base[j][0] = b0 + lk;
+    base[j][1] = b0 + lk * (PC - KW + 1);
+    base[j][2] = b0 + lk * ((PR - KH + 1) * PC - KW + 1);
+    base[j][3] = b0;
   }
   // the workgroup's bias values in LDS: read between output stores from
   // global memory they would each wait for the store before them
@@ -767,7 +780,8 @@ __device__ __forceinline__ void conv_smallc_f32(const float* __restrict__ x,
 #pragma unroll
     for (int i = 0; i < DIST && i < NPAIR; ++i)
 #pragma unroll
-      for (int j = 0; j < NB; ++j) bv[i][j] = pt[base[j] + smallc_off<C, KH, KWP, PR, PC>(i)];
+      for (int j = 0; j < NB; ++j)
+        bv[i][j] = pt[base[j][smallc_step<C, KH, KW>(i)] + smallc_off<KH, KW, PR, PC>(2 * i)];
 #pragma unroll
     for (int i = 0; i < NPAIR; ++i) {
 #pragma unroll
@@ -776,7 +790,8 @@ __device__ __forceinline__ void conv_smallc_f32(const float* __restrict__ x,
       if (i + DIST < NPAIR) {
 #pragma unroll
         for (int j = 0; j < NB; ++j)
-          bv[i % DIST][j] = pt[base[j] + smallc_off<C, KH, KWP, PR, PC>(i + DIST)];
+          bv[i % DIST][j] = pt[base[j][smallc_step<C, KH, KW>(i + DIST)] +
+                               smallc_off<KH, KW, PR, PC>(2 * (i + DIST))];
       }
       __builtin_amdgcn_sched_barrier(0);
     }

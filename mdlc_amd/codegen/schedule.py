@@ -295,11 +295,11 @@ def qmlp_layout(C: int, E: int, M: int, bm: Optional[int] = None) -> Optional[QM
 # ----- direct convolution for few input channels ---------------------------
 
 SMALLC_MAX_C = 4          # input channels up to which a conv takes the direct kernel
-SMALLC_MAX_PAIRS = 96     # weight registers per lane it may hold (C * KH * KW padded / 2)
+SMALLC_MAX_PAIRS = 96     # weight registers per lane it may hold (C * KH * KW / 2, rounded up)
 
 
 def smallc_pairs(C: int, KH: int, KW: int) -> int:
-    return C * KH * (KW + (KW & 1)) // 2
+    return (C * KH * KW + 1) // 2
 
 
 def smallc_fits(C: int, KH: int, KW: int, DH: int, DW: int) -> bool:
@@ -318,5 +318,5 @@ def smallc_tile(N: int, OC: int, OH: int, OW: int) -> tuple:
 
 
 def smallc_lds_bytes(C: int, KH: int, KW: int, SH: int, SW: int, TR: int, TC: int) -> int:
-    return 4 * C * ((TR - 1) * SH + KH) * ((TC - 1) * SW + KW + (KW & 1))
+    return 4 * C * ((TR - 1) * SH + KH) * ((TC - 1) * SW + KW)
 
