@@ -772,6 +772,12 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   __shared__ __attribute__((aligned(16))) i8 Xs[BM * XS];
   __shared__ __attribute__((aligned(16))) i8 Hs[BM * HS];
   __shared__ i8 tab[256];
+  // both GEMMs' bias and multipliers: staged with the table at the start, so
+  // neither epilogue waits on a global load in the middle of the chain
+  __shared__ __attribute__((aligned(16))) int b1s[E];
+  __shared__ __attribute__((aligned(16))) float m1s[E];
+  __shared__ __attribute__((aligned(16))) int b2s[C];
+  __shared__ __attribute__((aligned(16))) float m2s[C];
   const int tid = threadIdx.x;
   const int m0 = blockIdx.x * BM;
 
@@ -792,39 +798,34 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
     }
   }
   tab[tid] = g.table[tid];
+  for (int i = tid; i < E; i += NT) {
+    b1s[i] = g.b1[i];
+    m1s[i] = g.m1[i];
+  }
+  for (int i = tid; i < C; i += NT) {
+    b2s[i] = g.b2[i];
+    m2s[i] = g.m2[i];
+  }
   __syncthreads();
 
   QMlpFrags<EP, EP, NI2> w2f;
   qmlp_gemm<CP, XS, CP, E, BM, WGM1, WGN1, NI1>(Xs, g.W1, w1f, [&](int r, int n, const intx4& acc,
                                                                     int, int) {
-    const intx4 bv = *reinterpret_cast<const intx4*>(g.b1 + n);
-    const floatx4 mv = *reinterpret_cast<const floatx4*>(g.m1 + n);
+    const intx4 bv = *reinterpret_cast<const intx4*>(&b1s[n]);
+    const floatx4 mv = *reinterpret_cast<const floatx4*>(&m1s[n]);
     union { int w; i8 b[4]; } o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) o.b[j] = tab[(int)requant(acc[j] + bv[j], mv[j], (float)LO1) + 128];
     *reinterpret_cast<int*>(&Hs[r * HS + n]) = o.w;
   }, [&]() { w2f.load(g.W2, qmlp_col0<WGN2, NI2>(0)); });
-  // the second GEMM's bias and multipliers for this lane's columns, loaded
-  // before any output store (loads after a store to Y would wait for it)
-  constexpr int CH2 = WGN2 * NI2 * 16, NCH2 = C / CH2;
-  intx4 b2v[NCH2][NI2];
-  floatx4 m2v[NCH2][NI2];
-#pragma unroll
-  for (int ch = 0; ch < NCH2; ++ch)
-#pragma unroll
-    for (int ni = 0; ni < NI2; ++ni) {
-      const int n = qmlp_col0<WGN2, NI2>(ch * CH2) + ni * 16 + ((threadIdx.x & 63) >> 4) * 4;
-      b2v[ch][ni] = *reinterpret_cast<const intx4*>(g.b2 + n);
-      m2v[ch][ni] = *reinterpret_cast<const floatx4*>(g.m2 + n);
-    }
   __syncthreads();
 
   qmlp_gemm<EP, HS, EP, C, BM, WGM2, WGN2, NI2>(Hs, g.W2, w2f, [&](int r, int n, const intx4& acc,
-                                                                   int ch, int ni) {
+                                                                   int, int) {
     const int m = m0 + r;
     if (m >= g.M) return;
-    const intx4 bv = b2v[ch][ni];
-    const floatx4 mv = m2v[ch][ni];
+    const intx4 bv = *reinterpret_cast<const intx4*>(&b2s[n]);
+    const floatx4 mv = *reinterpret_cast<const floatx4*>(&m2s[n]);
     union { int w; i8 b[4]; } x, o;
     x.w = *reinterpret_cast<const int*>(&Xs[r * XS + n]);
 #pragma unroll
