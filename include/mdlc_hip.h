@@ -42,6 +42,12 @@ int mdlc_rtc_compile(const char* src, const char* name, const char* const* opts,
                      void** code, size_t* size, char* log, size_t log_len);
 void mdlc_rtc_free(void* code);
 
+/* hipRTC's version and the HIP runtime's (hipRuntimeGetVersion), neither of
+ * which needs a device. No counterpart in the reference (it caches nothing):
+ * the Python side keys its on-disk code-object cache on them, so objects built
+ * by another toolchain are never reused. */
+int mdlc_rtc_version(int* rtc_major, int* rtc_minor, int* runtime);
+
 /* Load a code object / resolve a kernel / unload.
  * Replaces: cuModuleLoadData and CudaModule.func, nvrtc_runtime.py:133-144. */
 int mdlc_module_load(const void* code, size_t size, void** module);

@@ -122,6 +122,7 @@ class TuneResult:
     measured: bool
     n_evaluated: int
     ranking: list = field(default_factory=list)
+    rejected: list = field(default_factory=list)   # "schedule: reason" per dropped candidate
 
 
 class AutotuneCache:
@@ -277,12 +278,14 @@ def _problem_graph(problem: dict, sched_seed: int = 0):
     return b.graph(), feeds
 
 
-def _compile_for(problem: dict, sched: MfmaSchedule):
+def _compile_for(problem: dict, sched: Optional[MfmaSchedule]):
+    """Compile the problem's graph with ``sched`` for every GEMM-shaped
+    launch (``None``: the lowering's own shape-aware default)."""
     from mdlc_amd.compiler import compile_graph
 
     g, feeds = _problem_graph(problem)
-    c = compile_graph(g, feeds=feeds, schedule_fn=lambda node, mnk: sched,
-                      conv_mode=problem.get("mode", "implicit"))
+    fn = None if sched is None else (lambda node, mnk: sched)
+    c = compile_graph(g, feeds=feeds, schedule_fn=fn, conv_mode=problem.get("mode", "implicit"))
     return c, feeds
 
 
@@ -294,37 +297,74 @@ def precompile(problem: dict, sched: MfmaSchedule) -> None:
     compile_code_object(c.module.sources())
 
 
-def measure(problem: dict, sched: MfmaSchedule, ctx, *, iters: int = 20, warmup: int = 3) -> float:
-    """Device time (ms) of one run of the problem's launches with ``sched``."""
+def measure(problem: dict, sched: Optional[MfmaSchedule], ctx, *, iters: int = 20,
+            warmup: int = 3, with_output: bool = False):
+    """Device time (ms) of one run of the problem's launches with ``sched``;
+    with ``with_output`` also the problem's output ``y`` after the runs."""
     from mdlc_amd.codegen.hip.hip_executor import HipExecutor
 
     c, feeds = _compile_for(problem, sched)
     ex = HipExecutor(c.module, ctx)
     try:
         ex._upload_feeds(feeds)
-        return ex.plan.time_ms(warmup, iters)
+        ms = ex.plan.time_ms(warmup, iters)
+        return (ms, ex.read("y")) if with_output else ms
     finally:
         ex.close()
 
 
+# A measured candidate is accepted only if its output agrees with the
+# default schedule's on the same feed: bit-exact for int8 (the integer
+# result does not depend on the schedule), and within the per-tensor fp32
+# tolerance otherwise (split-K and tile shape change the summation order).
+AGREE_RTOL, AGREE_ATOL = 1e-4, 1e-5
+
+
+def outputs_agree(got, want) -> bool:
+    import numpy as np
+
+    got, want = np.asarray(got), np.asarray(want)
+    if got.shape != want.shape:
+        return False
+    if np.issubdtype(want.dtype, np.integer):
+        return bool(np.array_equal(got, want))
+    return bool(np.all(np.abs(got.astype(np.float64) - want) <=
+                       AGREE_ATOL + AGREE_RTOL * np.abs(want.astype(np.float64))))
+
+
+class TuneError(RuntimeError):
+    pass
+
+
 def tune_problem(problem: dict, *, budget: int = 24, ctx=None, seed: int = 0) -> TuneResult:
+    """Best schedule for ``problem``: by the cost model, or (``ctx`` given)
+    by device time among candidates whose output matches the default
+    schedule's. Raises ``TuneError`` when no candidate survives."""
     M, N, K = problem["M"], problem["N"], problem["K"]
     cands = problem_candidates(problem, budget=budget, seed=seed)
     model = analytical_qcost if is_int8(problem) else analytical_cost
-    scored = []
+    scored, rejected = [], []
+    want = measure(problem, None, ctx, iters=1, warmup=0, with_output=True)[1] if ctx else None
     for s in cands:
-        if ctx is not None:
-            try:
-                metric = measure(problem, s, ctx)
-            except Exception:
-                continue
-        else:
-            metric = model(s, M, N, K)
+        if ctx is None:
+            scored.append((s, model(s, M, N, K)))
+            continue
+        try:
+            metric, got = measure(problem, s, ctx, with_output=True)
+        except Exception as exc:  # a candidate the lowering or hipRTC rejects
+            rejected.append(f"{s.key_full()}: {type(exc).__name__}: {exc}".splitlines()[0])
+            continue
+        if not outputs_agree(got, want):
+            rejected.append(f"{s.key_full()}: output differs from the default schedule's")
+            continue
         scored.append((s, metric))
+    if not scored:
+        raise TuneError(f"no candidate schedule for {problem_key(problem)} could be measured "
+                        f"({len(cands)} tried): " + "; ".join(rejected[:4]))
     scored.sort(key=lambda t: t[1])
     best, best_metric = scored[0]
     return TuneResult(problem_key(problem), best, best_metric, ctx is not None, len(scored),
-                      [(s.key_full(), m) for s, m in scored])
+                      [(s.key_full(), m) for s, m in scored], rejected)
 
 
 def tune_gemm(M: int, N: int, K: int, *, budget: int = 24, ctx=None, seed: int = 0) -> TuneResult:
@@ -388,5 +428,5 @@ def tuned_schedules() -> Tuner:
 __all__ = ["AutotuneCache", "Tuner", "TuneResult", "analytical_cost", "candidates",
            "is_implicit_conv", "is_int8", "measure", "problem_candidates", "qcandidates",
            "analytical_qcost",
-           "precompile", "problem_key", "tune_gemm", "tune_problem", "tuned_schedules",
+           "outputs_agree", "precompile", "problem_key", "TuneError", "tune_gemm", "tune_problem", "tuned_schedules",
            "DEFAULT_GEMM"]

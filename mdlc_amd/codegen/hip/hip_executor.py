@@ -276,6 +276,7 @@ class HipExecutor:
                 p.close()
             self.ctx.free(self.arena)
             self.arena = None
+            self.code.close()
 
 
 def run_on_gpu(module: HipModule, feeds: dict, *, timing: bool = False) -> dict:

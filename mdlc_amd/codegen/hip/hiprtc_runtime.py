@@ -45,6 +45,7 @@ _SIGS = {
                           ctypes.POINTER(ctypes.c_size_t), ctypes.c_char_p, ctypes.c_size_t],
                          ctypes.c_int),
     "mdlc_rtc_free": ([ctypes.c_void_p], None),
+    "mdlc_rtc_version": ([ctypes.POINTER(ctypes.c_int)] * 3, ctypes.c_int),
     "mdlc_module_load": ([ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)],
                          ctypes.c_int),
     "mdlc_get_function": ([ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)],
@@ -111,9 +112,24 @@ def hip_available() -> bool:
 
 # ----- hipRTC compile -------------------------------------------------------
 
+_TOOLCHAIN: Optional[str] = None
+
+
+def toolchain_version() -> str:
+    """``"hiprtc-<major>.<minor>/hip-<runtime version>"`` of the loaded
+    hipRTC and HIP runtime (no device needed)."""
+    global _TOOLCHAIN
+    if _TOOLCHAIN is None:
+        a, b, r = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        _ck(lib().mdlc_rtc_version(ctypes.byref(a), ctypes.byref(b), ctypes.byref(r)),
+            "mdlc_rtc_version")
+        _TOOLCHAIN = f"hiprtc-{a.value}.{b.value}/hip-{r.value}"
+    return _TOOLCHAIN
+
+
 def _cache_key(source: str, name: str, arch: str, options: tuple) -> str:
     h = hashlib.sha256()
-    for part in (source, name, arch, "\0".join(options)):
+    for part in (toolchain_version(), source, name, arch, "\0".join(options)):
         h.update(part.encode())
         h.update(b"\x00")
     return h.hexdigest()
@@ -123,7 +139,9 @@ def compile_code_object(source: str, name: str = "kernels.hip", arch: str = HIP_
                         options: Optional[tuple] = None, *, use_cache: bool = True) -> bytes:
     """Compile HIP source to a gfx950 code object with hipRTC.
 
-    Results are cached on disk keyed by sha256(source, name, arch, options).
+    Results are cached on disk keyed by sha256(hipRTC and HIP runtime
+    versions, source, name, arch, options), so a toolchain change never
+    reloads an object the old compiler built.
     A compile error raises ``HipError`` carrying the full hipRTC log.
     """
     opts = (f"--offload-arch={arch}",) + tuple(options if options is not None else RTC_OPTIONS)
@@ -170,7 +188,16 @@ class HipCodeModule:
             "hipModuleLoadData")
         self._funcs: dict = {}
 
+    def close(self) -> None:
+        """Unload the code object; its function handles become invalid."""
+        if self._mod is not None and self._mod.value:
+            _ck(lib().mdlc_module_unload(self._mod), "hipModuleUnload")
+        self._mod = None
+        self._funcs = {}
+
     def func(self, name: str) -> ctypes.c_void_p:
+        if self._mod is None:
+            raise HipError("code module is closed")
         if name not in self._funcs:
             f = ctypes.c_void_p()
             _ck(lib().mdlc_get_function(self._mod, name.encode(), ctypes.byref(f)),

@@ -168,6 +168,13 @@ int mdlc_rtc_compile(const char* src, const char* name, const char* const* opts,
 
 void mdlc_rtc_free(void* code) { std::free(code); }
 
+int mdlc_rtc_version(int* rtc_major, int* rtc_minor, int* runtime) {
+  if (!rtc_major || !rtc_minor || !runtime) return fail(kBadArg, "mdlc_rtc_version", "null argument");
+  hiprtcResult r = hiprtcVersion(rtc_major, rtc_minor);
+  if (r != HIPRTC_SUCCESS) return fail(static_cast<int>(r), "hiprtcVersion", hiprtcGetErrorString(r));
+  return check(hipRuntimeGetVersion(runtime), "hipRuntimeGetVersion");
+}
+
 int mdlc_module_load(const void* code, size_t size, void** module) {
   (void)size;
   if (!code || !module) return fail(kBadArg, "mdlc_module_load", "null argument");

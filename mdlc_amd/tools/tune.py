@@ -105,7 +105,8 @@ def main(argv=None) -> int:
         flops = 2.0 * p["M"] * p["N"] * p["K"]
         print(f"{res.key:48s} best {res.best.key_full():40s} {res.best_metric * 1e3:9.1f} us "
               f"({flops / res.best_metric / 1e9:6.1f} TFLOP/s; default {dflt * 1e3:9.1f} us) "
-              f"[{res.n_evaluated} cands, {time.time() - t0:.1f} s]", flush=True)
+              f"[{res.n_evaluated} cands, {len(res.rejected)} rejected, {time.time() - t0:.1f} s]",
+              flush=True)
     return 0
 
 
