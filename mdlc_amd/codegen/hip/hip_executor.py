@@ -33,11 +33,12 @@ from mdlc_amd.runtime.memory_planner import align_up, plan_memory
 
 class HipExecutor:
     def __init__(self, module: HipModule, ctx: Optional[HipContext] = None, *,
-                 use_graph: bool = False) -> None:
+                 use_graph: bool = False, use_cache: bool = True) -> None:
         self.module = module
         self.ctx = ctx or HipContext()
         g = module.graph
-        self.code = self.ctx.load_code(compile_code_object(module.sources(), arch=self.ctx.arch))
+        self.code = self.ctx.load_code(compile_code_object(module.sources(), arch=self.ctx.arch,
+                                                           use_cache=use_cache))
         self.funcs = {name: self.code.func(name) for name in module.kernels}
         for l in module.plan:
             if l.kernel_name not in self.funcs:

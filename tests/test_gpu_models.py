@@ -75,6 +75,71 @@ def test_resnet18_every_group(batch, mode, fold, hip_ctx):
     assert_close("logits", chained["logits"], want["logits"], FP32_NETWORK)
 
 
+@pytest.fixture(scope="module")
+def oracle_b32():
+    """The oracle's every tensor at batch 32, once per network: the values of
+    the reference's groups, which also cover every tensor of the folded graph
+    (the folds keep the unfolded tensors' names and values)."""
+    from mdlc_amd.tools.build_mobilenetv2 import make_input as mb_input
+
+    cache = {}
+
+    def get(name):
+        if name not in cache:
+            build, x = ((build_resnet18, make_input(32)) if name == "resnet18" else
+                        (build_mobilenetv2, mb_input(32, seed=5)))
+            c = compile_graph(build(batch=32), feeds={"input": x}, fuse_residual=False)
+            cache[name] = ({"input": x}, run_reference(c.graph, {"input": x}, return_all=True))
+        return cache[name]
+    return get
+
+
+def _every_group_b32(c, feeds, want, ctx):
+    ex = HipExecutor(c.module, ctx)
+    try:
+        ex._upload_feeds(feeds)
+        got = ex.run_isolated(want)
+        chained = ex.run(feeds)["outputs"]
+    finally:
+        ex.close()
+    _report_ratios(got, want)
+    for t, v in got.items():
+        assert_close(t, v, want[t], DEVICE_TENSOR)
+    assert_close("logits", chained["logits"], want["logits"], FP32_NETWORK)
+    return got
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("fold", [True, False], ids=["residual_folded", "reference_groups"])
+def test_resnet18_b32_every_group(fold, oracle_b32, hip_ctx):
+    """The headline config (batch 32, the shipped gfx950 schedules bench.py
+    runs): every fused group in isolation on the oracle's inputs within rtol
+    1e-4 / atol 1e-5. The batch-32 plan holds kernels batch 1 and 2 never
+    build: split-K slices with their ordered reduce, stream-K convs with
+    their fix-up, and the stem on 512 workgroups."""
+    feeds, want = oracle_b32("resnet18")
+    c = compile_graph(build_resnet18(batch=32), feeds=feeds, fuse_residual=fold)
+    kinds = {l.kind for l in c.module.plan}
+    assert {"splitk_reduce", "streamk_fixup", "conv_smallc"} <= kinds, kinds
+    assert any("_SK_" in l.kernel_name and l.kind == "conv" for l in c.module.plan)
+    assert any("_ST_" in l.kernel_name for l in c.module.plan)
+    got = _every_group_b32(c, feeds, want, hip_ctx)
+    assert len(got) == (23 if fold else 32)
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("fold", [True, False], ids=["residual_folded", "reference_groups"])
+def test_mobilenetv2_b32_every_group(fold, oracle_b32, hip_ctx):
+    """MobileNetV2 at batch 32 with its shipped schedules: every group in
+    isolation within rtol 1e-4 / atol 1e-5 (split-K conv and reduce, the
+    depthwise kernels at batch 32, the stem)."""
+    feeds, want = oracle_b32("mobilenetv2")
+    c = compile_graph(build_mobilenetv2(batch=32), feeds=feeds, fuse_residual=fold)
+    kinds = {l.kind for l in c.module.plan}
+    assert {"splitk_reduce", "dwconv", "conv_smallc"} <= kinds, kinds
+    _every_group_b32(c, feeds, want, hip_ctx)
+
+
 def test_resnet18_batch32_rows_match_single_images(hip_ctx):
     """At the benchmark batch the oracle is too slow for every image, so the
     device's batch-32 logits are checked against the oracle on two images

@@ -238,3 +238,188 @@ def test_a_planted_im2col_slip_is_caught(monkeypatch):
     monkeypatch.setattr(ops, "im2col", slipped)
     with pytest.raises(AssertionError):
         test_conv_matches_torch_float64(CONV_GEOMS[0])
+
+
+# ----- quantized global average pool (RepViT's head) ------------------------------
+
+def _qgap_brute(q, mult, flatten):
+    """Python-integer sum over each plane, one float32 multiply (float64
+    product of two float32 values is exact, then rounded once), Python's
+    round-half-even, clamp to [-127, 127]."""
+    n, c, h, w = q.shape
+    m = float(np.float32(mult))
+    out = []
+    for i in range(n):
+        row = []
+        for j in range(c):
+            s = sum(int(q[i, j, y, x]) for y in range(h) for x in range(w))
+            f = float(np.float32(float(np.float32(s)) * m))
+            row.append(max(-127, min(127, round(f))))
+        out.append(row if flatten else [[[v]] for v in row])
+    return np.array(out, dtype=np.int64)
+
+
+def _qgap_graph(shape, mult, flatten):
+    from mdlc_amd.ir import Graph, Node
+
+    g = Graph("qgap")
+    g.inputs, g.outputs = ["q"], ["y"]
+    g.add_node(Node("QGlobalAveragePool", ["q"], ["y"], {"mult": np.float32(mult), "flatten": flatten}))
+    return g
+
+
+@pytest.mark.parametrize("flatten", [False, True])
+def test_qgap_matches_integer_brute_force(flatten):
+    from oracle.reference import run_reference
+
+    rng = np.random.default_rng(21)
+    # 7x7 planes of codes, and a multiplier that puts ties (x.5) and values
+    # beyond +-127 among the results
+    q = rng.integers(-127, 128, (2, 6, 7, 7)).astype(np.int8)
+    q[0, 0] = 127                                   # sum 6223 -> saturates high
+    q[1, 1] = -127                                  # saturates low
+    q[0, 2] = 0
+    q[0, 2, 0, :3] = (1, 2, 2)                      # sum 5: 2.5 -> 2 (half to even)
+    q[0, 3] = 0
+    q[0, 3, 0, :2] = (3, 4)                         # sum 7: 3.5 -> 4
+    mult = 0.5
+    got = run_reference(_qgap_graph(q.shape, mult, flatten), {"q": q})["y"]
+    want = _qgap_brute(q, mult, flatten)
+    assert got.dtype == np.int8 and got.shape == want.shape
+    np.testing.assert_array_equal(got.astype(np.int64), want)
+    flat = want.reshape(2, 6)
+    assert flat[0, 0] == 127 and flat[1, 1] == -127 and flat[0, 2] == 2 and flat[0, 3] == 4
+    # the RepViT multiplier form s_in / (HW * s_out)
+    mult = np.float32(0.05 / (49 * 0.03))
+    np.testing.assert_array_equal(quant.global_avg_pool(q, mult).astype(np.int64),
+                                  _qgap_brute(q, mult, False))
+
+
+def test_qgap_planted_slips_are_caught(monkeypatch):
+    """Half-up rounding, or a sum over the wrong axes, must fail the check."""
+    real_rint = np.rint
+    monkeypatch.setattr(quant.np, "rint", lambda x: np.floor(np.asarray(x) + 0.5))
+    with pytest.raises(AssertionError):
+        test_qgap_matches_integer_brute_force(False)
+    monkeypatch.setattr(quant.np, "rint", real_rint)
+
+    real_gap = quant.global_avg_pool
+
+    def wrong_axes(q, mult):                        # sums the rows of one column only
+        acc = q.astype(np.int64).sum(axis=2, keepdims=True)[:, :, :, :1]
+        return quant.requant(acc.astype(np.int32), mult)
+
+    monkeypatch.setattr(quant, "global_avg_pool", wrong_axes)
+    with pytest.raises(AssertionError):
+        test_qgap_matches_integer_brute_force(False)
+    monkeypatch.setattr(quant, "global_avg_pool", real_gap)
+
+
+# ----- views, pad and matmul ------------------------------------------------------
+
+def _fill_c_order(values, shape):
+    """Place ``values`` (a flat list) into ``shape`` one index at a time in
+    row-major order, without NumPy's reshape."""
+    out = np.empty(shape, dtype=np.float64)
+    for k, idx in enumerate(np.ndindex(*shape)):
+        out[idx] = values[k]
+    return out
+
+
+@pytest.mark.parametrize("shape,axis", [((2, 3, 4, 5), 1), ((2, 3, 4, 5), 0), ((2, 3, 4, 5), 3),
+                                        ((2, 3, 4, 5), -2), ((6, 1, 1), 1), ((4,), 1)])
+def test_flatten_closed_form(shape, axis):
+    x = np.arange(int(np.prod(shape)), dtype=np.float32).reshape(shape) * 0.5 - 3
+    k = axis + len(shape) if axis < 0 else axis
+    lead = 1
+    for d in shape[:k]:
+        lead *= d
+    want_shape = (lead, int(np.prod(shape)) // lead)
+    got = ops.flatten(x, axis)
+    flat = [float(x[idx]) for idx in np.ndindex(*shape)]
+    assert got.shape == want_shape
+    np.testing.assert_array_equal(got, _fill_c_order(flat, want_shape))
+
+
+@pytest.mark.parametrize("shape,target,want_shape", [
+    ((2, 3, 4), [0, -1], (2, 12)),          # 0 copies the input dim
+    ((2, 3, 4), [4, 0, 2], (4, 3, 2)),
+    ((2, 3, 4), [-1], (24,)),
+    ((2, 512, 1, 1), [0, 512], (2, 512)),
+    ((6, 4), [2, 3, 4], (2, 3, 4)),
+])
+def test_reshape_closed_form(shape, target, want_shape):
+    x = np.arange(int(np.prod(shape)), dtype=np.float32).reshape(shape) - 7
+    got = ops.reshape(x, np.array(target, dtype=np.int64))
+    flat = [float(x[idx]) for idx in np.ndindex(*shape)]
+    assert got.shape == want_shape
+    np.testing.assert_array_equal(got, _fill_c_order(flat, want_shape))
+
+
+def _pad_brute(x, pads, value, mode):
+    half = len(pads) // 2
+    before, after = pads[:half], pads[half:]
+    out_shape = tuple(s + b + a for s, b, a in zip(x.shape, before, after))
+    out = np.empty(out_shape, dtype=np.float64)
+    for idx in np.ndindex(*out_shape):
+        src, inside = [], True
+        for d, i in enumerate(idx):
+            j, n = i - before[d], x.shape[d]
+            if 0 <= j < n:
+                src.append(j)
+            elif mode == "constant":
+                inside = False
+                break
+            elif mode == "edge":
+                src.append(min(max(j, 0), n - 1))
+            else:                                   # reflect: mirror without repeating the edge
+                period = 2 * (n - 1)
+                j = abs(j) % period
+                src.append(period - j if j >= n else j)
+        out[idx] = float(x[tuple(src)]) if inside else value
+    return out
+
+
+@pytest.mark.parametrize("mode,value", [("constant", 0.0), ("constant", -2.5), ("edge", 0.0),
+                                        ("reflect", 0.0)])
+def test_pad_brute_force(mode, value):
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((2, 3, 4, 5)).astype(np.float32)
+    pads = [0, 1, 2, 0, 0, 0, 1, 3]                 # begins then ends, per axis
+    got = ops.pad(x, np.array(pads), value, mode)
+    np.testing.assert_array_equal(got.astype(np.float64), _pad_brute(x, pads, value, mode))
+
+
+@pytest.mark.parametrize("a_shape,b_shape", [((5, 7), (7, 3)), ((2, 5, 7), (7, 3)),
+                                             ((2, 5, 7), (2, 7, 3)), ((1, 9), (9, 1))])
+def test_matmul_brute_force(a_shape, b_shape):
+    rng = np.random.default_rng(41)
+    a = rng.standard_normal(a_shape).astype(np.float32)
+    b = rng.standard_normal(b_shape).astype(np.float32)
+    got = ops.matmul(a, b)
+    A = a.reshape((-1,) + a_shape[-2:]).astype(np.float64)
+    B = np.broadcast_to(b, a_shape[:-2] + b_shape[-2:]).reshape((-1,) + b_shape[-2:]).astype(np.float64)
+    want = np.zeros((A.shape[0], a_shape[-2], b_shape[-1]))
+    for n in range(A.shape[0]):
+        for i in range(a_shape[-2]):
+            for j in range(b_shape[-1]):
+                want[n, i, j] = sum(A[n, i, k] * B[n, k, j] for k in range(a_shape[-1]))
+    assert got.shape == a_shape[:-1] + b_shape[-1:]
+    np.testing.assert_allclose(got.reshape(want.shape), want, rtol=1e-5, atol=1e-5)
+
+
+def test_view_and_matmul_planted_slips_are_caught(monkeypatch):
+    monkeypatch.setattr(ops, "matmul", lambda a, b: a @ b[..., ::-1])   # columns out of order
+    with pytest.raises(AssertionError):
+        test_matmul_brute_force((5, 7), (7, 3))
+    monkeypatch.undo()
+    monkeypatch.setattr(ops, "flatten", lambda x, axis=1: x.transpose().reshape(
+        int(np.prod(x.shape[:axis])) if axis > 0 else 1, -1))
+    with pytest.raises(AssertionError):
+        test_flatten_closed_form((2, 3, 4, 5), 1)
+    monkeypatch.undo()
+    real_pad = ops.pad
+    monkeypatch.setattr(ops, "pad", lambda x, pads, value=0.0, mode="constant":
+                        real_pad(x, np.roll(np.asarray(pads), len(pads) // 2), value, mode))
+    with pytest.raises(AssertionError):
+        test_pad_brute_force("constant", -2.5)
