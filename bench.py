@@ -5,15 +5,20 @@
 The default workload is the headline config: ResNet-18 fp32 at batch 32. One
 step is one forward pass of the whole network over one batch of synthetic
 N(0,1) images already resident in device memory (random-init weights of the
-config's architecture and distributions). Other workloads (for the other
-benchmark configs): ``mobilenetv2``, ``repvit_int8`` (bit-exact INT8 model),
-``micro_gemm`` (the five fused GEMM+bias+ReLU shapes), ``int8_gemm``
-(M = N = K = 4096, the compute-bound int8 shape).
+config's architecture and distributions). The default run also measures the
+other benchmark configs and reports them under ``config.secondary``:
+ResNet-18 b=1, MobileNetV2 b=1 and b=32, the RepViT-style INT8 model at b=32,
+the five fused GEMM+bias+ReLU micro shapes and the int8 GEMM at 4096^3
+(``--no-secondary`` skips them). Each config can also be run on its own with
+``--workload`` (``mobilenetv2``, ``repvit_int8``, ``micro_gemm``,
+``int8_gemm``).
 
-Prints one JSON line: throughput, the dominant kernel's roofline (its
+Prints one JSON line: throughput; the dominant kernel's roofline (its
 algorithmic work per launch over its average launch time, timed per launch
-with HIP events on the library's stream), and the NumPy oracle timed on the
-host cores over a bounded sample.
+with HIP events on the library's stream), also for the kernel together with
+the split-K reduce or stream-K fix-up launch that finishes its output; and
+the NumPy oracle timed on the host cores over a bounded sample, before the
+first device call.
 """
 
 from __future__ import annotations
@@ -21,6 +26,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
 import sys
 import time
 
@@ -34,37 +40,93 @@ PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_INT8_MFMA_TOPS = 5000.0
 PEAK_HBM_GBS = 8000.0
 CALIBRATION = "each Conv/Gemm LSUV-rescaled to unit output std as the reference exporters do"
+FINISHERS = ("splitk_reduce", "streamk_fixup")
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-# ----- CPU baseline: the oracle on a bounded sample -----------------------------
+# ----- host description and the CPU baseline ---------------------------------------
 
-def cpu_baseline(graph, make_feeds, seconds: float = 12.0, what: str = "forwards") -> dict:
-    """Time the NumPy oracle (a restatement of the reference executor) on
-    single-image feeds, repeated until ``seconds`` have elapsed."""
+def host_info() -> dict:
+    """What the CPU baseline ran on: model, logical CPUs, the CPUs this
+    process may use, thread settings and the BLAS thread pool."""
+    import numpy  # noqa: F401  (loads the bundled BLAS so it can be inspected)
+
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    pools = []
+    try:
+        from threadpoolctl import threadpool_info
+
+        pools = [{"api": p.get("internal_api"), "threads": p.get("num_threads")}
+                 for p in threadpool_info()]
+    except Exception:
+        pass
+    env = {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS",
+                                          "MKL_NUM_THREADS")}
+    return {"cpu_model": model, "cpu_count": os.cpu_count(), "usable_cpus": usable,
+            "env": env, "blas_pools": pools}
+
+
+def _threads_used(info: dict) -> int:
+    """Threads the oracle can run on: its convolutions are single-threaded
+    NumPy einsum loops, its matrix products use the BLAS pool."""
+    return max([1] + [p["threads"] or 1 for p in info["blas_pools"]])
+
+
+def cpu_baseline_network(name: str, seconds: float = 8.0) -> dict:
+    """The NumPy oracle (a restatement of the reference executor) on the
+    host: single images repeated for ``seconds``, then one forward of the
+    benchmark's batch of 32."""
+    from mdlc_amd.compiler import compile_graph
     from oracle.reference import ReferenceExecutor
 
-    ex = ReferenceExecutor(graph)
-    feeds = make_feeds()
-    ex.run(feeds)
+    build, make_input = builders(name)
+    info = host_info()
+    x1 = make_input(1, seed=7)
+    ex1 = ReferenceExecutor(compile_graph(build(batch=1), feeds={"input": x1}).graph)
+    ex1.run({"input": x1})
     n, t0 = 0, time.perf_counter()
     while True:
-        ex.run(feeds)
+        ex1.run({"input": x1})
         n += 1
         el = time.perf_counter() - t0
         if el >= seconds and n >= 2:
             break
-    return {"value": n / el, "unit": "images/s", "cores": 1, "kind": "port",
-            "sample": f"{n} single-image {what} through the NumPy oracle (the reference "
-                      f"executor's algorithm), {el:.1f} s, 1 thread, host of the GPU box"}
+    b1 = n / el
+    x32 = make_input(32)
+    ex32 = ReferenceExecutor(compile_graph(build(batch=32), feeds={"input": x32}).graph)
+    t0 = time.perf_counter()
+    ex32.run({"input": x32})
+    t32 = time.perf_counter() - t0
+    threads = _threads_used(info)
+    return {"value": 32 / t32, "unit": "images/s", "cores": threads, "kind": "port",
+            "sample": f"one batch-32 {name} forward ({t32:.1f} s) and {n} single-image forwards "
+                      f"({el:.1f} s, {b1:.2f} images/s) through the NumPy oracle (the reference "
+                      f"executor's algorithm: einsum convolutions, single-threaded; BLAS matrix "
+                      f"products on up to {threads} threads), host of the GPU box",
+            "batch1_images_per_s": b1, "host": info}
 
 
-# ----- device timing -----------------------------------------------------------------
+# ----- device timing ------------------------------------------------------------------
 
-def time_module(c, feeds, steps: int, warmup: int, profile_iters: int, use_graph: bool = False):
+def time_module(c, feeds, steps: int, warmup: int, profile_iters: int, use_graph: bool = False,
+                host_loop: bool = True):
+    """(ms per step by events, host seconds per step including the feed
+    upload and output read, per-launch profile, arena bytes)."""
     from mdlc_amd.codegen.hip.hip_executor import HipExecutor
 
     ex = HipExecutor(c.module, use_graph=use_graph)
@@ -73,10 +135,12 @@ def time_module(c, feeds, steps: int, warmup: int, profile_iters: int, use_graph
         ex.plan.run(warmup)
         ex.ctx.synchronize()
         ms = ex.plan.time_ms(0, steps)
-        t1 = time.perf_counter()
-        for _ in range(steps):
-            ex.run(feeds)
-        host_s = (time.perf_counter() - t1) / steps
+        host_s = None
+        if host_loop:
+            t1 = time.perf_counter()
+            for _ in range(steps):
+                ex.run(feeds)
+            host_s = (time.perf_counter() - t1) / steps
         prof = ex.profile(profile_iters)
         arena = ex.arena_bytes
     finally:
@@ -84,7 +148,29 @@ def time_module(c, feeds, steps: int, warmup: int, profile_iters: int, use_graph
     return ms, host_s, prof, arena
 
 
-def roofline(prof, *, traffic_json: str = "") -> tuple:
+def _bound(work: float, nbytes: float, peak: float) -> bool:
+    """MFMA-bound when the algorithmic intensity reaches the ridge point
+    peak / HBM bandwidth."""
+    ridge = peak * 1e12 / (PEAK_HBM_GBS * 1e9)
+    return bool(work) and (not nbytes or work / nbytes >= ridge)
+
+
+def _rate(work: float, nbytes: float, ms: float, int8: bool) -> dict:
+    peak = PEAK_INT8_MFMA_TOPS if int8 else PEAK_FP32_MFMA_TFLOPS
+    if _bound(work, nbytes, peak):
+        ach = work / (ms * 1e-3) / 1e12
+        r = {"bound": "mfma", "achieved": ach, "peak": peak, "unit": "TOP/s" if int8 else "TFLOP/s"}
+    else:
+        ach = nbytes / (ms * 1e-3) / 1e9
+        r = {"bound": "hbm", "achieved": ach, "peak": PEAK_HBM_GBS, "unit": "GB/s"}
+    r["frac"] = r["achieved"] / r["peak"]
+    return r
+
+
+def roofline(prof, *, traffic_json: str = "", verbose: bool = True) -> tuple:
+    """Roofline of the kernel with the largest share of the step, per launch,
+    plus the same kernel together with the split-K reduce / stream-K fix-up
+    launches that finish its output (``group``)."""
     per: dict = {}
     for launch, ms in prof:
         d = per.setdefault(launch.kernel_name, {"ms": 0.0, "flops": 0, "ops": 0, "bytes": 0,
@@ -95,31 +181,22 @@ def roofline(prof, *, traffic_json: str = "") -> tuple:
         d["bytes"] += launch.meta.get("bytes", 0)
         d["launches"] += 1
     total = sum(d["ms"] for d in per.values())
-    for name, d in sorted(per.items(), key=lambda kv: -kv[1]["ms"])[:24]:
-        if d["flops"]:
-            rate = f"{d['flops'] / d['ms'] / 1e9:8.1f} TFLOP/s"
-        elif d["ops"]:
-            rate = f"{d['ops'] / d['ms'] / 1e9:8.1f} TOP/s"
-        else:
-            rate = f"{d['bytes'] / d['ms'] / 1e6:8.1f} GB/s"
-        log(f"  {name:58s} {d['launches']:3d}x {d['ms']:8.3f} ms {rate}")
+    if verbose:
+        for name, d in sorted(per.items(), key=lambda kv: -kv[1]["ms"])[:24]:
+            if d["flops"]:
+                rate = f"{d['flops'] / d['ms'] / 1e9:8.1f} TFLOP/s"
+            elif d["ops"]:
+                rate = f"{d['ops'] / d['ms'] / 1e9:8.1f} TOP/s"
+            else:
+                rate = f"{d['bytes'] / d['ms'] / 1e6:8.1f} GB/s"
+            log(f"  {name:58s} {d['launches']:3d}x {d['ms']:8.3f} ms {rate}")
     name, d = max(per.items(), key=lambda kv: kv[1]["ms"])
     avg = d["ms"] / d["launches"]
-    # The bound is the roofline's: matrix cores when the kernel's algorithmic
-    # intensity (flops or ops per algorithmic HBM byte) is at or above the
-    # ridge point peak/8 TB/s, else HBM bandwidth.
-    work, peak, unit = ((d["flops"], PEAK_FP32_MFMA_TFLOPS, "TFLOP/s") if d["flops"] else
-                        (d["ops"], PEAK_INT8_MFMA_TOPS, "TOP/s"))
-    ridge = peak * 1e12 / (PEAK_HBM_GBS * 1e9)
-    if work and (not d["bytes"] or work / d["bytes"] >= ridge):
-        ach = work / d["launches"] / (avg * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": ach, "peak": peak, "unit": unit}
-    else:
-        ach = d["bytes"] / d["launches"] / (avg * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": ach, "peak": PEAK_HBM_GBS, "unit": "GB/s"}
+    int8 = not d["flops"] and bool(d["ops"])
+    work = d["flops"] or d["ops"]
+    roof = _rate(work / d["launches"], d["bytes"] / d["launches"], avg, int8)
     if work and d["bytes"]:
         roof["intensity"] = work / d["bytes"]
-    roof["frac"] = roof["achieved"] / roof["peak"]
     roof["traffic"] = None
     if traffic_json and os.path.exists(traffic_json):
         # HBM bytes per dispatch from the committed rocprofv3 FETCH_SIZE /
@@ -131,10 +208,38 @@ def roofline(prof, *, traffic_json: str = "") -> tuple:
             roof["traffic"] = m["traffic_bytes"]
     roof.update({"kernel": name, "launches_per_step": d["launches"], "avg_launch_ms": avg,
                  "share_of_step": d["ms"] / total})
+    # the launches that finish this kernel's output (same graph node, next in the plan)
+    group_ms, finishers = [], set()
+    for i, (launch, ms) in enumerate(prof):
+        if launch.kernel_name != name:
+            continue
+        t = ms
+        for nxt, nms in prof[i + 1:]:
+            if nxt.kind in FINISHERS and nxt.meta.get("node") is launch.meta.get("node"):
+                t += nms
+                finishers.add(nxt.kernel_name)
+            else:
+                break
+        group_ms.append(t)
+    if finishers:
+        gavg = sum(group_ms) / len(group_ms)
+        g = _rate(work / d["launches"], d["bytes"] / d["launches"], gavg, int8)
+        roof["group"] = {"kernels": [name] + sorted(finishers), "avg_ms": gavg,
+                         "achieved": g["achieved"], "frac": g["frac"]}
     return roof, per
 
 
 # ----- workloads ------------------------------------------------------------------------
+
+def builders(name: str):
+    if name == "resnet18":
+        from mdlc_amd.tools.build_resnet18 import build_resnet18 as build, make_input
+    elif name == "mobilenetv2":
+        from mdlc_amd.tools.build_mobilenetv2 import build_mobilenetv2 as build, make_input
+    else:
+        from mdlc_amd.tools.build_repvit_int8 import build_repvit_int8 as build, make_input
+    return build, make_input
+
 
 def schedule_source(args):
     """The shipped measured schedules, or those of ``--schedules PATH`` (a
@@ -146,99 +251,92 @@ def schedule_source(args):
     return Tuner(AutotuneCache(args.schedules), tune_misses=False)
 
 
-def network(args, name: str) -> dict:
+def compile_network(args, name: str, batch: int):
     from mdlc_amd.compiler import compile_graph
 
-    B = args.batch
-    if name == "resnet18":
-        from mdlc_amd.tools.build_resnet18 import build_resnet18 as build, make_input
-    elif name == "mobilenetv2":
-        from mdlc_amd.tools.build_mobilenetv2 import build_mobilenetv2 as build, make_input
-    else:
-        from mdlc_amd.tools.build_repvit_int8 import build_repvit_int8 as build, make_input
-    x = make_input(B)
+    build, make_input = builders(name)
+    x = make_input(batch)
     t0 = time.perf_counter()
     folds = dict(fuse_residual=False, fuse_int8_epilogues=False) if args.no_fold else {}
-    c = compile_graph(build(batch=B), feeds={"input": x}, conv_mode=args.conv_mode,
+    c = compile_graph(build(batch=batch), feeds={"input": x}, conv_mode=args.conv_mode,
                       schedule_fn=schedule_source(args), **folds)
-    log(f"{name} b={B}: compiled in {time.perf_counter() - t0:.1f} s, {len(c.module.plan)} launches")
-    ms, host_s, prof, arena = time_module(c, {"input": x}, args.steps, args.warmup,
-                                          args.profile_iters, args.graph)
-    value = B * 1000.0 / ms
-    log(f"{ms:.3f} ms/step, {value:.1f} images/s (arena {arena / 2**20:.1f} MiB)")
-    traffic = TRAFFIC_JSON if (name == "resnet18" and B == 32 and not args.no_fold) else ""
-    roof, _ = roofline(prof, traffic_json=traffic)
+    log(f"{name} b={batch}: compiled in {time.perf_counter() - t0:.1f} s, {len(c.module.plan)} launches")
+    return c, {"input": x}
+
+
+def network(args, name: str, batch: int, *, steps: int, headline: bool) -> dict:
+    c, feeds = compile_network(args, name, batch)
+    ms, host_s, prof, arena = time_module(c, feeds, steps, args.warmup, args.profile_iters,
+                                          args.graph, host_loop=headline)
+    value = batch * 1000.0 / ms
+    log(f"{name} b={batch}: {ms:.3f} ms/step, {value:.1f} images/s (arena {arena / 2**20:.1f} MiB)")
+    traffic = TRAFFIC_JSON if (name == "resnet18" and batch == 32 and not args.no_fold) else ""
+    roof, _ = roofline(prof, traffic_json=traffic, verbose=headline)
     int8 = name == "repvit_int8"
     work = sum(l.meta.get("ops" if int8 else "flops", 0) for l in c.module.plan)
-    metric = METRIC if (name == "resnet18" and B == 32) else \
-        f"{name} b={B} {'int8' if int8 else 'fp32'} images/sec"
-    if int8:
-        data = ("synthetic N(0,1) images, random-init int8 weights (w ~ N(0,0.05), per-channel "
-                "scales), activation scales U(0.01,0.1)")
-    else:
-        data = ("synthetic N(0,1) images, random-init weights (Kaiming-normal conv/FC, BN gamma "
-                "U(0.5,1.5) beta N(0,0.1) mean N(0,0.1) var U(0.5,1.5); " + CALIBRATION + ")")
-    line = {
-        "metric": metric, "value": value, "unit": "images/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "i8" if int8 else "f32", "data": data,
-        "config": {"workload": f"{name}_{'int8' if int8 else 'fp32'}_b{B}", "batch": B,
-                   "image": [3, 224, 224], "conv_mode": args.conv_mode,
-                   "backend_folds": not args.no_fold,
-                   "launches": len(c.module.plan), "gop_per_step": work / 1e9,
-                   ("network_tops" if int8 else "network_tflops"): work / (ms * 1e-3) / 1e12,
-                   "host_buffer_images_per_s": B / host_s},
-        "roofline": roof,
-    }
-    if not args.no_cpu_baseline:
-        c1 = compile_graph(build(batch=1), feeds={"input": make_input(1, seed=7)})
-        line["cpu_baseline"] = cpu_baseline(c1.graph, lambda: {"input": make_input(1, seed=7)},
-                                            what=f"{name} forwards")
+    metric = METRIC if (name == "resnet18" and batch == 32) else \
+        f"{name} b={batch} {'int8' if int8 else 'fp32'} images/sec"
+    line = {"metric": metric, "value": value, "unit": "images/s", "ms_per_step": ms,
+            "steps": steps, "dtype": "i8" if int8 else "f32",
+            "workload": f"{name}_{'int8' if int8 else 'fp32'}_b{batch}",
+            "launches": len(c.module.plan), "gop_per_step": work / 1e9,
+            ("network_tops" if int8 else "network_tflops"): work / (ms * 1e-3) / 1e12,
+            "roofline": roof}
+    if host_s:
+        line["host_buffer_images_per_s"] = batch / host_s
     return line
 
 
-def micro_gemm(args) -> dict:
+def micro_gemm(args, *, steps: int, cpu: bool) -> dict:
     from mdlc_amd.compiler import compile_graph
     from mdlc_amd.tools.micro_gemm import SHAPES, build_micro_gemm
 
-    shapes, total_flops, total_ms, cpu = {}, 0.0, 0.0, {}
+    shapes, total_flops, total_ms, cpu_rates = {}, 0.0, 0.0, {}
+    compiled = []
     for M, N, K in SHAPES:
         g, feeds = build_micro_gemm(M, N, K)
-        c = compile_graph(g, feeds=feeds, schedule_fn=schedule_source(args))
-        ms, _, _, _ = time_module(c, feeds, args.steps * 10, args.warmup, args.profile_iters)
-        fl = 2.0 * M * N * K
-        key = f"{M}x{N}x{K}"
-        shapes[key] = {"us": ms * 1e3, "tflops": fl / (ms * 1e-3) / 1e12,
-                       "frac_fp32_peak": fl / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS,
-                       "launches": len(c.module.plan)}
-        total_flops += fl
-        total_ms += ms
-        if not args.no_cpu_baseline:
-            from oracle.reference import run_reference
+        compiled.append(((M, N, K), compile_graph(g, feeds=feeds, schedule_fn=schedule_source(args)),
+                         feeds))
+    if cpu:                                   # host leg first, before any device call
+        from oracle.reference import run_reference
 
+        for (M, N, K), c, feeds in compiled:
             run_reference(c.graph, feeds)
             t0, n = time.perf_counter(), 0
-            while time.perf_counter() - t0 < 1.5 or n < 2:
+            while time.perf_counter() - t0 < 1.0 or n < 2:
                 run_reference(c.graph, feeds)
                 n += 1
-            cpu[key] = fl * n / (time.perf_counter() - t0) / 1e9
-        log(f"{key}: {ms * 1e3:.1f} us, {shapes[key]['tflops']:.1f} TFLOP/s")
+            cpu_rates[f"{M}x{N}x{K}"] = 2.0 * M * N * K * n / (time.perf_counter() - t0) / 1e9
+    for (M, N, K), c, feeds in compiled:
+        ms, _, prof, _ = time_module(c, feeds, steps, args.warmup, args.profile_iters,
+                                     host_loop=False)
+        fl = 2.0 * M * N * K
+        key = f"{M}x{N}x{K}"
+        roof, _ = roofline(prof, verbose=False)
+        shapes[key] = {"us": ms * 1e3, "tflops": fl / (ms * 1e-3) / 1e12,
+                       "frac_fp32_peak": fl / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS,
+                       "launches": len(c.module.plan),
+                       "step_roofline": _rate(fl, 4.0 * (M * K + K * N + N + M * N), ms, False),
+                       "roofline": roof}
+        total_flops += fl
+        total_ms += ms
+        log(f"micro {key}: {ms * 1e3:.1f} us, {shapes[key]['tflops']:.1f} TFLOP/s "
+            f"({len(c.module.plan)} launches)")
     line = {"metric": "fused GEMM+bias+ReLU micro-workload TFLOP/s (5 ResNet-18 batch-1 shapes)",
-            "value": total_flops / (total_ms * 1e-3) / 1e12, "unit": "TFLOP/s", "n_gpus": 1,
-            "steps": args.steps * 10, "warmup": args.warmup, "ms_per_step": total_ms,
-            "higher_is_better": True, "scaling": "strong", "vs_baseline": None, "dtype": "f32",
-            "data": "synthetic A, B, bias ~ N(0,1)/sqrt(K), fixed seed per shape",
-            "config": {"workload": "micro_gemm_bias_relu", "shapes": shapes}}
-    if cpu:
+            "value": total_flops / (total_ms * 1e-3) / 1e12, "unit": "TFLOP/s",
+            "ms_per_step": total_ms, "steps": steps, "dtype": "f32",
+            "workload": "micro_gemm_bias_relu", "shapes": shapes}
+    if cpu_rates:
+        info = host_info()
         line["cpu_baseline"] = {
-            "value": sum(cpu.values()) / len(cpu), "unit": "GFLOP/s (mean over shapes)",
-            "cores": 1, "kind": "port",
-            "sample": "each shape through the NumPy oracle (A @ B + bias, relu) for >= 1.5 s: "
-                      + ", ".join(f"{k}: {v:.1f}" for k, v in cpu.items())}
+            "value": sum(cpu_rates.values()) / len(cpu_rates), "unit": "GFLOP/s (mean over shapes)",
+            "cores": _threads_used(info), "kind": "port", "host": info,
+            "sample": "each shape through the NumPy oracle (A @ B + bias, relu; BLAS) for >= 1 s: "
+                      + ", ".join(f"{k}: {v:.1f}" for k, v in cpu_rates.items())}
     return line
 
 
-def int8_gemm(args) -> dict:
+def int8_gemm(args, *, steps: int, cpu: bool) -> dict:
     import numpy as np
 
     from mdlc_amd.compiler import compile_graph
@@ -248,22 +346,80 @@ def int8_gemm(args) -> dict:
     rng = np.random.default_rng(0)
     b = GraphBuilder("i8gemm")
     b.input("xq", (M, K), dtype="int8")
-    b.const("w", rng.integers(-127, 128, (N, K)).astype(np.int8))
+    w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    b.const("w", w)
     b.const("b", rng.integers(-1000, 1000, N).astype(np.int32))
     b.const("m", rng.uniform(2e-6, 1e-5, N).astype(np.float32))
     b.node("QGemm", ["xq", "w", "b", "m"], "y", transB=1)
     b.output("y")
     feeds = {"xq": rng.integers(-127, 128, (M, K)).astype(np.int8)}
     c = compile_graph(b.graph(), feeds=feeds, schedule_fn=schedule_source(args))
-    ms, _, prof, _ = time_module(c, feeds, args.steps, args.warmup, args.profile_iters)
+    cpu_line = None
+    if cpu:                                   # host leg first: 32 rows through the oracle
+        from oracle.quant import gemm_acc, requant
+
+        rows = 32
+        t0 = time.perf_counter()
+        requant(gemm_acc(feeds["xq"][:rows], w, None), np.ones(N, np.float32) * 1e-5)
+        el = time.perf_counter() - t0
+        info = host_info()
+        cpu_line = {"value": 2.0 * rows * N * K / el / 1e12, "unit": "TOP/s", "cores": 1,
+                    "kind": "port", "host": info,
+                    "sample": f"{rows} of the {M} rows through the oracle's exact int64 "
+                              f"matmul + requant ({el:.2f} s; NumPy integer matmul, one thread)"}
+    ms, _, prof, _ = time_module(c, feeds, steps, args.warmup, args.profile_iters, host_loop=False)
     tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-    roof, _ = roofline(prof)
+    roof, _ = roofline(prof, verbose=False)
     log(f"int8 GEMM {M}^3: {ms * 1e3:.1f} us, {tops:.0f} TOP/s")
-    return {"metric": f"int8 GEMM {M}x{N}x{K} TOP/s (int32 acc, requantized int8 out)",
-            "value": tops, "unit": "TOP/s", "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True,
-            "scaling": "strong", "vs_baseline": None, "dtype": "i8", "data": "synthetic int8 codes",
-            "config": {"workload": "int8_gemm", "M": M, "N": N, "K": K}, "roofline": roof}
+    line = {"metric": f"int8 GEMM {M}x{N}x{K} TOP/s (int32 acc, requantized int8 out)",
+            "value": tops, "unit": "TOP/s", "ms_per_step": ms, "steps": steps, "dtype": "i8",
+            "workload": "int8_gemm", "M": M, "N": N, "K": K, "roofline": roof}
+    if cpu_line:
+        line["cpu_baseline"] = cpu_line
+    return line
+
+
+def full_line(args, part: dict, *, scaling: str, data: str, config: dict) -> dict:
+    """The driver's JSON contract around one measured part."""
+    keep = {k: v for k, v in part.items()
+            if k in ("launches", "gop_per_step", "network_tflops", "network_tops",
+                     "host_buffer_images_per_s", "shapes", "M", "N", "K")}
+    out = {"metric": part["metric"], "value": part["value"], "unit": part["unit"], "n_gpus": 1,
+           "steps": part["steps"], "warmup": args.warmup, "ms_per_step": part["ms_per_step"],
+           "higher_is_better": True, "scaling": scaling, "vs_baseline": None,
+           "dtype": part["dtype"], "data": data,
+           "config": {"workload": part["workload"], **config, **keep}}
+    if "roofline" in part:
+        out["roofline"] = part["roofline"]
+    if "cpu_baseline" in part:
+        out["cpu_baseline"] = part["cpu_baseline"]
+    return out
+
+
+def data_text(name: str) -> str:
+    if name == "repvit_int8":
+        return ("synthetic N(0,1) images, random-init int8 weights (w ~ N(0,0.05), per-channel "
+                "scales), activation scales U(0.01,0.1)")
+    if name in ("micro_gemm", "int8_gemm"):
+        return ("synthetic A, B, bias ~ N(0,1)/sqrt(K), fixed seed per shape" if name == "micro_gemm"
+                else "synthetic int8 codes")
+    return ("synthetic N(0,1) images, random-init weights (Kaiming-normal conv/FC, BN gamma "
+            "U(0.5,1.5) beta N(0,0.1) mean N(0,0.1) var U(0.5,1.5); " + CALIBRATION + ")")
+
+
+def secondary(args) -> dict:
+    """The other benchmark configs, each with its own roofline block."""
+    out = {}
+    for name, batch, steps in (("resnet18", 1, 50), ("mobilenetv2", 1, 50), ("mobilenetv2", 32, 20),
+                               ("repvit_int8", 32, 20)):
+        part = network(args, name, batch, steps=steps, headline=False)
+        out[part["workload"]] = {k: v for k, v in part.items() if k not in ("workload", "dtype")}
+    out["micro_gemm_bias_relu"] = micro_gemm(args, steps=200, cpu=False)
+    size = args.size
+    args.size = 4096
+    out["int8_gemm_4096"] = int8_gemm(args, steps=20, cpu=False)
+    args.size = size
+    return out
 
 
 def main(argv=None) -> int:
@@ -282,6 +438,8 @@ def main(argv=None) -> int:
     ap.add_argument("--no-fold", action="store_true",
                     help="the reference's fused groups only (no residual / int8 / pool folds)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="measure only the selected workload")
     ap.add_argument("--profile-iters", type=int, default=3)
     args = ap.parse_args(argv)
     if args.gpus != 1:
@@ -289,12 +447,24 @@ def main(argv=None) -> int:
               "inference shards by batch across GPUs, which is not part of this build",
               file=sys.stderr)
         return 2
-    if args.workload == "micro_gemm":
-        line = micro_gemm(args)
-    elif args.workload == "int8_gemm":
-        line = int8_gemm(args)
+    cpu = not args.no_cpu_baseline
+    w = args.workload
+    if w == "micro_gemm":
+        part = micro_gemm(args, steps=args.steps * 10, cpu=cpu)
+        line = full_line(args, part, scaling="strong", data=data_text(w), config={})
+    elif w == "int8_gemm":
+        part = int8_gemm(args, steps=args.steps, cpu=cpu)
+        line = full_line(args, part, scaling="strong", data=data_text(w), config={})
     else:
-        line = network(args, args.workload)
+        base = cpu_baseline_network(w) if cpu else None      # host leg before any device call
+        part = network(args, w, args.batch, steps=args.steps, headline=True)
+        if base:
+            part["cpu_baseline"] = base
+        line = full_line(args, part, scaling="weak", data=data_text(w),
+                         config={"batch": args.batch, "image": [3, 224, 224],
+                                 "conv_mode": args.conv_mode, "backend_folds": not args.no_fold})
+        if w == "resnet18" and args.batch == 32 and not args.no_secondary:
+            line["config"]["secondary"] = secondary(args)
     print(json.dumps(line), flush=True)
     return 0
 

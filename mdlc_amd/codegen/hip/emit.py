@@ -10,6 +10,7 @@ extended because nothing runs on the host here:
 
   gemm        dense GEMM + epilogue (Gemm/MatMul, and conv after im2col)
   conv        implicit-GEMM convolution (no column buffer)
+  gconv       grouped convolution: the implicit GEMM with one grid row per group
   conv_smallc direct convolution for few input channels (stems): input patch
               in LDS, weights in registers, matrix cores
   im2col      batched column matrix for the explicit conv path
@@ -19,7 +20,8 @@ extended because nothing runs on the host here:
   quantize, qgemm, qconv, qdwconv, qadd, qlut, qgap, dequantize, qmlp,
   qconv_first (INT8 path, int8 activations channels-last on the device)
   elementwise fused pointwise chain (also single pointwise ops)
-  maxpool, gap, copy (reshaping views: Flatten/Reshape/Identity/...)
+  maxpool, avgpool, gap, copy (reshaping views: Flatten/Reshape/Identity/...)
+  softmax, transpose, pad, concat (one launch per Concat operand)
 
 Every op of the graph gets a device launch or lowering raises
 ``NotImplementedError``: there is no host fallback. Constant operands that
@@ -43,7 +45,7 @@ from mdlc_amd.codegen.hip.emit_int8 import Int8LoweringMixin
 from mdlc_amd.codegen.hip.plan import LIBRARY_PARTS, QUANT_OPS, HipModule, Launch, round4, round16  # noqa: F401
 from mdlc_amd.codegen.schedule import (MfmaSchedule, default_schedule, smallc_fits, smallc_pairs,
                                       smallc_tile, split_slices)
-from mdlc_amd.ir import Graph, Node
+from mdlc_amd.ir import DType, Graph, Node
 from mdlc_amd.passes.fuse_elementwise import ELEMENTWISE
 from mdlc_amd.passes.shape_inference import conv_geometry
 
@@ -163,12 +165,14 @@ class HipCodegen(Int8LoweringMixin):
                 solo = Node("FusedElementwise", node.real_inputs(), list(node.outputs),
                             {"subgraph": [node]}, node.name, [op])
                 self._lower_elementwise(g, solo, origin=node)
-            elif op == "MaxPool":
-                self._lower_maxpool(g, node)
+            elif op in ("MaxPool", "AveragePool"):
+                self._lower_pool(g, node)
             elif op == "GlobalAveragePool":
                 self._lower_gap(g, node)
             elif op in VIEW_OPS:
                 self._lower_view(g, node)
+            elif op in ("Softmax", "Transpose", "Pad", "Concat"):
+                getattr(self, "_lower_" + op.lower())(g, node)
             elif op in QUANT_OPS:
                 getattr(self, "_lower_" + op.lower())(g, node)
             else:
@@ -187,7 +191,10 @@ class HipCodegen(Int8LoweringMixin):
         a = node.attrs
         act = a.get("activation")
         if geo["group"] != 1:
-            self._lower_dwconv(g, node, geo, has_bias)
+            if geo["ICG"] == 1 and geo["OC"] % geo["C"] == 0:
+                self._lower_dwconv(g, node, geo, has_bias)
+            else:
+                self._lower_grouped_conv(g, node, geo, has_bias)
             return
         if self.conv_mode == "implicit" and self.small_conv and smallc_fits(geo["C"], geo["KH"], geo["KW"], geo["DH"],
                                                         geo["DW"]):
@@ -245,6 +252,62 @@ class HipCodegen(Int8LoweringMixin):
         meta.update({"ldb": ldc})
         self._emit_gemm("gemm", sched, [wdev, cols], bias, y, meta, epi, bmode=0, vec_a=True,
                         out_nchw=True)
+
+    def _lower_grouped_conv(self, g: Graph, node: Node, geo: dict, has_bias: bool) -> None:
+        """A grouped convolution (1 < group, more than one input channel per
+        group) as one launch of the implicit-GEMM conv over all groups: the
+        grid's y index is the group, whose GEMM is M = OC/group, N = batch *
+        OH * OW, K = C/group * KH * KW over its own input channels and weight
+        rows, scattered to its own output channels. The reference runs this
+        op on the host (mdlc/codegen/cuda/emit.py:175-180, runtime/ops.py:69-78).
+        Both conv modes use the gather (no per-group column matrices); the
+        schedule runs without split-K or stream-K."""
+        G, OC, C = geo["group"], geo["OC"], geo["C"]
+        if OC % G or C % G:
+            raise ValueError(f"group {G} does not divide channels {C} -> {OC}")
+        ocg, icg = OC // G, geo["ICG"]
+        KH, KW, OH, OW, N = geo["KH"], geo["KW"], geo["OH"], geo["OW"], geo["N"]
+        K, P = icg * KH * KW, N * OH * OW
+        x, w, y = node.inputs[0], node.inputs[1], node.outputs[0]
+        a = node.attrs
+        act = a.get("activation")
+        problem = {"kind": "conv", "mode": "implicit", "M": ocg, "N": P, "K": K, "batch": N,
+                   "bias": has_bias, "act": act, "group": G,
+                   **{k: geo[k] for k in ("H", "W", "KH", "KW", "SH", "SW", "DH", "DW",
+                                          "PT", "PB", "PL", "PR", "OH", "OW")}, "C": icg}
+        sched = self._schedule(node, (ocg, P, K), problem)
+        if sched.SK > 1 or sched.ST:
+            sched = MfmaSchedule(sched.BM, sched.BN, sched.BK, sched.WGM, sched.WGN, sched.MS, sched.DB)
+        if not sched.conv_valid():
+            raise ValueError(f"schedule {sched.key_full()} does not fit the convolution gather")
+        tap_major = icg % sched.BK == 0
+        warr = np.asarray(g.initializers[w], np.float32)          # [OC][icg][KH][KW]
+        if tap_major:
+            wdev, lda = self._pack(f"{w}__dev_tap", warr.transpose(0, 2, 3, 1).reshape(OC, K)), K
+        else:
+            wdev, lda = self._pack_rows(g, w, OC, K)
+        bias = [node.inputs[2]] if has_bias else []
+        res = self._residual_epilogue(g, node)
+        extra = [res["res_input"]] if res["res_input"] else []
+        win = (KH, KW, geo["SH"], geo["SW"], geo["DH"], geo["DW"], geo["PT"], geo["PL"])
+        bmode = 3 if tap_major else 2
+        sig = ("gconv", sched, has_bias, self._act_sig(a), bmode, lda % 4 == 0, win, res["residual"])
+        rtag = "_res" if extra else ""
+        kname = self._kernel(sig, lambda i: T.gemm_kernel(
+            f"gconv_{sched.key()}_{act or 'none'}{rtag}_{i}", sched, with_bias=has_bias,
+            bias_mode="row", activation=act, attrs=self._act_attrs(a), bmode=bmode,
+            out_nchw=True, vec_a=lda % 4 == 0, win=win, residual=res["residual"], grouped=True))
+        tiles = -(-ocg // sched.BM) * -(-P // sched.BN)
+        self.plan.append(Launch(
+            "gconv", kname, [wdev, x] + bias + extra, [y], (tiles, G, 1),
+            (sched.threads_per_block(), 1, 1),
+            {"M": ocg, "N": P, "K": K, "lda": lda, "Cin": icg, "H": geo["H"], "W": geo["W"],
+             "OH": OH, "OW": OW, "ksplit": 1, "kchunk": K, "ximg": C * geo["H"] * geo["W"],
+             "cimg": OC * OH * OW, "group": G, "with_bias": has_bias, "node": node,
+             "sched": sched, "k_order": "tap" if tap_major else "channel",
+             "flops": 2 * OC * P * K,
+             "bytes": 4 * (N * C * geo["H"] * geo["W"] + OC * K + P * OC * (1 + len(extra))
+                           + (OC if has_bias else 0))}))
 
     def _lower_conv_smallc(self, g: Graph, node: Node, geo: dict, has_bias: bool) -> None:
         """A conv with few input channels (a network's stem): the direct
@@ -396,9 +459,6 @@ class HipCodegen(Int8LoweringMixin):
              "bytes": 4 * rest * sched.BM * sched.BN * (2 + len(extra))}))
 
     def _lower_dwconv(self, g: Graph, node: Node, geo: dict, has_bias: bool) -> None:
-        if geo["ICG"] != 1 or geo["OC"] % geo["C"] != 0:
-            raise NotImplementedError(
-                f"HIP codegen: grouped conv with group={geo['group']} (only depthwise) unsupported")
         a = node.attrs
         act = a.get("activation")
         win = (geo["KH"], geo["KW"], geo["SH"], geo["SW"], geo["DH"], geo["DW"])
@@ -519,26 +579,36 @@ class HipCodegen(Int8LoweringMixin):
             (256, 1, 1), {"N": out_n, "node": origin or node, "scalar_consts": consts,
                           "bytes": 4 * out_n * (nin + len(node.outputs))}))
 
-    def _lower_maxpool(self, g: Graph, node: Node) -> None:
+    def _lower_pool(self, g: Graph, node: Node) -> None:
+        """MaxPool (-inf padding, ops.py:109-125) or AveragePool (zero
+        padding, divisor KH*KW with count_include_pad, else the taps inside
+        the input, ops.py:128-146) on the sliding-window kernel."""
         from mdlc_amd.passes.shape_inference import resolve_pads
 
         xs = self._shape(g, node.inputs[0])
         ys = self._shape(g, node.outputs[0])
         a = node.attrs
+        avg = node.op_type == "AveragePool"
         kh, kw = a["kernel_shape"]
         sh, sw = a.get("strides", [1, 1])
-        dh, dw = a.get("dilations", [1, 1])
+        dh, dw = (1, 1) if avg else a.get("dilations", [1, 1])
         (pt, _), (pl, _) = resolve_pads(a.get("auto_pad", "NOTSET"), a.get("pads"), xs[2:],
                                         (kh, kw), (sh, sw), (dh, dw))
         win = (kh, kw, sh, sw, dh, dw)
-        kname = self._kernel(("maxpool", win), lambda i: T.maxpool_kernel(
-            f"maxpool_{'x'.join(str(v) for v in win)}_{i}", win))
+        tag = "x".join(str(v) for v in win)
+        if avg:
+            cip = bool(a.get("count_include_pad", 0))
+            kname = self._kernel(("avgpool", win, cip), lambda i: T.avgpool_kernel(
+                f"avgpool_{tag}_{'cip' if cip else 'valid'}_{i}", win, cip))
+        else:
+            kname = self._kernel(("maxpool", win), lambda i: T.maxpool_kernel(f"maxpool_{tag}_{i}", win))
         total = int(np.prod(ys))
         threads = xs[0] * xs[1] * -(-ys[2] // T.WINDOW_VH) * ys[3]
         if max(threads, xs[2] * xs[3]) >= 2 ** 31:
-            raise NotImplementedError("HIP codegen: max pool too large for 32-bit indices")
+            raise NotImplementedError("HIP codegen: pooling too large for 32-bit indices")
         self.plan.append(Launch(
-            "maxpool", kname, [node.inputs[0]], [node.outputs[0]], (-(-threads // 256), 1, 1),
+            "avgpool" if avg else "maxpool", kname, [node.inputs[0]], [node.outputs[0]],
+            (-(-threads // 256), 1, 1),
             (256, 1, 1), {"planes": xs[0] * xs[1], "H": xs[2], "W": xs[3], "OH": ys[2],
                           "OW": ys[3], "KH": kh, "KW": kw, "SH": sh, "SW": sw, "PT": pt, "PL": pl,
                           "DH": dh, "DW": dw, "node": node,
@@ -568,6 +638,103 @@ class HipCodegen(Int8LoweringMixin):
         self.plan.append(Launch(
             "copy", "copy_bytes", [src], [node.outputs[0]], (max(1, -(-threads // 256)), 1, 1),
             (256, 1, 1), {"nbytes": nbytes, "node": node, "bytes": 2 * nbytes}))
+
+    # -- ops the reference ran on the host (emit.py:32-35) ------------------
+
+    def _float_operand(self, g: Graph, node: Node, e: str) -> tuple:
+        if self.layout.get(e) == "NHWC" or g.info(e).dtype != DType.FLOAT32:
+            raise NotImplementedError(
+                f"HIP codegen: {node.op_type} on {e!r} needs a float32 NCHW tensor")
+        return self._shape(g, e)
+
+    def _lower_softmax(self, g: Graph, node: Node) -> None:
+        """Softmax over ``axis`` (default -1, as the reference executor
+        reads it, reference.py:172-173): the tensor as [outer][L][inner]."""
+        xs = self._float_operand(g, node, node.inputs[0])
+        ax = int(node.attrs.get("axis", -1))
+        ax = ax + len(xs) if ax < 0 else ax
+        outer = int(np.prod(xs[:ax])) if ax else 1
+        L, inner = xs[ax], int(np.prod(xs[ax + 1:])) if ax + 1 < len(xs) else 1
+        rows = inner == 1
+        kname = self._kernel(("softmax", rows), lambda i: T.softmax_kernel(
+            "softmax_rows_f32" if rows else "softmax_cols_f32", rows))
+        grid = (-(-outer // 4),) if rows else (-(-(outer * inner) // 256),)
+        total = outer * L * inner
+        self.plan.append(Launch(
+            "softmax", kname, [node.inputs[0]], [node.outputs[0]], grid + (1, 1), (256, 1, 1),
+            {"outer": outer, "L": L, "inner": inner, "rows": rows, "node": node,
+             "bytes": 8 * total}))
+
+    def _lower_transpose(self, g: Graph, node: Node) -> None:
+        xs = self._float_operand(g, node, node.inputs[0])
+        perm = node.attrs.get("perm") or list(range(len(xs)))[::-1]
+        if len(xs) > 6:
+            raise NotImplementedError("HIP codegen: Transpose of more than six dimensions")
+        strides = [int(np.prod(xs[d + 1:])) for d in range(len(xs))]
+        od = [xs[p] for p in perm]
+        total = int(np.prod(xs))
+        self._kernel("transpose", lambda i: T.transpose_kernel("transpose_f32"))
+        self.plan.append(Launch(
+            "transpose", "transpose_f32", [node.inputs[0]], [node.outputs[0]],
+            (max(1, -(-total // 256)), 1, 1), (256, 1, 1),
+            {"total": total, "out_dims": od, "src_strides": [strides[p] for p in perm],
+             "node": node, "bytes": 8 * total}))
+
+    def _lower_pad(self, g: Graph, node: Node) -> None:
+        """Pad with ``pads`` / ``value`` from inputs 1 / 2 or the attributes
+        (reference.py Pad dispatch, ops.py:249-255)."""
+        xs = self._float_operand(g, node, node.inputs[0])
+        ins, a = node.inputs, node.attrs
+        def operand(i, attr, default):
+            if len(ins) > i and ins[i]:
+                if not g.is_constant(ins[i]):
+                    raise NotImplementedError(f"HIP codegen: Pad {attr} must be constant")
+                return g.initializers[ins[i]]
+            return a.get(attr, default)
+        pads = [int(v) for v in np.asarray(operand(1, "pads", None)).ravel()]
+        value = float(np.asarray(operand(2, "value", 0.0), np.float32).reshape(()))
+        mode = a.get("mode", "constant")
+        if isinstance(mode, bytes):
+            mode = mode.decode()
+        if mode not in T.PAD_MODES:
+            raise NotImplementedError(f"HIP codegen: Pad mode {mode!r}")
+        half = len(pads) // 2
+        before, after = pads[:half], pads[half:]
+        if len(xs) > 6 or half != len(xs) or min(pads) < 0:
+            raise NotImplementedError(f"HIP codegen: Pad {pads} of a {len(xs)}-d tensor")
+        if mode == "reflect" and any(p >= n for p, n in zip(before + after, xs + xs)):
+            raise NotImplementedError("HIP codegen: reflect Pad wider than its axis")
+        if mode == "edge" and any(n == 0 for n in xs):
+            raise NotImplementedError("HIP codegen: edge Pad of an empty axis")
+        od = [n + b + e for n, b, e in zip(xs, before, after)]
+        total = int(np.prod(od))
+        kname = self._kernel(("pad", mode), lambda i: T.pad_kernel(f"pad_{mode}_f32", mode))
+        self.plan.append(Launch(
+            "pad", kname, [ins[0]], [node.outputs[0]], (max(1, -(-total // 256)), 1, 1),
+            (256, 1, 1),
+            {"total": total, "out_dims": od, "in_dims": list(xs), "before": before,
+             "value": value, "node": node, "bytes": 4 * (int(np.prod(xs)) + total)}))
+
+    def _lower_concat(self, g: Graph, node: Node) -> None:
+        """One launch per operand, each writing its slab of the output."""
+        parts = [e for e in node.inputs if e]
+        shapes = [self._float_operand(g, node, e) for e in parts]
+        ax = int(node.attrs.get("axis", 0))
+        ax = ax + len(shapes[0]) if ax < 0 else ax
+        outer = int(np.prod(shapes[0][:ax])) if ax else 1
+        inner = int(np.prod(shapes[0][ax + 1:])) if ax + 1 < len(shapes[0]) else 1
+        total_ax = sum(s[ax] for s in shapes)
+        self._kernel("concat", lambda i: T.concat_kernel("concat_part_f32"))
+        off = 0
+        for e, s in zip(parts, shapes):
+            run = s[ax] * inner
+            n = outer * run
+            self.plan.append(Launch(
+                "concat", "concat_part_f32", [e], [node.outputs[0]],
+                (max(1, -(-n // 256)), 1, 1), (256, 1, 1),
+                {"rows": outer, "run": run, "dst_stride": total_ax * inner, "dst_off": off * inner,
+                 "node": node, "bytes": 8 * n}))
+            off += s[ax]
 
 
 def emit_hip_module(graph: Graph, schedule_fn: Optional[ScheduleFn] = None, *,

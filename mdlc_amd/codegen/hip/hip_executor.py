@@ -119,6 +119,10 @@ class HipExecutor:
             args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
             args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["Cin"]), I(m["H"]),
                      I(m["W"]), I(m["OH"]), I(m["OW"]), I(m["ksplit"]), I(m["kchunk"])]
+        elif k == "gconv":
+            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+            args += [I(m[f]) for f in ("M", "N", "K", "lda", "Cin", "H", "W", "OH", "OW", "ksplit",
+                                       "kchunk", "ximg", "cimg")]
         elif k == "conv_smallc":
             args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
             args += [I(m[f]) for f in ("batch", "H", "W", "OC", "OH", "OW")]
@@ -137,12 +141,25 @@ class HipExecutor:
             args += [I(m[f]) for f in ("N", "C", "H", "W", "OC", "OH", "OW", "PT", "PL")]
         elif k == "elementwise":
             args = [P(e) for e in l.inputs] + [P(o) for o in l.outputs] + [I(m["N"])]
-        elif k == "maxpool":
+        elif k in ("maxpool", "avgpool"):
             args = [P(l.inputs[0]), P(l.outputs[0])]
             args += [I(m[f]) for f in ("planes", "H", "W", "OH", "OW", "KH", "KW", "SH", "SW",
                                        "PT", "PL", "DH", "DW")]
         elif k == "gap":
             args = [P(l.inputs[0]), P(l.outputs[0]), I(m["planes"]), I(m["HW"])]
+        elif k == "softmax":
+            args = [P(l.inputs[0]), P(l.outputs[0])]
+            args += ([Arg.i64(m["outer"]), I(m["L"])] if m["rows"] else
+                     [Arg.i64(m["outer"]), I(m["L"]), I(m["inner"])])
+        elif k == "transpose":
+            args = [P(l.inputs[0]), P(l.outputs[0]), Arg.i64(m["total"]), Arg.dims6(m["out_dims"]),
+                    Arg.dims6(m["src_strides"])]
+        elif k == "pad":
+            args = [P(l.inputs[0]), P(l.outputs[0]), Arg.i64(m["total"]), Arg.dims6(m["out_dims"]),
+                    Arg.dims6(m["in_dims"]), Arg.dims6(m["before"], fill=0), Arg.f32(m["value"])]
+        elif k == "concat":
+            args = [P(l.inputs[0]), P(l.outputs[0])] + [Arg.i64(m[f]) for f in
+                                                         ("rows", "run", "dst_stride", "dst_off")]
         elif k == "copy":
             args = [P(l.inputs[0]), P(l.outputs[0]), Arg.i64(m["nbytes"])]
         elif k == "quantize":

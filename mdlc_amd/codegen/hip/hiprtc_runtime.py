@@ -311,6 +311,15 @@ class Arg:
     def f32(v: float) -> "Arg":
         return Arg(struct.pack("<f", float(v)))
 
+    @staticmethod
+    def dims6(vals, fill: int = 1) -> "Arg":
+        """``mdlc::Dims6``: up to six ints, left-padded with ``fill`` to six
+        (1 for extents, 0 for offsets)."""
+        vals = [int(v) for v in vals]
+        if len(vals) > 6:
+            raise HipError(f"more than six dimensions: {vals}")
+        return Arg(struct.pack("<6i", *([fill] * (6 - len(vals)) + vals)))
+
 
 def pack_plan(launches: list) -> bytes:
     """Serialise [(function_handle, grid, block, lds_bytes, [Arg])] in the

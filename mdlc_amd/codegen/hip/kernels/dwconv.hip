@@ -1,6 +1,7 @@
 // Per-plane sliding-window kernels over NCHW float32: depthwise convolution
-// (group == C, channel multiplier OC/C, fused bias/activation epilogue) and
-// max pooling share one template. Taps are combined in (kh, kw) order.
+// (group == C, channel multiplier OC/C, fused bias/activation epilogue), max
+// pooling and average pooling share one template. Taps are combined in
+// (kh, kw) order.
 // Indices within a plane are 32-bit (the host checks the sizes).
 namespace mdlc {
 
@@ -8,6 +9,7 @@ namespace mdlc {
 template <class Epi>
 struct DwOp {
   static constexpr bool weights = true;
+  static constexpr int average = 0;
   __device__ __forceinline__ static float pad() { return 0.f; }
   __device__ __forceinline__ static float init() { return 0.f; }
   __device__ __forceinline__ static float step(float acc, float x, float w) { return acc + w * x; }
@@ -17,10 +19,24 @@ struct DwOp {
 // Max pool: out-of-range taps are -inf (the NumPy padding value).
 struct MaxOp {
   static constexpr bool weights = false;
+  static constexpr int average = 0;
   __device__ __forceinline__ static float pad() { return -__builtin_inff(); }
   __device__ __forceinline__ static float init() { return -__builtin_inff(); }
   __device__ __forceinline__ static float step(float acc, float x, float) { return fmaxf(acc, x); }
   __device__ __forceinline__ static float finish(float acc, float) { return acc; }
+};
+
+// Average pool: padding taps add zero; finish() divides the window sum by
+// the divisor the template passes: KH*KW (average == 2, count_include_pad)
+// or the number of taps inside the input (average == 1).
+template <bool INCLUDE_PAD>
+struct AvgOp {
+  static constexpr bool weights = false;
+  static constexpr int average = INCLUDE_PAD ? 2 : 1;
+  __device__ __forceinline__ static float pad() { return 0.f; }
+  __device__ __forceinline__ static float init() { return 0.f; }
+  __device__ __forceinline__ static float step(float acc, float x, float) { return acc + x; }
+  __device__ __forceinline__ static float finish(float acc, float den) { return acc / den; }
 };
 
 // Column-strip form: each thread owns VH vertically adjacent outputs of one
@@ -63,6 +79,11 @@ __device__ __forceinline__ void window_column_f32(const float* __restrict__ x,
 #pragma unroll
   for (int k = 0; k < KH * KW; ++k) wr[k] = Op::weights ? w[oc * KH * KW + k] : 0.f;
   const float b = bias ? bias[oc] : 0.f;
+  int cols_in = 0;                                  // taps of this column inside the input
+  if (Op::average == 1) {
+#pragma unroll
+    for (int kw = 0; kw < KW; ++kw) cols_in += (unsigned)(iw0 + kw * DW) < (unsigned)W;
+  }
   float* yp = y + (size_t)plane * OH * OW + ow;
 #pragma unroll
   for (int j = 0; j < VH; ++j) {
@@ -72,7 +93,16 @@ __device__ __forceinline__ void window_column_f32(const float* __restrict__ x,
     for (int kh = 0; kh < KH; ++kh)
 #pragma unroll
       for (int kw = 0; kw < KW; ++kw) acc = Op::step(acc, v[j * SH + kh * DH][kw], wr[kh * KW + kw]);
-    yp[(oh0 + j) * OW] = Op::finish(acc, b);
+    float arg = b;
+    if (Op::average == 2) {
+      arg = (float)(KH * KW);
+    } else if (Op::average == 1) {
+      int rows_in = 0;
+#pragma unroll
+      for (int kh = 0; kh < KH; ++kh) rows_in += (unsigned)(ih0 + j * SH + kh * DH) < (unsigned)H;
+      arg = (float)max(rows_in * cols_in, 1);
+    }
+    yp[(oh0 + j) * OW] = Op::finish(acc, arg);
   }
 }
 

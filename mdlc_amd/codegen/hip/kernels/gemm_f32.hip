@@ -72,6 +72,10 @@ struct GemmArgs {
   int ksplit, kchunk;            // K slices (grid = tiles * ksplit) and slice depth; with
                                  // stream-K, ksplit = the tiles done whole (see gemm_f32_mfma)
   float* __restrict__ ws;        // stream-K partial-tile workspace [2 * SKW][BM * BN]
+  int ximg;                      // floats per input image (conv gathers): Cin*H*W, or the
+                                 // whole image's C*H*W for one group of a grouped conv
+  int cimg;                      // floats per output image (OUT == 1): M*hw, or OC*hw for
+                                 // one group of a grouped conv
 };
 
 __device__ __forceinline__ float pick(const float4& v, int q) {
@@ -171,7 +175,7 @@ __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0,
       const int s = p - n * ohw;
       const int oh = s / g.OW;
       const int ow = s - oh * g.OW;
-      g_base = n * g.Cin * g.H * g.W;
+      g_base = n * g.ximg;
       g_ih = oh * Win::SH - Win::PT;
       g_iw = ow * Win::SW - Win::PL;
     }
@@ -365,7 +369,7 @@ __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0,
       rstride = g.N;
     } else if (OUT == 1) {
       const int n = col / g.hw;
-      cofs[ni] = (size_t)n * g.M * g.hw + (col - n * g.hw);
+      cofs[ni] = (size_t)n * g.cimg + (col - n * g.hw);
       rstride = g.hw;
     } else {
       cofs[ni] = col;

@@ -123,7 +123,8 @@ def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: s
                 activation: Optional[str] = None, attrs: Optional[dict] = None,
                 alpha: float = 1.0, beta: float = 1.0, bmode: int = 0, out_nchw: bool = False,
                 vec_a: bool = True, win: Optional[tuple] = None,
-                residual: Optional[str] = None, stream_k: int = 0) -> tuple:
+                residual: Optional[str] = None, stream_k: int = 0,
+                grouped: bool = False) -> tuple:
     """(name, source) of one GEMM instantiation.
 
     Kernel ABI (the reference's gemm ABI plus trailing layout arguments):
@@ -139,7 +140,10 @@ def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: s
     ``splitk_reduce_kernel``. With ``stream_k`` = SKW > 0 a workspace pointer
     ``ws`` precedes the output, ``ksplit`` is the number of tiles done whole
     and the last SKW workgroups compute the remaining tiles in pieces
-    (``streamk_fixup_kernel`` finishes them).
+    (``streamk_fixup_kernel`` finishes them). ``grouped`` (conv only): one
+    launch runs every group of a grouped convolution, blockIdx.y selecting
+    the group's weights, input channels, bias, residual and output channels;
+    two trailing arguments give the whole input and output image strides.
     """
     attrs = attrs or {}
     s = sched
@@ -161,15 +165,27 @@ def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: s
             f"{out}, {epi}, {winty}, {int(stream_k)}>")
     nt = s.threads_per_block()
     ws_arg = "float* __restrict__ ws, " if stream_k else ""
-    ws_val = ", ws" if stream_k else ""
+    ws_val = "ws" if stream_k else "nullptr"
+    if grouped and (split or stream_k or bmode < 2):
+        raise ValueError("a grouped convolution runs the implicit gather without split-K or stream-K")
     if bmode >= 2:
+        # grouped: blockIdx.y is the group; M, Cin and the weights are one
+        # group's, ximg / cimg the whole images' strides
+        shift = ""
+        if grouped:
+            shift = ("  const size_t grp = blockIdx.y;\n"
+                     "  A += grp * M * lda; x += grp * Cin * H * W; y += grp * M * OH * OW;\n"
+                     + ("  bias += grp * M;\n" if with_bias else "")
+                     + ("  res += grp * M * OH * OW;\n" if residual else ""))
+        strides = ", int ximg, int cimg" if grouped else ""
+        img = "ximg, cimg" if grouped else "Cin * H * W, M * OH * OW"
         src.append(
             f'extern "C" __global__ __launch_bounds__({nt}) void {name}(\n'
             f"    const float* __restrict__ A, const float* __restrict__ x, {bias_arg}{ws_arg}"
             f"float* __restrict__ y,\n    int M, int N, int K, int lda, int Cin, int H, int W, "
-            f"int OH, int OW, int ksplit, int kchunk) {{\n"
+            f"int OH, int OW, int ksplit, int kchunk{strides}) {{\n{shift}"
             f"  mdlc::GemmArgs g{{A, x, {bias_val}, y, M, N, K, lda, 0, 0, OH * OW, Cin, H, W, OH, OW, "
-            f"ksplit, kchunk{ws_val}}};\n"
+            f"ksplit, kchunk, {ws_val}, {img}}};\n"
             f"  {tmpl}(g);\n}}\n")
     else:
         src.append(
@@ -178,7 +194,7 @@ def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: s
             f"float* __restrict__ C,\n    int M, int N, int K, int lda, int ldb, int ldc, int hw, "
             f"int ksplit, int kchunk) {{\n"
             f"  mdlc::GemmArgs g{{A, B, {bias_val}, C, M, N, K, lda, ldb, ldc, hw, 0, 0, 0, 0, 0, "
-            f"ksplit, kchunk{ws_val}}};\n"
+            f"ksplit, kchunk, {ws_val}, 0, M * hw}};\n"
             f"  {tmpl}(g);\n}}\n")
     return name, "\n".join(src)
 
@@ -271,6 +287,66 @@ def maxpool_kernel(name: str, win: tuple, vh: int = WINDOW_VH) -> tuple:
         "    int OH, int OW, int KH, int KW, int SH, int SW, int PT, int PL, int DH, int DW) {\n"
         f"  mdlc::window_column_f32<{', '.join(str(v) for v in win)}, {vh}, mdlc::MaxOp>("
         "x, nullptr, nullptr, y, planes, 1, H, W, 1, OH, OW, PT, PL);\n}\n")
+
+
+def avgpool_kernel(name: str, win: tuple, include_pad: bool, vh: int = WINDOW_VH) -> tuple:
+    """Average pool for ``win`` = (KH, KW, SH, SW, 1, 1): the window sum in
+    float32, (kh, kw) order, divided by KH*KW (``include_pad``) or by the
+    number of taps inside the input. Same ABI and grid as ``maxpool_kernel``."""
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const float* __restrict__ x, float* __restrict__ y, int planes, int H, int W,\n"
+        "    int OH, int OW, int KH, int KW, int SH, int SW, int PT, int PL, int DH, int DW) {\n"
+        f"  mdlc::window_column_f32<{', '.join(str(v) for v in win)}, {vh}, "
+        f"mdlc::AvgOp<{'true' if include_pad else 'false'}>>("
+        "x, nullptr, nullptr, y, planes, 1, H, W, 1, OH, OW, PT, PL);\n}\n")
+
+
+def softmax_kernel(name: str, rows: bool) -> tuple:
+    """Softmax over one axis. ``rows`` (the axis is innermost): ABI (x, y,
+    long long rows, int L), one 64-lane wave per row, four rows per 256-thread
+    workgroup; otherwise ABI (x, y, long long outer, int L, int inner), one
+    thread per (outer, inner) column."""
+    if rows:
+        return name, (
+            f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+            "    const float* __restrict__ x, float* __restrict__ y, long long rows, int L) {\n"
+            "  mdlc::softmax_rows_f32(x, y, rows, L);\n}\n")
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const float* __restrict__ x, float* __restrict__ y, long long outer, int L, int inner) {\n"
+        "  mdlc::softmax_cols_f32(x, y, outer, L, inner);\n}\n")
+
+
+def transpose_kernel(name: str = "transpose_f32") -> tuple:
+    """ABI (x, y, long long total, Dims6 out_dims, Dims6 src_strides)."""
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const float* __restrict__ x, float* __restrict__ y, long long total, mdlc::Dims6 od,\n"
+        "    mdlc::Dims6 ss) {\n  mdlc::transpose_f32(x, y, total, od, ss);\n}\n")
+
+
+PAD_MODES = {"constant": 0, "edge": 1, "reflect": 2}
+
+
+def pad_kernel(name: str, mode: str) -> tuple:
+    """ABI (x, y, long long total, Dims6 out_dims, Dims6 in_dims, Dims6
+    pads_before, float value)."""
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const float* __restrict__ x, float* __restrict__ y, long long total, mdlc::Dims6 od,\n"
+        "    mdlc::Dims6 id, mdlc::Dims6 before, float value) {\n"
+        f"  mdlc::pad_f32<{PAD_MODES[mode]}>(x, y, total, od, id, before, value);\n}}\n")
+
+
+def concat_kernel(name: str = "concat_part_f32") -> tuple:
+    """One Concat operand. ABI (x, y, long long rows, long long run, long
+    long dst_stride, long long dst_off)."""
+    return name, (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        "    const float* __restrict__ x, float* __restrict__ y, long long rows, long long run,\n"
+        "    long long dst_stride, long long dst_off) {\n"
+        "  mdlc::concat_part_f32(x, y, rows, run, dst_stride, dst_off);\n}\n")
 
 
 def gap_kernel(name: str = "global_avg_pool") -> tuple:

@@ -24,7 +24,7 @@ the member is an ``Add`` of ``y`` and one other tensor ``r`` of the same
 shape, both from outside the group, ``r`` not depending on ``y``; the
 pointwise members folded after it each read only the previous one's output,
 which nothing else reads; ``y`` has no other consumer and is not a graph
-output; and the conv is not grouped.
+output; and the conv is not depthwise (one input channel per group).
 """
 
 from __future__ import annotations
@@ -50,6 +50,16 @@ def _external_inputs(sub: list) -> list:
 class FuseResidualEpilogue(Pass):
     name = "fuse_residual_epilogue"
 
+    @staticmethod
+    def _depthwise(graph: Graph, conv: Node) -> bool:
+        """A grouped conv with one input channel per group runs on the
+        depthwise window kernel, which has no residual epilogue; other
+        grouped convs run the implicit GEMM, which has."""
+        if int(conv.attrs.get("group", 1)) == 1:
+            return False
+        w = graph.info(conv.inputs[1])
+        return w is None or len(w.shape) < 2 or int(w.shape[1]) == 1
+
     def _peel(self, graph: Graph, grp: Node):
         """(conv, chain, y, r) for the first member of ``grp`` that is
         ``Add(y, r)`` of a foldable conv output, extended by the pointwise
@@ -71,7 +81,7 @@ class FuseResidualEpilogue(Pass):
                 conv = prod.get(y)
                 if conv is None or conv.op_type not in CONVS or y in internal or r in internal:
                     continue
-                if int(conv.attrs.get("group", 1)) != 1 or conv.attrs.get("residual_subgraph"):
+                if conv.attrs.get("residual_subgraph") or self._depthwise(graph, conv):
                     continue
                 if y in graph.outputs or uses.get(y, 0) != 1:
                     continue

@@ -124,9 +124,9 @@ def test_activation_expressions_follow_numpy_semantics():
 def test_unsupported_op_raises_instead_of_host_fallback():
     from mdlc_amd.tools.graph_builder import GraphBuilder
 
-    b = GraphBuilder("sm")
+    b = GraphBuilder("shape")
     b.input("x", (2, 8))
-    b.node("Softmax", ["x"], "y", axis=1)
+    b.node("Shape", ["x"], "y")
     b.output("y")
     with pytest.raises(NotImplementedError, match="no device lowering"):
         compile_graph(b.graph())
