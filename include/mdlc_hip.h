@@ -83,10 +83,16 @@ int mdlc_event_elapsed_ms(void* start, void* stop, float* ms);
 /* Packed launch plans: the executor's launch loop in C++.
  * Replaces: the Python `issue()` loop of GpuExecutor.run, gpu_executor.py:63-91.
  *
- * Layout (little endian): "MDLP", u32 version (=1), u32 n_launches, u32 0;
+ * Layout (little endian): "MDLP", u32 version (1 or 2), u32 n_launches,
+ * u32 0; version 2 adds u64 ws_base, u64 ws_bytes (the workspace the plan's
+ * kernels use: split-K partial sums, stream-K pieces, column matrices);
  * then per launch: u64 function, u32 grid[3], u32 block[3], u32 lds_bytes,
  * u32 n_args, then per argument u32 nbytes followed by the value bytes,
- * zero-padded to a multiple of 8.
+ * zero-padded to a multiple of 8. In version 2 an nbytes with its top bit
+ * set (0x80000000 | 8) marks a workspace pointer whose value is an offset
+ * below ws_bytes; the plan passes ws_base + offset. A version-2 plan with
+ * ws_base 0 has no workspace of its own and runs only through
+ * mdlc_plan_run_static (the other entries refuse it).
  *
  * mdlc_plan_run enqueues every launch `iters` times without waiting.
  * mdlc_plan_time_ms brackets `iters` runs (after `warmup` runs) with events.
@@ -101,6 +107,22 @@ int mdlc_plan_run(void* plan, int iters);
 int mdlc_plan_time_ms(void* plan, int warmup, int iters, float* ms);
 int mdlc_plan_profile(void* plan, int iters, float* per_launch_ms);
 int mdlc_plan_use_graph(void* plan, int enable);
+
+/* mdlc_plan_run without a caller workspace: the plan's workspace pointers
+ * are rebased on the library's static scratch, a file-scope device array of
+ * 64 MiB per GPU that mdlc_init resolves once per device and that is held
+ * until the process ends. Allocates nothing (no hipMalloc, hipFree or
+ * allocating library call), so callers that cannot allocate device memory
+ * (code being captured into a HIP graph, tight serving loops, harnesses that
+ * forbid it) can run a plan. A plan whose ws_bytes exceeds 64 MiB is refused
+ * with an error. Every call on one GPU shares that GPU's array and leaves
+ * its contents behind; the kernels write every workspace element they read
+ * in the same call, so nothing needs clearing. Calls that overlap on one GPU
+ * (another thread or process running a plan on it at the same time) race.
+ * No counterpart in the reference: its executor allocated every buffer per
+ * run (gpu_executor.py:48-61); this entry is for the callers that cannot
+ * allocate. */
+int mdlc_plan_run_static(void* plan, int iters);
 
 #ifdef __cplusplus
 }

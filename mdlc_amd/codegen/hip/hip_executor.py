@@ -26,15 +26,22 @@ from typing import Optional
 import numpy as np
 
 from mdlc_amd.codegen.hip.emit import HipModule, Launch
-from mdlc_amd.codegen.hip.hiprtc_runtime import Arg, HipContext, HipError, Plan, compile_code_object
+from mdlc_amd.codegen.hip.hiprtc_runtime import (STATIC_SCRATCH_BYTES, Arg, HipContext, HipError, Plan,
+                                                 compile_code_object)
 from mdlc_amd.ir import DType
 from mdlc_amd.runtime.memory_planner import align_up, plan_memory
 
 
 class HipExecutor:
     def __init__(self, module: HipModule, ctx: Optional[HipContext] = None, *,
-                 use_graph: bool = False, use_cache: bool = True) -> None:
+                 use_graph: bool = False, use_cache: bool = True,
+                 static_scratch: bool = False) -> None:
+        """``static_scratch``: the scratch regions (split-K / stream-K
+        workspace, column matrices) are not part of the arena; the plan runs
+        through ``mdlc_plan_run_static`` on the library's per-GPU static
+        scratch, so ``run`` allocates no device memory for them."""
         self.module = module
+        self.static_scratch = static_scratch
         self.ctx = ctx or HipContext()
         g = module.graph
         self.code = self.ctx.load_code(compile_code_object(module.sources(), arch=self.ctx.arch,
@@ -81,12 +88,26 @@ class HipExecutor:
             cls = module.scratch_class.get(name, "cols")
             regions[cls] = max(regions.get(cls, 0), r * ld * 4)
         region_at: dict = {}
+        ws = 0                                  # static mode: offsets within the workspace
         for cls in sorted(regions):
-            region_at[cls] = cur
-            cur += align_up(regions[cls])
+            if static_scratch:
+                region_at[cls] = ws
+                ws += align_up(regions[cls])
+            else:
+                region_at[cls] = cur
+                cur += align_up(regions[cls])
+        self.ws_offsets: dict = {}
         for name, (r, ld) in module.scratch_shapes.items():
-            self.offsets[name] = region_at[module.scratch_class.get(name, "cols")]
+            at = region_at[module.scratch_class.get(name, "cols")]
+            if static_scratch:
+                self.ws_offsets[name] = at
+            else:
+                self.offsets[name] = at
             self.shapes[name], self.dtypes[name] = (r, ld), np.dtype(np.float32)
+        self.ws_bytes = ws
+        if static_scratch and ws > STATIC_SCRATCH_BYTES:
+            raise HipError(f"the plan's workspace of {ws} bytes exceeds the static scratch of "
+                           f"{STATIC_SCRATCH_BYTES} bytes; run it with the arena's workspace")
         self.arena_bytes = cur
         self.arena = self.ctx.malloc(max(cur, 256))
         self.base = int(self.arena.value)
@@ -94,7 +115,7 @@ class HipExecutor:
             self.ctx.htod(self.base + self.offsets[name], arr)
 
         self.launch_records = [self._record(l) for l in module.plan]
-        self.plan = Plan(self.launch_records)
+        self.plan = self._make_plan(self.launch_records)
         if use_graph:
             self.plan.use_graph(True)
         self._single: Optional[list] = None
@@ -106,9 +127,17 @@ class HipExecutor:
             raise HipError(f"tensor {name!r} has no arena slot")
         return self.base + self.offsets[name]
 
+    def _make_plan(self, records: list) -> Plan:
+        return Plan(records, (0, max(self.ws_bytes, 1)) if self.static_scratch else None)
+
+    def _arg_ptr(self, e: str) -> Arg:
+        if e in self.ws_offsets:
+            return Arg.ws(self.ws_offsets[e])
+        return Arg.ptr(self.ptr(e))
+
     def _record(self, l: Launch) -> tuple:
         m = l.meta
-        P = lambda e: Arg.ptr(self.ptr(e))  # noqa: E731
+        P = self._arg_ptr
         I = Arg.i32  # noqa: E741
         k = l.kind
         if k == "gemm":
@@ -231,18 +260,25 @@ class HipExecutor:
             arr = np.ascontiguousarray(arr.transpose(0, 2, 3, 1))
         self.ctx.htod(self.ptr(name), arr)
 
+    def _run_plan(self, plan: Plan, iters: int = 1) -> None:
+        if self.static_scratch:
+            plan.run_static(iters)
+        else:
+            plan.run(iters)
+
     def run(self, feeds: dict, *, timing: bool = False, warmup: int = 3, iters: int = 10) -> dict:
         self._upload_feeds(feeds)
-        self.plan.run(1)
+        self._run_plan(self.plan)
         self.ctx.synchronize()
         out = {"outputs": {o: self.read(o) for o in self.module.graph.outputs}}
         if timing:
-            out["ms"] = self.plan.time_ms(warmup, iters)
+            out["ms"] = (self.ctx.time_ms(lambda: self.plan.run_static(1), iters, warmup)
+                         if self.static_scratch else self.plan.time_ms(warmup, iters))
         return out
 
     def _singles(self) -> list:
         if self._single is None:
-            self._single = [Plan([r]) for r in self.launch_records]
+            self._single = [self._make_plan([r]) for r in self.launch_records]
         return self._single
 
     def run_all(self, feeds: dict) -> dict:
@@ -251,7 +287,7 @@ class HipExecutor:
         self._upload_feeds(feeds)
         env = {}
         for l, p in zip(self.module.plan, self._singles()):
-            p.run(1)
+            self._run_plan(p)
             self.ctx.synchronize()
             for o in l.outputs:
                 if o not in self.module.scratch_shapes:
@@ -276,7 +312,7 @@ class HipExecutor:
                 if e in env and e not in consts:
                     self.write(e, env[e])
             for i in idxs:
-                singles[i].run(1)
+                self._run_plan(singles[i])
             self.ctx.synchronize()
             for o in node.outputs:
                 if o:

@@ -74,7 +74,11 @@ _SIGS = {
     "mdlc_plan_profile": ([ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_float)],
                           ctypes.c_int),
     "mdlc_plan_use_graph": ([ctypes.c_void_p, ctypes.c_int], ctypes.c_int),
+    "mdlc_plan_run_static": ([ctypes.c_void_p, ctypes.c_int], ctypes.c_int),
 }
+
+# Size of the library's static scratch array per GPU (mdlc_plan_run_static).
+STATIC_SCRATCH_BYTES = 64 << 20
 
 
 def lib() -> ctypes.CDLL:
@@ -290,10 +294,16 @@ class HipContext:
 class Arg:
     """A kernel argument for a packed plan: a raw value of a fixed width."""
 
-    __slots__ = ("data",)
+    __slots__ = ("data", "workspace")
 
-    def __init__(self, data: bytes) -> None:
+    def __init__(self, data: bytes, workspace: bool = False) -> None:
         self.data = data
+        self.workspace = workspace
+
+    @staticmethod
+    def ws(offset: int) -> "Arg":
+        """A pointer ``offset`` bytes into the plan's workspace (plan format 2)."""
+        return Arg(struct.pack("<Q", int(offset)), workspace=True)
 
     @staticmethod
     def ptr(v: int) -> "Arg":
@@ -321,25 +331,33 @@ class Arg:
         return Arg(struct.pack("<6i", *([fill] * (6 - len(vals)) + vals)))
 
 
-def pack_plan(launches: list) -> bytes:
+def pack_plan(launches: list, workspace: Optional[tuple] = None) -> bytes:
     """Serialise [(function_handle, grid, block, lds_bytes, [Arg])] in the
-    layout mdlc_plan_create expects."""
-    out = [b"MDLP", struct.pack("<III", 1, len(launches), 0)]
+    layout mdlc_plan_create expects. ``workspace`` = (base, bytes) writes
+    format 2, where ``Arg.ws`` arguments are offsets into that workspace
+    (base 0: none of the caller's, the plan runs on the static scratch)."""
+    ver = 1 if workspace is None else 2
+    out = [b"MDLP", struct.pack("<III", ver, len(launches), 0)]
+    if workspace is not None:
+        out.append(struct.pack("<QQ", int(workspace[0]), int(workspace[1])))
     for fn, grid, block, lds, args in launches:
         g = (list(grid) + [1, 1])[:3]
         bl = (list(block) + [1, 1])[:3]
         out.append(struct.pack("<Q3I3III", int(fn), *g, *bl, int(lds), len(args)))
         for a in args:
             n = len(a.data)
-            out.append(struct.pack("<I", n) + a.data + b"\0" * ((-n) % 8))
+            if a.workspace and workspace is None:
+                raise HipError("a workspace argument needs a format-2 plan")
+            tag = (n | 0x80000000) if a.workspace else n
+            out.append(struct.pack("<I", tag) + a.data + b"\0" * ((-n) % 8))
     return b"".join(out)
 
 
 class Plan:
     """A launch plan living in the C++ runtime."""
 
-    def __init__(self, launches: list) -> None:
-        blob = pack_plan(launches)
+    def __init__(self, launches: list, workspace: Optional[tuple] = None) -> None:
+        blob = pack_plan(launches, workspace)
         self._blob = ctypes.create_string_buffer(blob, len(blob))
         self._h = ctypes.c_void_p()
         _ck(lib().mdlc_plan_create(self._blob, len(blob), ctypes.byref(self._h)),
@@ -348,6 +366,10 @@ class Plan:
 
     def run(self, iters: int = 1) -> None:
         _ck(lib().mdlc_plan_run(self._h, iters), "mdlc_plan_run")
+
+    def run_static(self, iters: int = 1) -> None:
+        """Run on the library's static scratch (allocates nothing)."""
+        _ck(lib().mdlc_plan_run_static(self._h, iters), "mdlc_plan_run_static")
 
     def time_ms(self, warmup: int = 3, iters: int = 10) -> float:
         ms = ctypes.c_float()

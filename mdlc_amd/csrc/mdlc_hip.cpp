@@ -13,11 +13,20 @@
 
 #include "mdlc_hip.h"
 
+// The allocation-free plan runner's workspace (mdlc_plan_run_static): a
+// file-scope device array, one copy per GPU, held until the process ends.
+// Host code never uses its name as an address: mdlc_init resolves each
+// device's copy with hipGetSymbolAddress and keeps the pointer per device.
+constexpr size_t kStaticScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
 namespace {
 
 std::string g_err;
 hipStream_t g_stream = nullptr;
 int g_device = -1;
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
 
 enum ShimCode : int { kBadArg = 9001, kBadPlan = 9002 };
 
@@ -46,6 +55,13 @@ struct Launch {
   unsigned lds;
   std::vector<uint64_t> blob;    // argument values, 8-byte slots
   std::vector<void*> argv;       // pointers into blob, one per argument
+  // workspace arguments (plan format 2): blob slot and offset into the
+  // workspace; the static runner's copy of the values, rebased on the
+  // device's static scratch at each call
+  std::vector<size_t> ws_slot;
+  std::vector<uint64_t> ws_off;
+  std::vector<uint64_t> sblob;
+  std::vector<void*> sargv;
 };
 
 struct Plan {
@@ -53,7 +69,18 @@ struct Plan {
   bool use_graph = false;
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph = nullptr;
+  uint64_t ws_base = 0;          // the caller's workspace (0: none bound)
+  uint64_t ws_bytes = 0;         // workspace the plan's kernels use
+  bool has_ws = false;           // some argument is a workspace pointer
 };
+
+// A plan whose workspace arguments have no caller workspace behind them can
+// only run on the static scratch.
+int need_workspace(const Plan* p, const char* what) {
+  if (p->has_ws && p->ws_base == 0)
+    return fail(kBadPlan, what, "the plan has no workspace bound; run it with mdlc_plan_run_static");
+  return 0;
+}
 
 int enqueue(Launch& l) {
   return check(hipModuleLaunchKernel(l.fn, l.grid[0], l.grid[1], l.grid[2], l.block[0],
@@ -63,10 +90,12 @@ int enqueue(Launch& l) {
 }
 
 int enqueue_plan(Plan* p) {
+  int rc = need_workspace(p, "mdlc_plan_run");
+  if (rc) return rc;
   if (p->use_graph && p->exec != nullptr)
     return check(hipGraphLaunch(p->exec, g_stream), "hipGraphLaunch");
   for (auto& l : p->launches) {
-    int rc = enqueue(l);
+    rc = enqueue(l);
     if (rc) return rc;
   }
   return 0;
@@ -111,6 +140,12 @@ int mdlc_init(int device, char* arch, int arch_len) {
     rc = check(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), "hipStreamCreate");
     if (rc) return rc;
     g_device = device;
+  }
+  if (device >= 0 && device < kMaxDevices && g_scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    rc = check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (rc) return rc;
+    g_scratch_ptr[device] = ptr;
   }
   if (arch && arch_len > 0) {
     hipDeviceProp_t prop;
@@ -267,9 +302,13 @@ int mdlc_plan_create(const void* packed, size_t nbytes, void** plan) {
   char magic[4];
   uint32_t version = 0, n = 0, reserved = 0;
   if (!take(cur, end, &magic) || std::memcmp(magic, "MDLP", 4) != 0 || !take(cur, end, &version) ||
-      version != 1 || !take(cur, end, &n) || !take(cur, end, &reserved))
+      (version != 1 && version != 2) || !take(cur, end, &n) || !take(cur, end, &reserved))
     return fail(kBadPlan, "mdlc_plan_create", "bad header");
   Plan* p = new Plan();
+  if (version == 2 && (!take(cur, end, &p->ws_base) || !take(cur, end, &p->ws_bytes))) {
+    delete p;
+    return fail(kBadPlan, "mdlc_plan_create", "bad header");
+  }
   p->launches.resize(n);
   for (uint32_t i = 0; i < n; ++i) {
     Launch& l = p->launches[i];
@@ -287,7 +326,14 @@ int mdlc_plan_create(const void* packed, size_t nbytes, void** plan) {
     std::vector<size_t> slot(nargs);
     for (uint32_t a = 0; a < nargs; ++a) {
       uint32_t sz = 0;
-      if (!take(cur, end, &sz) || sz == 0 || sz > 64) {
+      if (!take(cur, end, &sz)) {
+        delete p;
+        return fail(kBadPlan, "mdlc_plan_create", "bad argument size");
+      }
+      // format 2: the top bit marks a workspace pointer given as an offset
+      const bool ws = version == 2 && (sz & 0x80000000u);
+      sz &= 0x7fffffffu;
+      if (sz == 0 || sz > 64 || (ws && sz != 8)) {
         delete p;
         return fail(kBadPlan, "mdlc_plan_create", "bad argument size");
       }
@@ -300,9 +346,23 @@ int mdlc_plan_create(const void* packed, size_t nbytes, void** plan) {
       l.blob.resize(l.blob.size() + padded / 8, 0);
       std::memcpy(l.blob.data() + slot[a], cur, sz);
       cur += padded;
+      if (ws) {
+        const uint64_t off = l.blob[slot[a]];
+        if (off >= p->ws_bytes) {
+          delete p;
+          return fail(kBadPlan, "mdlc_plan_create", "workspace offset outside the workspace");
+        }
+        l.ws_slot.push_back(slot[a]);
+        l.ws_off.push_back(off);
+        l.blob[slot[a]] = p->ws_base ? p->ws_base + off : 0;
+        p->has_ws = true;
+      }
     }
     l.argv.resize(nargs);
     for (uint32_t a = 0; a < nargs; ++a) l.argv[a] = l.blob.data() + slot[a];
+    l.sblob = l.blob;
+    l.sargv.resize(nargs);
+    for (uint32_t a = 0; a < nargs; ++a) l.sargv[a] = l.sblob.data() + slot[a];
   }
   *plan = p;
   return 0;
@@ -334,6 +394,33 @@ int mdlc_plan_run(void* plan, int iters) {
   return 0;
 }
 
+int mdlc_plan_run_static(void* plan, int iters) {
+  int rc = need_stream("mdlc_plan_run_static");
+  if (rc) return rc;
+  Plan* p = static_cast<Plan*>(plan);
+  if (!p || iters < 0) return fail(kBadArg, "mdlc_plan_run_static", "bad arguments");
+  if (p->ws_bytes > kStaticScratchBytes) {
+    char buf[160];
+    std::snprintf(buf, sizeof(buf), "the plan's workspace of %llu bytes exceeds the static scratch of %llu bytes",
+                  static_cast<unsigned long long>(p->ws_bytes),
+                  static_cast<unsigned long long>(kStaticScratchBytes));
+    return fail(kBadArg, "mdlc_plan_run_static", buf);
+  }
+  void* base = (g_device >= 0 && g_device < kMaxDevices) ? g_scratch_ptr[g_device] : nullptr;
+  if (base == nullptr) return fail(kBadArg, "mdlc_plan_run_static", "no static scratch on this device");
+  for (int it = 0; it < iters; ++it) {
+    for (auto& l : p->launches) {
+      for (size_t j = 0; j < l.ws_slot.size(); ++j)
+        l.sblob[l.ws_slot[j]] = reinterpret_cast<uint64_t>(base) + l.ws_off[j];
+      rc = check(hipModuleLaunchKernel(l.fn, l.grid[0], l.grid[1], l.grid[2], l.block[0], l.block[1],
+                                       l.block[2], l.lds, g_stream, l.sargv.data(), nullptr),
+                 "hipModuleLaunchKernel");
+      if (rc) return rc;
+    }
+  }
+  return 0;
+}
+
 int mdlc_plan_time_ms(void* plan, int warmup, int iters, float* ms) {
   if (!ms || iters <= 0) return fail(kBadArg, "mdlc_plan_time_ms", "bad arguments");
   int rc = mdlc_plan_run(plan, warmup);
@@ -361,6 +448,7 @@ int mdlc_plan_profile(void* plan, int iters, float* per_launch_ms) {
   if (rc) return rc;
   Plan* p = static_cast<Plan*>(plan);
   if (!per_launch_ms || iters <= 0) return fail(kBadArg, "mdlc_plan_profile", "bad arguments");
+  if ((rc = need_workspace(p, "mdlc_plan_profile"))) return rc;
   size_t n = p->launches.size();
   std::vector<hipEvent_t> ev(2 * n, nullptr);
   for (auto& e : ev)
@@ -392,6 +480,7 @@ int mdlc_plan_use_graph(void* plan, int enable) {
     p->use_graph = false;
     return 0;
   }
+  if ((rc = need_workspace(p, "mdlc_plan_use_graph"))) return rc;
   if (p->exec == nullptr) {
     rc = check(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
     if (rc) return rc;
