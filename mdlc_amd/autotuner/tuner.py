@@ -25,6 +25,7 @@ from typing import Optional
 from mdlc_amd.codegen.schedule import (
     CUS, DEFAULT_GEMM, MfmaSchedule, default_qdw_schedule, default_qschedule, default_schedule,
     gemm_search_space, qdw_search_space, qdw_valid, qgemm_search_space, qsched_valid, split_slices,
+    wsplit_search_space,
 )
 
 LDS_PER_CU = 160 * 1024
@@ -32,7 +33,8 @@ MFMA_FLOPS_PER_CU_CLK = 256          # fp32 MFMA, dense
 CLOCK_GHZ = 2.4
 HBM_GBS = 8000.0
 LAUNCH_US = 2.0
-SPLITS = (1, 2, 3, 4, 5, 6, 8)
+L2_CU_GBS = 150.0                    # one CU's L2 -> L1 read rate (64 B/clk)
+SPLITS = (1, 2, 3, 4, 5, 6, 8, 12, 16, 24, 32)
 
 
 def analytical_cost(sched: MfmaSchedule, M: int, N: int, K: int) -> float:
@@ -47,7 +49,16 @@ def analytical_cost(sched: MfmaSchedule, M: int, N: int, K: int) -> float:
     * Memory: A re-read once per column tile and B once per row tile, at
       HBM bandwidth, overlapped with compute.
     * Split-K adds the workspace round trip and a second launch.
+    * The wave-split kernel (``WK`` > 1) is one launch whose tiles each
+      stream (BM + BN) x K operands through one CU: costed by that per-CU
+      traffic at the L2-to-CU rate, against its MFMA time.
     """
+    if sched.WK > 1:
+        tiles = -(-M // sched.BM) * -(-N // sched.BN)
+        per_cu = -(-tiles // CUS)
+        load = per_cu * (sched.BM + sched.BN) * K * 4.0 / (L2_CU_GBS * 1e3)
+        mfma = per_cu * 2.0 * sched.BM * sched.BN * K / (MFMA_FLOPS_PER_CU_CLK * CLOCK_GHZ * 1e3) / 0.5
+        return max(load, mfma) + LAUNCH_US
     slices, chunk = split_slices(K, sched)
     tiles = -(-M // sched.BM) * -(-N // sched.BN)
     wgs = tiles * slices
@@ -166,11 +177,13 @@ def is_implicit_conv(problem: dict) -> bool:
 
 
 def candidates(M: int, N: int, K: int, *, budget: int = 24, seed: int = 0, extra_random: int = 4,
-               conv: bool = False, stream_k: int = 4) -> list:
+               conv: bool = False, stream_k: int = 4, unroll: int = 4) -> list:
     """The ``budget`` best schedules by the cost model, a seeded random few
     more, the shape-aware default (``conv``: implicit-GEMM convolution
-    schedules only), and the stream-K form of the ``stream_k`` best unsplit
-    ones whose tile count is above the CU count and not a multiple of it."""
+    schedules only), the stream-K form of the ``stream_k`` best unsplit
+    ones whose tile count is above the CU count and not a multiple of it,
+    and the K loop unrolled by two of the ``unroll`` best double-buffered
+    ones (the cost model does not see the unroll, so it is measured)."""
     space = list(gemm_search_space(SPLITS))
     space = [s for s in space if split_slices(K, s)[0] == s.SK or s.SK == 1]
     if conv:
@@ -185,6 +198,9 @@ def candidates(M: int, N: int, K: int, *, budget: int = 24, seed: int = 0, extra
         pick.append(d)
     uneven = [s for s in pick if s.SK == 1 and _tiles(s, M, N) > CUS and _tiles(s, M, N) % CUS]
     pick += [s.with_stream_k() for s in uneven[:stream_k]]
+    pick += [s.with_unroll(2) for s in [s for s in pick if s.DB and s.UN == 1][:unroll]]
+    if not conv:                      # dense GEMMs: every wave-split form is measured too
+        pick += list(wsplit_search_space())
     return pick
 
 
@@ -315,8 +331,11 @@ def measure(problem: dict, sched: Optional[MfmaSchedule], ctx, *, iters: int = 2
 
 # A measured candidate is accepted only if its output agrees with the
 # default schedule's on the same feed: bit-exact for int8 (the integer
-# result does not depend on the schedule), and within the per-tensor fp32
-# tolerance otherwise (split-K and tile shape change the summation order).
+# result does not depend on the schedule), and for fp32 within rtol 1e-4
+# plus an absolute 1e-5 of the output's RMS magnitude (split-K and tile
+# shape change the summation order, so outputs near zero differ by a few
+# ulps of the typical term, not of themselves; a wrong tile is off by the
+# whole magnitude).
 AGREE_RTOL, AGREE_ATOL = 1e-4, 1e-5
 
 
@@ -328,8 +347,10 @@ def outputs_agree(got, want) -> bool:
         return False
     if np.issubdtype(want.dtype, np.integer):
         return bool(np.array_equal(got, want))
-    return bool(np.all(np.abs(got.astype(np.float64) - want) <=
-                       AGREE_ATOL + AGREE_RTOL * np.abs(want.astype(np.float64))))
+    w = want.astype(np.float64)
+    scale = float(np.sqrt(np.mean(w * w))) if w.size else 0.0
+    return bool(np.all(np.abs(got.astype(np.float64) - w) <= AGREE_ATOL * max(scale, 1.0)
+                       + AGREE_RTOL * np.abs(w)))
 
 
 class TuneError(RuntimeError):

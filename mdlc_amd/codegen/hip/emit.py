@@ -9,6 +9,8 @@ mdlc/codegen/cuda/emit.py:38-95 (``Launch``, ``CudaModule``); the kinds are
 extended because nothing runs on the host here:
 
   gemm        dense GEMM + epilogue (Gemm/MatMul, and conv after im2col)
+  gemm_ws     dense GEMM with the K range split over the waves of a workgroup
+              (small M x N, deep K: one launch, no split-K workspace)
   conv        implicit-GEMM convolution (no column buffer)
   gconv       grouped convolution: the implicit GEMM with one grid row per group
   conv_smallc direct convolution for few input channels (stems): input patch
@@ -121,18 +123,20 @@ class HipCodegen(Int8LoweringMixin):
         self.consts[name] = np.ascontiguousarray(array, dtype=np.float32)
         return name
 
-    def _pack_rows(self, g: Graph, src: str, rows: int, cols: int, transpose: bool = False) -> tuple:
+    def _pack_rows(self, g: Graph, src: str, rows: int, cols: int, transpose: bool = False,
+                   tag: str = "") -> tuple:
         """Constant as a row-major [rows][ld] float32 matrix, ld = cols rounded
-        up to 4, zero padded. Returns (device name, ld)."""
+        up to 4, zero padded. ``tag`` names a second layout of the same
+        constant. Returns (device name, ld)."""
         arr = np.asarray(g.initializers[src], dtype=np.float32)
         mat = arr.T if transpose else arr.reshape(rows, cols) if arr.ndim != 2 else arr
         mat = np.asarray(mat).reshape(rows, cols)
         ld = round4(cols)
         if ld == cols:
-            return self._pack(f"{src}__dev", mat), ld
+            return self._pack(f"{src}__dev{tag}", mat), ld
         pad = np.zeros((rows, ld), dtype=np.float32)
         pad[:, :cols] = mat
-        return self._pack(f"{src}__dev_ld{ld}", pad), ld
+        return self._pack(f"{src}__dev{tag}_ld{ld}", pad), ld
 
     @staticmethod
     def _act_sig(a: dict) -> tuple:
@@ -277,7 +281,8 @@ class HipCodegen(Int8LoweringMixin):
                                           "PT", "PB", "PL", "PR", "OH", "OW")}, "C": icg}
         sched = self._schedule(node, (ocg, P, K), problem)
         if sched.SK > 1 or sched.ST:
-            sched = MfmaSchedule(sched.BM, sched.BN, sched.BK, sched.WGM, sched.WGN, sched.MS, sched.DB)
+            sched = MfmaSchedule(sched.BM, sched.BN, sched.BK, sched.WGM, sched.WGN, sched.MS, sched.DB,
+                                 1, False, sched.UN)
         if not sched.conv_valid():
             raise ValueError(f"schedule {sched.key_full()} does not fit the convolution gather")
         tap_major = icg % sched.BK == 0
@@ -378,6 +383,20 @@ class HipCodegen(Int8LoweringMixin):
                epi["alpha"], epi["beta"], win, residual)
         meta = dict(meta, ksplit=slices, kchunk=chunk, ldc=epi["ldc"], hw=epi["hw"])
         meta.setdefault("ldb", 0)
+        if sched.WK > 1:
+            if kind != "gemm" or bmode > 1 or out_nchw or residual:
+                raise ValueError(f"schedule {sched.key()} is for dense GEMMs only")
+            b_kn = bool(meta.get("b_kn"))
+            va = vec_a and K % 16 == 0 and meta["lda"] % 4 == 0 and (not b_kn or meta["ldb"] % 4 == 0)
+            wsig = ("gemm_ws", sched, bool(bias), epi["bias_mode"], epi["act_sig"], epi["alpha"],
+                    epi["beta"], va, b_kn)
+            kname = self._kernel(wsig, lambda i: T.gemm_wsplit_kernel(
+                f"gemm_{sched.key()}_{act or 'none'}_{epi['bias_mode']}_{i}", sched,
+                with_bias=bool(bias), bias_mode=epi["bias_mode"], activation=act,
+                attrs=epi["attrs"], alpha=epi["alpha"], beta=epi["beta"], vec_a=va, b_kn=b_kn))
+            self.plan.append(Launch("gemm_ws", kname, operands + bias, [out], (tiles, 1, 1), block,
+                                    meta))
+            return
         if sched.ST and tiles % STREAM_K_WGS:
             self._emit_stream_k(kind, sched, operands, bias, out, meta, epi, bmode=bmode,
                                 vec_a=vec_a, out_nchw=out_nchw, win=win, tiles=tiles)
@@ -502,7 +521,16 @@ class HipCodegen(Int8LoweringMixin):
         else:
             adev, lda = A, K
             vec_a = K % 4 == 0
-        if g.is_constant(B):
+        act = a.get("activation")
+        problem = {"kind": "gemm", "M": M, "N": N, "K": K, "bias": has_bias, "act": act,
+                   "vec_a": vec_a, "bmode": 0 if g.is_constant(B) or N % 4 == 0 else 1}
+        sched = self._schedule(node, (M, N, K), problem)
+        b_kn = sched.WK > 1 and sched.BT and g.is_constant(B)
+        if b_kn:
+            # the wave-split kernel reads constant weights K-contiguous per column
+            bdev, ldb = self._pack_rows(g, B, N, K, transpose=not tb, tag="_kn")
+            bmode = 0
+        elif g.is_constant(B):
             bdev, ldb = self._pack_rows(g, B, K, N, transpose=bool(tb))
             bmode = 0
         elif tb:
@@ -522,11 +550,8 @@ class HipCodegen(Int8LoweringMixin):
                 bias_ins = [self._pack(f"{c}__col{N}", np.full(N, carr.reshape(()), np.float32))]
             else:
                 raise NotImplementedError(f"HIP codegen: Gemm C of shape {carr.shape} unsupported")
-        act = a.get("activation")
-        problem = {"kind": "gemm", "M": M, "N": N, "K": K, "bias": has_bias, "act": act,
-                   "vec_a": vec_a, "bmode": bmode}
-        sched = self._schedule(node, (M, N, K), problem)
         meta = {"M": M, "N": N, "K": K, "lda": lda, "ldb": ldb, "transA": ta, "transB": tb,
+                "b_kn": b_kn,
                 "alpha": alpha, "beta": beta, "with_bias": has_bias, "node": node,
                 "sched": sched, "flops": 2 * M * N * K,
                 "bytes": 4 * (M * K + K * N + M * N + (N if has_bias else 0))}

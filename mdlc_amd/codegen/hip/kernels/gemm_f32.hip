@@ -21,6 +21,8 @@
 // A and B tiles of depth BK are staged through LDS, double buffered (DB: the
 // next tile's global loads are in flight while the current tile feeds the
 // MFMAs, one barrier per K step) or single buffered (two barriers per step).
+// A double-buffered loop may be unrolled by two (UN = 2) so that the two
+// LDS buffers are compile-time operands.
 // LDS rows are padded by 4 floats: rows stay 16-byte aligned for
 // ds_read_b128 and consecutive rows start on different banks.
 //
@@ -86,7 +88,7 @@ __device__ __forceinline__ float pick(const float4& v, int q) {
 // the epilogue for OUT (slice ks of a split-K workspace for OUT == 2); slot
 // >= 0: raw sums into the stream-K workspace, tile-local rows of BN.
 template <int BM, int BN, int BK, int WGM, int WGN, int MS, bool DB, bool VA, int BMODE, int OUT,
-          class Epi, class Win>
+          class Epi, class Win, int UN = 1>
 __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0, int kbeg, int kend,
                                               int ks, int slot) {
   constexpr int NT = WGM * WGN * 64;
@@ -319,14 +321,40 @@ __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0,
     load_tiles(kbeg);
     store_tiles(0);
     __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-      const int cur = kt & 1;
-      load_tiles(kbeg + (kt + 1) * BK);
-      __builtin_amdgcn_s_setprio(1);
-      compute(cur);
-      __builtin_amdgcn_s_setprio(0);
-      store_tiles(cur ^ 1);
-      __syncthreads();
+    if (UN == 2) {
+      // K loop unrolled by two: both buffers are named at compile time, so
+      // every LDS address is a constant offset from a base fixed per thread
+      int kt = 0;
+      for (; kt + 2 <= nk; kt += 2) {
+        load_tiles(kbeg + (kt + 1) * BK);
+        __builtin_amdgcn_s_setprio(1);
+        compute(0);
+        __builtin_amdgcn_s_setprio(0);
+        store_tiles(1);
+        __syncthreads();
+        load_tiles(kbeg + (kt + 2) * BK);
+        __builtin_amdgcn_s_setprio(1);
+        compute(1);
+        __builtin_amdgcn_s_setprio(0);
+        store_tiles(0);
+        __syncthreads();
+      }
+      if (kt < nk) {                   // odd step count: the last tile is in buffer 0
+        __builtin_amdgcn_s_setprio(1);
+        compute(0);
+        __builtin_amdgcn_s_setprio(0);
+        __syncthreads();               // LDS free before a following piece's prologue
+      }
+    } else {
+      for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        load_tiles(kbeg + (kt + 1) * BK);
+        __builtin_amdgcn_s_setprio(1);
+        compute(cur);
+        __builtin_amdgcn_s_setprio(0);
+        store_tiles(cur ^ 1);
+        __syncthreads();
+      }
     }
   } else {
     for (int kt = 0; kt < nk; ++kt) {
@@ -456,7 +484,7 @@ __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0,
 // to workspace slot 2j + p and streamk_fixup_f32 adds each tile's pieces in
 // K order and applies the epilogue.
 template <int BM, int BN, int BK, int WGM, int WGN, int MS, bool DB, bool VA, int BMODE, int OUT,
-          class Epi, class Win, int SKW = 0>
+          class Epi, class Win, int SKW = 0, int UN = 1>
 __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
   const int tiles_m = (g.M + BM - 1) / BM;
   const int tiles_n = (g.N + BN - 1) / BN;
@@ -466,7 +494,7 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
     const int ks = t / tiles;
     const int tt = t - ks * tiles;
     const int kbeg = ks * g.kchunk;
-    gemm_f32_tile<BM, BN, BK, WGM, WGN, MS, DB, VA, BMODE, OUT, Epi, Win>(
+    gemm_f32_tile<BM, BN, BK, WGM, WGN, MS, DB, VA, BMODE, OUT, Epi, Win, UN>(
         g, (tt % tiles_m) * BM, (tt / tiles_m) * BN, kbeg, min(g.K, kbeg + g.kchunk), ks, -1);
     return;
   }
@@ -491,7 +519,7 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
     const int tt = (int)(it / KT);
     const int k0 = (int)(it - (long long)tt * KT);
     const int k1 = (int)min((long long)KT, k0 + (it1 - it));
-    gemm_f32_tile<BM, BN, BK, WGM, WGN, MS, DB, VA, BMODE, OUT, Epi, Win>(
+    gemm_f32_tile<BM, BN, BK, WGM, WGN, MS, DB, VA, BMODE, OUT, Epi, Win, UN>(
         g, (tt % tiles_m) * BM, (tt / tiles_m) * BN, k0 * BK, min(g.K, k1 * BK), 0, slot);
     it += k1 - k0;
     if (slot >= 0) ++slot;

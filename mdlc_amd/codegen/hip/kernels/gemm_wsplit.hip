@@ -1,0 +1,175 @@
+// Small-output fp32 GEMM, one launch, K split across the waves of a
+// workgroup:
+//
+//   C = epi(A[M x K] * B[K x N], bias)
+//
+// For GEMMs whose M x N gives few 64x64 tiles but whose K is deep (batch-1
+// convolutions as GEMMs, a fully connected layer at small batch), a tile per
+// workgroup leaves most CUs idle and a split-K grid needs a second launch to
+// add the slices. Here a workgroup of WK waves owns one (16*MI) x (16*NI)
+// output tile; wave w computes the partial sums of the whole tile over its
+// own contiguous 1/WK of the K steps, straight from global memory into
+// registers (no LDS staging: every operand element is used by exactly one
+// wave), with the next steps' loads in flight while the current ones feed
+// v_mfma_f32_16x16x4f32. The WK partial tiles then meet in LDS and are added
+// in wave order (a fixed order: results do not depend on timing), the
+// epilogue is applied and the tile is stored.
+//
+// Operand fragments: in each 16-deep K step, lane l = 16*g + i holds
+// A[m0 + i][k0 + 4g + q] and B[k0 + 4g + q][n0 + i] for q = 0..3, and MFMA q
+// takes element q, so lane group g supplies k = k0 + 4g + q: every k of the
+// step exactly once, for A and B alike. A's four values are one 16-byte load
+// when VA (K % 16 == 0 and lda % 4 == 0). B is either row-major [K][ldb]
+// (four loads, each a 64-byte run of a B row across the 16 lanes of a
+// group) or, BKN, stored K-contiguous per column as [N][ldb] (constant
+// weights packed that way), when its four values are one 16-byte load too.
+// Every vector memory instruction costs the CU's address pipeline the same
+// whatever its width, so the 16-byte forms matter more than the bytes.
+namespace mdlc {
+
+template <int MI, int NI, int WK, int UN, bool VA, bool BKN, class Epi>
+__device__ __forceinline__ void gemm_f32_wsplit(const float* __restrict__ A,
+                                                const float* __restrict__ B,
+                                                const float* __restrict__ bias,
+                                                float* __restrict__ C, int M, int N, int K,
+                                                int lda, int ldb, int ldc) {
+  constexpr int TM = 16 * MI, TN = 16 * NI;
+  __shared__ __attribute__((aligned(16))) floatx4 red[WK][MI][NI][64];
+
+  const int tiles_m = (M + TM - 1) / TM;
+  const int m0 = (blockIdx.x % tiles_m) * TM;
+  const int n0 = (blockIdx.x / tiles_m) * TN;
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+
+  // this wave's contiguous share of the 16-deep K steps
+  const int steps = (K + 15) / 16;
+  const int s0 = (int)((long long)steps * w / WK);
+  const int s1 = (int)((long long)steps * (w + 1) / WK);
+
+  const float* ap[MI];
+  bool aok[MI];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) {
+    const int row = m0 + mi * 16 + li;
+    aok[mi] = row < M;
+    ap[mi] = A + (size_t)min(row, M - 1) * lda + 4 * lg;
+  }
+  const float* bp[NI];
+  bool bok[NI];
+#pragma unroll
+  for (int ni = 0; ni < NI; ++ni) {
+    const int col = n0 + ni * 16 + li;
+    bok[ni] = col < N;
+    bp[ni] = BKN ? B + (size_t)min(col, N - 1) * ldb + 4 * lg
+                 : B + (size_t)(4 * lg) * ldb + min(col, N - 1);
+  }
+
+  floatx4 acc[MI][NI];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // UN steps per stage, two stages of registers: the loads of stage j + 1
+  // are issued before the MFMAs of stage j
+  float av[2][UN][MI][4];
+  float bv[2][UN][NI][4];
+  auto load = [&](int buf, int s) {
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const int k0 = (s + u) * 16;
+      const bool live = s + u < s1;
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi) {
+        if (VA) {
+          const float4 v = (live && aok[mi]) ? ld4(ap[mi] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+          av[buf][u][mi][0] = v.x;
+          av[buf][u][mi][1] = v.y;
+          av[buf][u][mi][2] = v.z;
+          av[buf][u][mi][3] = v.w;
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const bool ok = live && aok[mi] && k0 + 4 * lg + q < K;
+            av[buf][u][mi][q] = ok ? ap[mi][k0 + q] : 0.f;
+          }
+        }
+      }
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) {
+        if (BKN && VA) {
+          const float4 v = (live && bok[ni]) ? ld4(bp[ni] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+          bv[buf][u][ni][0] = v.x;
+          bv[buf][u][ni][1] = v.y;
+          bv[buf][u][ni][2] = v.z;
+          bv[buf][u][ni][3] = v.w;
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const bool ok = live && bok[ni] && k0 + 4 * lg + q < K;
+            bv[buf][u][ni][q] = ok ? (BKN ? bp[ni][k0 + q] : bp[ni][(size_t)(k0 + q) * ldb]) : 0.f;
+          }
+        }
+      }
+    }
+  };
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < UN; ++u)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+          for (int ni = 0; ni < NI; ++ni)
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[buf][u][mi][q], bv[buf][u][ni][q],
+                                                               acc[mi][ni], 0, 0, 0);
+  };
+
+  if (s0 < s1) {
+    load(0, s0);
+    int s = s0;
+    // two stages per trip so both register sets are compile-time names
+    for (; s + 2 * UN < s1; s += 2 * UN) {
+      load(1, s + UN);
+      compute(0);
+      load(0, s + 2 * UN);
+      compute(1);
+    }
+    if (s + UN < s1) {
+      load(1, s + UN);
+      compute(0);
+      compute(1);
+    } else {
+      compute(0);
+    }
+  }
+
+  // partial tiles meet in LDS; every thread then owns some tile elements
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) red[w][mi][ni][lane] = acc[mi][ni];
+  __syncthreads();
+  const float* redf = reinterpret_cast<const float*>(&red[0][0][0][0]);
+  for (int e = threadIdx.x; e < TM * TN; e += WK * 64) {
+    const int row = e / TN, col = e - (e / TN) * TN;
+    const int mi = row / 16, ni = col / 16;
+    // 16x16x4 output layout: lane 16*(r/4) + c holds rows 4*(r/4) .. +3 of column c
+    const int rr = row % 16, cc = col % 16;
+    const int slot = ((mi * NI + ni) * 64 + (rr / 4) * 16 + cc) * 4 + (rr % 4);
+    float v = 0.f;
+#pragma unroll
+    for (int k = 0; k < WK; ++k) v += redf[k * MI * NI * 256 + slot];
+    const int gr = m0 + row, gc = n0 + col;
+    if (gr < M && gc < N) {
+      const float b = Epi::bias == 2 ? bias[gc] : (Epi::bias == 1 ? bias[gr] : 0.f);
+      C[(size_t)gr * ldc + gc] = Epi::apply(v, b);
+    }
+  }
+}
+
+}  // namespace mdlc

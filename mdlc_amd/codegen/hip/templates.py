@@ -162,7 +162,7 @@ def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: s
     out = 2 if split else (1 if out_nchw else 0)
     tmpl = (f"mdlc::gemm_f32_mfma<{s.BM}, {s.BN}, {s.BK}, {s.WGM}, {s.WGN}, {s.MS}, "
             f"{'true' if s.DB else 'false'}, {'true' if vec_a else 'false'}, {bmode}, "
-            f"{out}, {epi}, {winty}, {int(stream_k)}>")
+            f"{out}, {epi}, {winty}, {int(stream_k)}, {s.UN}>")
     nt = s.threads_per_block()
     ws_arg = "float* __restrict__ ws, " if stream_k else ""
     ws_val = "ws" if stream_k else "nullptr"
@@ -197,6 +197,28 @@ def gemm_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: s
             f"ksplit, kchunk, {ws_val}, 0, M * hw}};\n"
             f"  {tmpl}(g);\n}}\n")
     return name, "\n".join(src)
+
+
+def gemm_wsplit_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_mode: str,
+                       activation: Optional[str], attrs: dict, alpha: float = 1.0,
+                       beta: float = 1.0, vec_a: bool, b_kn: bool) -> tuple:
+    """The wave-split GEMM (``sched.WK`` waves share the K range of one
+    tile). ABI: (A, B, [bias], C, int M, int N, int K, int lda, int ldb,
+    int ldc); one workgroup of 64 * WK threads per BM x BN tile, m fastest.
+    ``b_kn``: B is stored [N][ldb] (K contiguous per output column)."""
+    s = sched
+    epi = f"{name}_epi"
+    src = epilogue_struct(epi, bias_mode=bias_mode if with_bias else None, activation=activation,
+                          attrs=attrs, alpha=alpha, beta=beta)
+    bias_arg = "const float* __restrict__ bias, " if with_bias else ""
+    return name, src + (
+        f'extern "C" __global__ __launch_bounds__({s.threads_per_block()}) void {name}(\n'
+        f"    const float* __restrict__ A, const float* __restrict__ B, {bias_arg}"
+        "float* __restrict__ C, int M, int N,\n    int K, int lda, int ldb, int ldc) {\n"
+        f"  mdlc::gemm_f32_wsplit<{s.BM // 16}, {s.BN // 16}, {s.WK}, {s.UN}, "
+        f"{'true' if vec_a else 'false'}, {'true' if b_kn else 'false'}, {epi}>(A, B, "
+        f"{'bias' if with_bias else 'nullptr'}, C, "
+        "M, N, K, lda, ldb, ldc);\n}\n")
 
 
 def splitk_reduce_kernel(name: str, *, with_bias: bool, bias_mode: str,

@@ -39,9 +39,14 @@ class MfmaSchedule:
     DB: bool = True
     SK: int = 1
     ST: bool = False        # stream-K remainder (fp32 GEMM/conv, SK == 1): see gemm_f32_mfma
+    UN: int = 1             # K-loop unroll of the double-buffered fp32 loop (1 or 2); with
+                            # WK > 1, the 16-deep K steps per register stage (1, 2, 4, 8)
+    WK: int = 1             # > 1: the wave-split kernel (dense fp32 GEMM): WK waves share the
+                            # K range of one BM x BN tile (BM, BN in 16, 32), one launch
+    BT: bool = False        # wave-split only: constant B stored K-contiguous per column
 
     def threads_per_block(self) -> int:
-        return 64 * self.WGM * self.WGN
+        return 64 * self.WGM * self.WGN * self.WK
 
     def wave_tile(self) -> tuple:
         return self.BM // self.WGM, self.BN // self.WGN
@@ -58,9 +63,15 @@ class MfmaSchedule:
         return (2 if self.DB else 1) * (self.BM * (self.BK + 4) + b) * elem_bytes
 
     def is_valid(self) -> bool:
+        if self.WK != 1:
+            return self.wsplit_valid()
+        if self.BT:
+            return False
         if min(self.BM, self.BN, self.BK, self.WGM, self.WGN, self.SK) <= 0 or self.MS not in (16, 32):
             return False
         if self.ST and self.SK != 1:
+            return False
+        if self.UN not in (1, 2) or (self.UN == 2 and not self.DB):
             return False
         wm, wn = self.wave_tile()
         if self.BM % self.WGM or self.BN % self.WGN:
@@ -77,10 +88,20 @@ class MfmaSchedule:
             return False
         return True
 
+    def wsplit_valid(self) -> bool:
+        """The wave-split kernel: 16x16x4 MFMAs, a (BM x BN) tile of 16x16
+        blocks per wave, WK waves over K, no LDS staging, one launch."""
+        # two register stages of UN steps: 2 * UN * (MI + NI) * 4 operand VGPRs
+        regs = 2 * self.UN * (self.BM // 16 + self.BN // 16) * 4
+        return (self.WK in (2, 4, 8, 16) and self.BM in (16, 32) and self.BN in (16, 32)
+                and self.MS == 16 and self.WGM == 1 and self.WGN == 1 and self.BK == 16
+                and not self.DB and self.SK == 1 and not self.ST and self.UN in (1, 2, 4, 8)
+                and regs <= 192)
+
     def conv_valid(self) -> bool:
         """Valid for the implicit-GEMM convolution kernels, whose gather gives
         each B column to NT / BN threads with BK / (NT / BN) k rows each."""
-        if not self.is_valid():
+        if self.WK != 1 or not self.is_valid():
             return False
         nt = self.threads_per_block()
         if nt % self.BN or self.BK % (nt // self.BN):
@@ -88,17 +109,30 @@ class MfmaSchedule:
         return self.lds_bytes(b_kmajor=True) <= LDS_LIMIT
 
     def key(self) -> str:
+        if self.WK != 1:
+            return (f"WS{self.WK}_BM{self.BM}_BN{self.BN}{f'_U{self.UN}' if self.UN > 1 else ''}"
+                    f"{'_BT' if self.BT else ''}")
         return (f"BM{self.BM}_BN{self.BN}_BK{self.BK}_W{self.WGM}x{self.WGN}"
-                f"_M{self.MS}{'_DB' if self.DB else ''}")
+                f"_M{self.MS}{'_DB' if self.DB else ''}{'_U2' if self.UN == 2 else ''}")
 
     def key_full(self) -> str:
         return self.key() + (f"_SK{self.SK}" if self.SK > 1 else "") + ("_ST" if self.ST else "")
 
+    @staticmethod
+    def wsplit(bm: int, bn: int, wk: int, un: int = 1, bt: bool = False) -> "MfmaSchedule":
+        return MfmaSchedule(bm, bn, 16, 1, 1, 16, False, 1, False, un, wk, bt)
+
     def with_split(self, sk: int) -> "MfmaSchedule":
-        return MfmaSchedule(self.BM, self.BN, self.BK, self.WGM, self.WGN, self.MS, self.DB, sk)
+        return MfmaSchedule(self.BM, self.BN, self.BK, self.WGM, self.WGN, self.MS, self.DB, sk,
+                            False, self.UN)
 
     def with_stream_k(self) -> "MfmaSchedule":
-        return MfmaSchedule(self.BM, self.BN, self.BK, self.WGM, self.WGN, self.MS, self.DB, 1, True)
+        return MfmaSchedule(self.BM, self.BN, self.BK, self.WGM, self.WGN, self.MS, self.DB, 1, True,
+                            self.UN)
+
+    def with_unroll(self, un: int) -> "MfmaSchedule":
+        return MfmaSchedule(self.BM, self.BN, self.BK, self.WGM, self.WGN, self.MS, self.DB, self.SK,
+                            self.ST, un)
 
     def as_dict(self) -> dict:
         return asdict(self)
@@ -115,6 +149,17 @@ def gemm_search_space(splits=(1,)) -> Iterator[MfmaSchedule]:
                                 s = MfmaSchedule(bm, bn, bk, wgm, wgn, ms, db, sk)
                                 if s.is_valid():
                                     yield s
+
+
+def wsplit_search_space() -> Iterator[MfmaSchedule]:
+    for bm in (16, 32):
+        for bn in (16, 32):
+            for wk in (4, 8, 16):
+                for un in (1, 2, 4, 8):
+                    for bt in (False, True):
+                        s = MfmaSchedule.wsplit(bm, bn, wk, un, bt)
+                        if s.is_valid():
+                            yield s
 
 
 def split_slices(K: int, sched: MfmaSchedule) -> tuple:

@@ -41,6 +41,9 @@ def model_problems(model: str, batch: int, conv_mode: str) -> list:
         return [{"kind": "qgemm", "M": batch, "N": batch, "K": batch, "out_f32": False}]
     if model == "fp32_gemm":          # a square dense fp32 GEMM, M = N = K = batch
         return [{"kind": "gemm", "M": batch, "N": batch, "K": batch}]
+    if model == "micro":              # the five fused GEMM+bias+ReLU micro shapes
+        from mdlc_amd.tools.micro_gemm import SHAPES
+        return [{"kind": "gemm", "M": M, "N": N, "K": K} for M, N, K in SHAPES]
     if model == "resnet18":
         from mdlc_amd.tools.build_resnet18 import build_resnet18
         graph = build_resnet18(batch=batch, calibrate=False)

@@ -33,6 +33,14 @@ SCHEDULES = [
     MfmaSchedule(32, 32, 16, 1, 1, 16, True, 2),       # split-K with 16x16x4
     MfmaSchedule(32, 32, 16, 1, 1, 16, True, 1, True),  # stream-K: every tile in pieces
     MfmaSchedule(64, 64, 16, 2, 2, 32, False, 1, True),
+    MfmaSchedule(64, 64, 16, 2, 2, 32, True, 1, False, 2),      # K loop unrolled by two
+    MfmaSchedule(64, 64, 16, 2, 2, 32, True, 3, False, 2),      # ... with split-K slices
+    MfmaSchedule(32, 32, 16, 1, 1, 16, True, 1, True, 2),       # ... with stream-K pieces
+    MfmaSchedule.wsplit(16, 16, 4),                            # K over the waves of a workgroup
+    MfmaSchedule.wsplit(32, 32, 16, 2),
+    MfmaSchedule.wsplit(16, 32, 8, 2),
+    MfmaSchedule.wsplit(16, 16, 8, 8),
+    MfmaSchedule.wsplit(32, 16, 4, 1, True),                   # weights K-contiguous per column
 ]
 
 
@@ -78,6 +86,20 @@ def test_micro_gemm_shapes(M, N, K, hip_ctx):
     g, feeds = build_micro_gemm(M, N, K)
     c, got, want = device_run(g, feeds, ctx=hip_ctx)
     assert [n.op_type for n in c.graph.nodes] == ["FusedGemmAct"]
+    assert_close("C", got["C"], want["C"])
+
+
+@pytest.mark.parametrize("sched", [MfmaSchedule.wsplit(16, 16, 8), MfmaSchedule.wsplit(32, 16, 16, 2),
+                                   MfmaSchedule.wsplit(16, 32, 4, 2), MfmaSchedule.wsplit(16, 16, 16, 8),
+                                   MfmaSchedule.wsplit(32, 16, 4, 4), MfmaSchedule.wsplit(16, 16, 8, 2, True),
+                                   MfmaSchedule.wsplit(32, 32, 4, 1, True)], ids=lambda s: s.key())
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_micro_gemm_wave_split(M, N, K, sched, hip_ctx):
+    """The one-launch wave-split kernel on the micro shapes (16-byte A loads,
+    K % 16 == 0) against the oracle."""
+    g, feeds = build_micro_gemm(M, N, K)
+    c, got, want = device_run(g, feeds, ctx=hip_ctx, schedule_fn=lambda n, mnk: sched)
+    assert [l.kind for l in c.module.plan] == ["gemm_ws"]
     assert_close("C", got["C"], want["C"])
 
 
@@ -239,6 +261,7 @@ CONV_SCHEDULES = [
     MfmaSchedule(128, 64, 16, 4, 2, 16, True),      # 8 threads/column, 2 rows each
     MfmaSchedule(64, 64, 32, 4, 2, 16, True),       # 8 threads/column, 4 rows each
     MfmaSchedule(32, 128, 32, 1, 2, 32, False),     # 1 thread/column, 32 rows, single buffered
+    MfmaSchedule(64, 64, 32, 4, 2, 16, True, 1, False, 2),   # K loop unrolled by two
 ]
 
 
