@@ -41,14 +41,14 @@ class Int8LoweringMixin:
                              f"writes {want}; rerun shape inference")
 
     def _emit_qgemm(self, node, sched, a_in, b_dev, bias, mult, out, meta, *, amode, out_f32, lo, win,
-                    gv=16, epi=0, aux=None, depthwise=False):
+                    gv=16, epi=0, aux=None, depthwise=False, out_i32=False):
         """One int8 GEMM launch. The kernel reads bias and mult four columns
         at a time, so both are packed zero padded to a multiple of 16; its
         buffer loads take 32-bit offsets, so every operand stays under 2 GiB."""
         M, N, K = meta["M"], meta["N"], meta["K"]
         g = self._graph
         self._check_dtype(g, a_in, "int8")
-        self._check_dtype(g, out, "float32" if out_f32 else "int8")
+        self._check_dtype(g, out, "float32" if out_f32 else ("int32" if out_i32 else "int8"))
         if meta["ldb"] % sched.BK or meta["ldb"] < K:
             raise ValueError(f"int8 weights must be padded to a multiple of BK={sched.BK}")
         a_bytes = (M * meta["lda"] if amode == 0 else
@@ -66,20 +66,22 @@ class Int8LoweringMixin:
         bias_dev = self._pack_raw(f"{bias}__dev{n16}", bpad)
         mult_dev = self._pack_raw(f"{mult}__dev{n16}", mpad)
         cin = sched.BN if depthwise else (meta["Cin"] if amode else 0)
-        sig = ("qgemm", sched, amode, gv, cin, out_f32, lo, win, epi, depthwise)
+        sig = ("qgemm", sched, amode, gv, cin, out_f32, lo, win, epi, depthwise, out_i32)
         tag = "qdwmfma" if depthwise else ("qconv" if amode else "qgemm")
         etag = ("", "_lut", "_add")[epi]
         kname = self._kernel(sig, lambda i: T.qgemm_kernel(
-            f"{tag}_{sched.key()}_a{amode}{'' if not amode else f'g{gv}'}_{'f32' if out_f32 else 'i8'}"
-            f"{etag}_{i}", sched, amode=amode, out_f32=out_f32, lo=lo, win=win, gv=gv, cin=cin, epi=epi,
-            depthwise=depthwise))
+            f"{tag}_{sched.key()}_a{amode}{'' if not amode else f'g{gv}'}_"
+            f"{'f32' if out_f32 else ('i32' if out_i32 else 'i8')}{etag}_{i}", sched, amode=amode,
+            out_f32=out_f32, lo=lo, win=win, gv=gv, cin=cin, epi=epi, depthwise=depthwise,
+            out_i32=out_i32))
         tiles = -(-M // sched.BM) * -(-N // sched.BN)
         ins = [a_in, b_dev, bias_dev, mult_dev] + ([aux] if aux else [])
         # algorithmic HBM bytes: activation, weights, bias/mult, output, residual
         a_read = a_bytes if amode else M * K
         w_read = N * (K // sched.BN if depthwise else K)
         ops = meta.get("depthwise_ops", 2 * M * N * K)
-        nbytes = (a_read + w_read + 8 * N + M * N * (4 if out_f32 else 1) + (M * N if epi == 2 else 0))
+        nbytes = (a_read + w_read + 8 * N + M * N * (4 if out_f32 or out_i32 else 1)
+                  + (M * N if epi == 2 else 0))
         self.plan.append(Launch("qgemm", kname, ins, [out], (tiles, 1, 1),
                                 (sched.threads_per_block(), 1, 1),
                                 dict(meta, node=node, sched=sched, ops=ops, bytes=nbytes,
@@ -327,7 +329,8 @@ class Int8LoweringMixin:
             raise NotImplementedError("HIP codegen: QGemm expects the weight as [N][K] (transB=1)")
         M, K = self._shape(g, x)
         N = self._shape(g, w)[0]
-        out_f32 = node.attrs.get("out_dtype", "int8") == "float32"
+        out_dtype = node.attrs.get("out_dtype", "int8")
+        out_f32, out_i32 = out_dtype == "float32", out_dtype == "int32"
         lo = 0 if node.attrs.get("activation") == "Relu" else -127
         if K % 16:
             raise NotImplementedError("HIP codegen: QGemm needs K % 16 == 0")
@@ -340,7 +343,7 @@ class Int8LoweringMixin:
         meta = {"M": M, "N": N, "K": K, "lda": K, "ldb": ldb, "ldc": N, "Cin": 0, "H": 0, "W": 0,
                 "OH": 0, "OW": 0}
         self._emit_qgemm(node, sched, x, wdev, b, m, node.outputs[0], meta, amode=0,
-                         out_f32=out_f32, lo=lo, win=None)
+                         out_f32=out_f32, lo=lo, win=None, out_i32=out_i32)
 
     def _lower_qadd(self, g, node):
         a, b = node.inputs[:2]

@@ -129,7 +129,19 @@ __device__ __forceinline__ void qgemm_epilogue(const QGemmArgs& g, Acc& acc, int
       for (int mi = 0; mi < MI; ++mi) {
         const int row = m0 + wm0 + mi * MS + li;
         if (row >= g.M) continue;
-        if (OUT == 1) {
+        if (OUT == 2) {
+          int* cp = static_cast<int*>(g.C) + (size_t)row * g.ldc + col;
+          int o[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[j] = acc[mi][ni][4 * q + j] + bv[j];
+          if (full) {
+            *reinterpret_cast<intx4*>(cp) = intx4{o[0], o[1], o[2], o[3]};
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (col + j < g.N) cp[j] = o[j];
+          }
+        } else if (OUT == 1) {
           float* cp = static_cast<float*>(g.C) + (size_t)row * g.ldc + col;
           float o[4];
 #pragma unroll
@@ -170,6 +182,32 @@ __device__ __forceinline__ void qgemm_epilogue(const QGemmArgs& g, Acc& acc, int
     }
 }
 
+// Scheduling hints for the interleaved int8 pipeline, as compile-time
+// recursion (the hint's arguments must be constants): per sub-step, its
+// MFS MFMAs each followed by one of EXTRA instructions of class MASK (LDS
+// reads 0x100 or LDS writes 0x200), any surplus of those after the last.
+template <int I, int MFS, int EXTRA, int MASK>
+struct PipeInterleave {
+  __device__ __forceinline__ static void emit() {
+    if constexpr (I < MFS) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if constexpr (I < EXTRA) __builtin_amdgcn_sched_group_barrier(MASK, 1, 0);
+      PipeInterleave<I + 1, MFS, EXTRA, MASK>::emit();
+    } else if constexpr (EXTRA > MFS) {
+      __builtin_amdgcn_sched_group_barrier(MASK, EXTRA - MFS, 0);
+    }
+  }
+};
+template <int SUB, int SUBS, int MFS, int NFR, int NST>
+struct PipeOrder {
+  __device__ __forceinline__ static void emit() {
+    if constexpr (SUB < SUBS) {
+      PipeInterleave<0, MFS, SUB + 1 < SUBS ? NFR : NST, SUB + 1 < SUBS ? 0x100 : 0x200>::emit();
+      PipeOrder<SUB + 1, SUBS, MFS, NFR, NST>::emit();
+    }
+  }
+};
+
 // C[m][n] = q(sum_k A[m][k] * B[n][k] + bias[n]).
 //
 // AMODE 0: dense A [M][lda] (lda % 16 == 0).
@@ -184,7 +222,8 @@ __device__ __forceinline__ void qgemm_epilogue(const QGemmArgs& g, Acc& acc, int
 //          arithmetic — cheap next to what the vector ALUs would take — and
 //          each input byte is still fetched once per tap.
 // OUT 0: int8 requantized output (LO = lower clamp); OUT 1: float32
-//        float(acc) * mult[n] (dequantized logits).
+//        float(acc) * mult[n] (dequantized logits); OUT 2: the int32
+//        accumulators plus bias, as they are (the exactness check).
 // EPI (OUT 0 only): 0 = the requantized codes; 1 = table[code + 128] (a
 //        fused lookup, table staged in LDS); 2 = a fused residual add,
 //        clamp(rint(f32(f32(r) * res_mult) + f32(f32(code) * acc_mult)))
@@ -202,7 +241,7 @@ __device__ __forceinline__ void qgemm_epilogue(const QGemmArgs& g, Acc& acc, int
 // consecutive output columns per accumulator group, stored as one 32-bit
 // (int8) or 128-bit (float) write.
 template <int BM, int BN, int BK, int WGM, int WGN, int MS, bool DB, int AMODE, int GV, int CIN, int OUT,
-          int LO, int EPI, int DWG, class Win>
+          int LO, int EPI, int DWG, class Win, bool PIPE = false>
 __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   constexpr int NT = WGM * WGN * 64;
   constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -366,16 +405,72 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   // basic block the scheduler can interleave with the MFMAs. The waves raise
   // their issue priority while they feed the matrix cores.
   constexpr bool kTwoSets = DB && MfmaI8<MS>::kAcc * MI * NI + 8 * (A_PT + B_PT) <= 192;
-  intx4 ra0[A_PT], rb0[B_PT], ra1[kTwoSets ? A_PT : 1], rb1[kTwoSets ? B_PT : 1];
+  static_assert(!PIPE || DB, "the interleaved pipeline needs two LDS buffers");
+  intx4 ra0[A_PT], rb0[B_PT], ra1[kTwoSets && !PIPE ? A_PT : 1], rb1[kTwoSets && !PIPE ? B_PT : 1];
   const int nk = (g.K + BK - 1) / BK;
-  if constexpr (kTwoSets) {
-    load_tiles(0, ra0, rb0);
-    load_tiles(BK, ra1, rb1);
+  // K tiles are visited from a per-tile starting tile, wrapping around:
+  // integer accumulation is exact in any order, and with every workgroup
+  // at a different K offset the rows the chip fetches at one time (K bytes
+  // apart: 4096 for a 4096-deep GEMM) stop landing on the same memory
+  // channels. Indices past the last tile stay past it (they load zeros).
+  const int krot = (mt * tiles_n + nt) % nk;
+  auto kofs = [&](int kt) -> int { return (kt < nk ? (kt + krot) % nk : kt) * BK; };
+  if constexpr (PIPE) {
+    // Interleaved pipeline (double-buffered LDS, one register set for the
+    // global staging): within one K tile the fragments of sub-step s + 1
+    // are read from LDS while the MFMAs of sub-step s run, the next tile's
+    // global loads are issued at the start, and written to the idle LDS
+    // buffer between the MFMAs of the last sub-step. The scheduling hints
+    // lay the iteration out in that order, so a wave keeps the matrix core
+    // fed on its own, without a second wave on the SIMD to hide latency.
+    constexpr int SUBS = KSUB / 16;
+    constexpr int NFR = MI + NI;                 // LDS reads per sub-step
+    constexpr int NST = A_PT + B_PT;             // LDS writes (and global loads) per tile
+    constexpr int MFS = MI * NI;                 // MFMAs per sub-step
+    auto read_frags = [&](intx4 (&fa)[MI], intx4 (&fb)[NI], const i8* as, const i8* bs, int sub) {
+      const int kk = lk * KSUB + sub * 16;
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+        fa[mi] = *reinterpret_cast<const intx4*>(as + (wm0 + mi * MS + li) * LDS_ROW + kk);
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+        fb[ni] = *reinterpret_cast<const intx4*>(bs + (wn0 + ni * MS + li) * LDS_ROW + kk);
+    };
+    load_tiles(kofs(0), ra0, rb0);
+    store_tiles(0, ra0, rb0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const i8* as = &As[kt & 1][0];
+      const i8* bs = &Bs[kt & 1][0];
+      intx4 fa[2][MI], fb[2][NI];
+      read_frags(fa[0], fb[0], as, bs, 0);
+      load_tiles(kofs(kt + 1), ra0, rb0);
+#pragma unroll
+      for (int sub = 0; sub < SUBS; ++sub) {
+        if (sub + 1 < SUBS) read_frags(fa[(sub + 1) & 1], fb[(sub + 1) & 1], as, bs, sub + 1);
+        else store_tiles((kt + 1) & 1, ra0, rb0);
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+          for (int ni = 0; ni < NI; ++ni)
+            acc[mi][ni] = MfmaI8<MS>::step(fb[sub & 1][ni], fa[sub & 1][mi], acc[mi][ni]);
+      }
+      // order: first fragments, the global loads, then per sub-step its
+      // MFMAs alternating with the next sub-step's reads (the last one's
+      // with the LDS writes)
+      __builtin_amdgcn_sched_group_barrier(0x100, NFR, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, NST, 0);
+      PipeOrder<0, SUBS, MFS, NFR, NST>::emit();
+      __syncthreads();
+    }
+  } else if constexpr (kTwoSets) {
+    load_tiles(kofs(0), ra0, rb0);
+    load_tiles(kofs(1), ra1, rb1);
     store_tiles(0, ra0, rb0);
     __syncthreads();
     auto step = [&](int kt, intx4 (&ra_in)[A_PT], intx4 (&rb_in)[B_PT], intx4 (&ra_nx)[A_PT],
                     intx4 (&rb_nx)[B_PT]) {
-      load_tiles((kt + 2) * BK, ra_in, rb_in);
+      load_tiles(kofs(kt + 2), ra_in, rb_in);
       __builtin_amdgcn_s_setprio(1);
       compute(kt & 1);
       __builtin_amdgcn_s_setprio(0);
@@ -387,11 +482,11 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
       if (kt + 1 < nk) step(kt + 1, ra1, rb1, ra0, rb0);
     }
   } else if constexpr (DB) {
-    load_tiles(0, ra0, rb0);
+    load_tiles(kofs(0), ra0, rb0);
     store_tiles(0, ra0, rb0);
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
-      load_tiles((kt + 1) * BK, ra0, rb0);
+      load_tiles(kofs(kt + 1), ra0, rb0);
       __builtin_amdgcn_s_setprio(1);
       compute(kt & 1);
       __builtin_amdgcn_s_setprio(0);
@@ -401,11 +496,11 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   } else {
     // one LDS buffer (half the LDS, e.g. for 256-byte K tiles): the next
     // tile waits in registers while the current one is consumed
-    load_tiles(0, ra0, rb0);
+    load_tiles(kofs(0), ra0, rb0);
     for (int kt = 0; kt < nk; ++kt) {
       store_tiles(0, ra0, rb0);
       __syncthreads();
-      load_tiles((kt + 1) * BK, ra0, rb0);
+      load_tiles(kofs(kt + 1), ra0, rb0);
       __builtin_amdgcn_s_setprio(1);
       compute(0);
       __builtin_amdgcn_s_setprio(0);

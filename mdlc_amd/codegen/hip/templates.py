@@ -514,12 +514,13 @@ def elementwise_signature(node: Node, scalar_consts: dict) -> tuple:
 
 def qgemm_kernel(name: str, sched: MfmaSchedule, *, amode: int, out_f32: bool, lo: int,
                  win: Optional[tuple] = None, gv: int = 16, cin: int = 0, epi: int = 0,
-                 depthwise: bool = False) -> tuple:
+                 depthwise: bool = False, out_i32: bool = False) -> tuple:
     """int8 MFMA GEMM / implicit conv with the requant (or dequant) epilogue.
     ``amode`` 0 = dense A, 1 = NHWC gather of ``gv`` bytes over ``cin``
     channels; ``epi`` 1 = fused table lookup, 2 = fused residual add;
     ``depthwise``: block-diagonal depthwise conv (``cin`` = BN channels per
-    block, the tensor's channel count passed as Cin).
+    block, the tensor's channel count passed as Cin). ``out_i32``: the raw
+    int32 accumulators plus bias, no requantization.
     ABI: (A, B, bias, mult, C, aux, int M, int N, int K, int lda, int ldb,
     int ldc, int Cin, int H, int W, int OH, int OW, float res_mult,
     float acc_mult)."""
@@ -528,7 +529,9 @@ def qgemm_kernel(name: str, sched: MfmaSchedule, *, amode: int, out_f32: bool, l
     nt = s.threads_per_block()
     tmpl = (f"mdlc::qgemm_i8_mfma<{s.BM}, {s.BN}, {s.BK}, {s.WGM}, {s.WGN}, {s.MS}, "
             f"{'true' if s.DB else 'false'}, {amode}, "
-            f"{gv}, {cin}, {1 if out_f32 else 0}, {int(lo)}, {epi}, {1 if depthwise else 0}, {winty}>")
+            f"{gv}, {cin}, {1 if out_f32 else (2 if out_i32 else 0)}, {int(lo)}, {epi}, "
+            f"{1 if depthwise else 0}, {winty}, "
+            f"{'true' if s.UN == 2 else 'false'}>")
     return name, (
         f'extern "C" __global__ __launch_bounds__({nt}) void {name}(\n'
         "    const signed char* __restrict__ A, const signed char* __restrict__ B,\n"

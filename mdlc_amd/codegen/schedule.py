@@ -211,7 +211,11 @@ def default_schedule(M: int, N: int, K: int) -> MfmaSchedule:
 # (DB) or single buffered.
 
 def qsched_valid(s: MfmaSchedule) -> bool:
-    if s.MS not in (16, 32) or s.SK != 1:
+    """Valid for the int8 GEMM/conv kernel; ``UN == 2`` selects its
+    interleaved pipeline (double-buffered only)."""
+    if s.MS not in (16, 32) or s.SK != 1 or s.ST or s.WK != 1 or s.BT:
+        return False
+    if s.UN not in (1, 2) or (s.UN == 2 and not s.DB):
         return False
     wm, wn = s.wave_tile()
     if s.BM % s.WGM or s.BN % s.WGN or wm % s.MS or wn % s.MS:
@@ -268,7 +272,8 @@ def qgemm_search_space():
     for bm in (32, 64, 128, 256):
         for bn in (32, 64, 128, 256):
             for bk in (64, 128, 256):
-                for wgm, wgn in ((1, 1), (2, 1), (1, 2), (2, 2), (4, 1), (1, 4), (4, 2), (2, 4)):
+                for wgm, wgn in ((1, 1), (2, 1), (1, 2), (2, 2), (4, 1), (1, 4), (4, 2), (2, 4),
+                                 (4, 4)):
                     for ms in (32, 16):
                         for db in (True, False):
                             s = MfmaSchedule(bm, bn, bk, wgm, wgn, ms, db, 1)

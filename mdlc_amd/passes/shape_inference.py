@@ -113,7 +113,8 @@ def node_output_infos(node: Node, shape_of, dtype_of, const_of) -> list:
         m = sa[1] if a.get("transA", 0) else sa[0]
         nn = sb[0] if a.get("transB", 0) else sb[1]
         if op == "QGemm":
-            return [((m, nn), DType.FLOAT32 if a.get("out_dtype") == "float32" else DType.INT8)]
+            od = a.get("out_dtype", "int8")
+            return [((m, nn), {"float32": DType.FLOAT32, "int32": DType.INT32}.get(od, DType.INT8))]
         return [((m, nn), d0)]
     if op == "MatMul":
         sa, sb = shape_of(ins[0]), shape_of(ins[1])

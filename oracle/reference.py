@@ -221,6 +221,8 @@ class ReferenceExecutor:
             return [quant.qadd(ins[0], q, a["res_mult"], a["acc_mult"])]
         if op == "QGemm":
             acc = quant.gemm_acc(ins[0], ins[1], opt(2))
+            if a.get("out_dtype", "int8") == "int32":
+                return [acc]
             if a.get("out_dtype", "int8") == "float32":
                 return [acc.astype(np.float32) * ins[3].astype(np.float32)[None, :]]
             lo = 0 if a.get("activation") == "Relu" else quant.QMIN

@@ -96,7 +96,10 @@ QSCHEDULES = [MfmaSchedule(256, 256, 128, 4, 2, 32, True),   # two register sets
               MfmaSchedule(256, 256, 64, 2, 2, 32, True),    # 256 accumulators, one set
               MfmaSchedule(128, 64, 128, 2, 1, 16, True),
               MfmaSchedule(32, 32, 64, 1, 1, 32, True),
-              MfmaSchedule(128, 128, 256, 2, 2, 16, False)]  # single LDS buffer, 256-byte K tiles
+              MfmaSchedule(128, 128, 256, 2, 2, 16, False),  # single LDS buffer, 256-byte K tiles
+              MfmaSchedule(256, 256, 128, 2, 2, 32, True, 1, False, 2),   # interleaved pipeline
+              MfmaSchedule(128, 64, 64, 2, 2, 16, True, 1, False, 2),
+              MfmaSchedule(256, 256, 128, 4, 4, 16, True)]     # 16 waves
 
 
 @pytest.mark.parametrize("sched", QSCHEDULES, ids=lambda s: s.key())
@@ -119,7 +122,7 @@ def test_qconv_gather_widths_and_tiles(case, sched, hip_ctx):
                                    MfmaSchedule(128, 128, 64, 2, 2, 32, True),
                                    MfmaSchedule(32, 64, 64, 1, 2, 32, True)] + QSCHEDULES[:2],
                          ids=lambda s: "default" if s is None else s.key())
-@pytest.mark.parametrize("out", ["int8", "float32"])
+@pytest.mark.parametrize("out", ["int8", "float32", "int32"])
 def test_qgemm_bit_exact(sched, out, hip_ctx):
     rng = np.random.default_rng(3)
     M, N, K = 77, 130, 384
@@ -337,9 +340,40 @@ def test_qconv_fused_epilogues(case, oc, sched, hip_ctx):
     np.testing.assert_array_equal(got["z"], got2["z"])
 
 
+@pytest.mark.parametrize("sched", [None, QSCHEDULES[0], QSCHEDULES[5], QSCHEDULES[7]],
+                         ids=lambda s: "default" if s is None else s.key())
+def test_qgemm_int32_accumulators_exact(sched, hip_ctx):
+    """The raw int32 accumulators (out_dtype int32: acc + bias, no requant)
+    at K = 4096, with rows and columns of +-127 codes so that |acc| reaches
+    127 * 127 * 4096 = 66e6 > 2^24 (where a float32 route would round),
+    equal the exact int64 product."""
+    rng = np.random.default_rng(21)
+    M, N, K = 300, 260, 4096
+    x = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    x[:3] = 127
+    x[3] = -127
+    w[:2] = 127
+    w[5] = -127
+    bias = rng.integers(-2 ** 20, 2 ** 20, N).astype(np.int32)
+    b = GraphBuilder("qacc")
+    b.input("xq", (M, K), dtype="int8")
+    b.const("w", w)
+    b.const("b", bias)
+    b.const("m", np.ones(N, np.float32))
+    b.node("QGemm", ["xq", "w", "b", "m"], "y", transB=1, out_dtype="int32")
+    b.output("y")
+    _, got, want = device_run(b.graph(), {"xq": x}, ctx=hip_ctx,
+                              schedule_fn=None if sched is None else _Fixed(sched))
+    exact = x.astype(np.int64) @ w.astype(np.int64).T + bias
+    assert got["y"].dtype == np.int32 and np.abs(exact).max() > 2 ** 24
+    np.testing.assert_array_equal(want["y"], exact)
+    np.testing.assert_array_equal(got["y"], exact)
+
+
 def test_int8_gemm_4096_cube_rows_exact(hip_ctx):
-    """The compute-bound int8 shape (M = N = K = 4096): a sample of output
-    rows against an exact float64 product (|acc| < 2^53)."""
+    """The compute-bound int8 shape (M = N = K = 4096) with the shipped
+    schedule: every output against an exact float64 product (|acc| < 2^53)."""
     from mdlc_amd.codegen.hip.hip_executor import HipExecutor
     from mdlc_amd.compiler import compile_graph
 
@@ -362,11 +396,11 @@ def test_int8_gemm_4096_cube_rows_exact(hip_ctx):
         y = ex.run({"xq": xq})["outputs"]["y"]
     finally:
         ex.close()
-    rows = rng.choice(M, 48, replace=False)
-    acc = (xq[rows].astype(np.float64) @ wq.T.astype(np.float64)).astype(np.int64) + bias
-    f = acc.astype(np.int32).astype(np.float32) * mult
-    want = np.clip(np.rint(f), -127, 127).astype(np.int8)
-    np.testing.assert_array_equal(y[rows], want)
+    for r0 in range(0, M, 1024):                   # all rows, 1024 at a time
+        acc = (xq[r0:r0 + 1024].astype(np.float64) @ wq.T.astype(np.float64)).astype(np.int64) + bias
+        f = acc.astype(np.int32).astype(np.float32) * mult
+        want = np.clip(np.rint(f), -127, 127).astype(np.int8)
+        np.testing.assert_array_equal(y[r0:r0 + 1024], want)
 
 
 @pytest.mark.parametrize("case", [(2, 3, 31, 24, 3, 2, "lut"), (1, 3, 16, 24, 3, 2, None),
