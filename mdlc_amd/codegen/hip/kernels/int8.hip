@@ -408,13 +408,7 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
   static_assert(!PIPE || DB, "the interleaved pipeline needs two LDS buffers");
   intx4 ra0[A_PT], rb0[B_PT], ra1[kTwoSets && !PIPE ? A_PT : 1], rb1[kTwoSets && !PIPE ? B_PT : 1];
   const int nk = (g.K + BK - 1) / BK;
-  // K tiles are visited from a per-tile starting tile, wrapping around:
-  // integer accumulation is exact in any order, and with every workgroup
-  // at a different K offset the rows the chip fetches at one time (K bytes
-  // apart: 4096 for a 4096-deep GEMM) stop landing on the same memory
-  // channels. Indices past the last tile stay past it (they load zeros).
-  const int krot = (mt * tiles_n + nt) % nk;
-  auto kofs = [&](int kt) -> int { return (kt < nk ? (kt + krot) % nk : kt) * BK; };
+  auto kofs = [&](int kt) -> int { return kt * BK; };   // byte offset of K tile kt
   if constexpr (PIPE) {
     // Interleaved pipeline (double-buffered LDS, one register set for the
     // global staging): within one K tile the fragments of sub-step s + 1
