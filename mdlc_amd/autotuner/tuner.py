@@ -34,6 +34,7 @@ CLOCK_GHZ = 2.4
 HBM_GBS = 8000.0
 LAUNCH_US = 2.0
 L2_CU_GBS = 150.0                    # one CU's L2 -> L1 read rate (64 B/clk)
+LDS_B_PER_CLK = 64.0                 # LDS bytes per clock a CU sustains (128-bit accesses)
 SPLITS = (1, 2, 3, 4, 5, 6, 8, 12, 16, 24, 32)
 
 
@@ -46,6 +47,8 @@ def analytical_cost(sched: MfmaSchedule, M: int, N: int, K: int) -> float:
       last round.
     * Compute per round: the tile's MFMA flops at the per-CU rate, derated
       when fewer than 2 waves per SIMD are resident (no one to hide latency).
+    * LDS: the tile writes plus every wave's fragment reads per K step, at
+      the rate a CU sustains; partly overlapped with the MFMAs.
     * Memory: A re-read once per column tile and B once per row tile, at
       HBM bandwidth, overlapped with compute.
     * Split-K adds the workspace round trip and a second launch.
@@ -75,9 +78,15 @@ def analytical_cost(sched: MfmaSchedule, M: int, N: int, K: int) -> float:
     wg_flops = 2.0 * sched.BM * sched.BN * kp
     round_us = wg_flops * per_cu / (MFMA_FLOPS_PER_CU_CLK * CLOCK_GHZ * 1e3) / eff
     compute = rounds * round_us
+    # LDS: each K step writes the A and B tiles once and every wave reads
+    # its WM rows of A and WN columns of B; at the ~64 B/clk a CU sustains
+    # for 128-bit reads this rivals the MFMA time for small wave tiles
+    wm, wn = sched.wave_tile()
+    lds_step = 4.0 * sched.BK * ((sched.BM + sched.BN) + waves * (wm + wn))
+    lds = rounds * per_cu * lds_step * (kp // sched.BK) / (LDS_B_PER_CLK * CLOCK_GHZ * 1e3)
     traffic = 4.0 * (-(-N // sched.BN) * M * K + -(-M // sched.BM) * K * N)
     memory = traffic / (HBM_GBS * 1e3)
-    t = max(compute, memory) + LAUNCH_US
+    t = max(compute, lds, memory) + 0.3 * min(compute, lds) + LAUNCH_US
     if slices > 1:
         t += 4.0 * (slices + 1) * M * N / (HBM_GBS * 1e3) + LAUNCH_US
     return t
@@ -196,6 +205,16 @@ def candidates(M: int, N: int, K: int, *, budget: int = 24, seed: int = 0, extra
     d = default_schedule(M, N, K)
     if d not in pick:
         pick.append(d)
+    # the model's best form of every large-wave-tile layout (wave tile of at
+    # least 32 x 64: fewer LDS bytes per flop), so that those are measured
+    # even where the model ranks small tiles first
+    seen = {(s.BM, s.BN, s.WGM, s.WGN, s.MS) for s in pick}
+    for s in ranked:
+        wm, wn = s.wave_tile()
+        key = (s.BM, s.BN, s.WGM, s.WGN, s.MS)
+        if wm * wn >= 2048 and s.BK >= 16 and key not in seen and len(seen) < budget + 24:
+            seen.add(key)
+            pick.append(s)
     uneven = [s for s in pick if s.SK == 1 and _tiles(s, M, N) > CUS and _tiles(s, M, N) % CUS]
     pick += [s.with_stream_k() for s in uneven[:stream_k]]
     pick += [s.with_unroll(2) for s in [s for s in pick if s.DB and s.UN == 1][:unroll]]

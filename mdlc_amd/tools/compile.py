@@ -58,6 +58,8 @@ def main(argv=None) -> int:
                     help="accepted for compatibility: structural verification always runs after "
                          "each pass; numerical verification needs the test oracle")
     ap.add_argument("--run", action="store_true", help="run one forward on the device and time it")
+    ap.add_argument("--save-outputs", default="", metavar="NPZ",
+                    help="with --run: write the graph outputs (and the feeds) to an .npz file")
     args = ap.parse_args(argv)
 
     from mdlc_amd.compiler import compile_graph, compile_onnx
@@ -111,6 +113,12 @@ def main(argv=None) -> int:
             ex.close()
         shapes = ", ".join(f"{k}{tuple(v.shape)}" for k, v in res["outputs"].items())
         print(f"\nran on the device: {res['ms']:.3f} ms ({shapes})")
+        if args.save_outputs:
+            import numpy as np
+
+            np.savez(args.save_outputs, **{f"out:{k}": v for k, v in res["outputs"].items()},
+                     **{f"in:{k}": np.asarray(v) for k, v in feeds.items()})
+            print(f"wrote outputs and feeds to {args.save_outputs}")
     return 0
 
 

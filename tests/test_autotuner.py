@@ -5,6 +5,8 @@ from __future__ import annotations
 
 import os
 
+import pytest
+
 from mdlc_amd.autotuner import AutotuneCache, Tuner, analytical_cost, tune_gemm
 from mdlc_amd.autotuner.tuner import TUNED_PATH, candidates, problem_key
 from mdlc_amd.codegen.schedule import (
@@ -107,3 +109,24 @@ def test_shipped_tuned_schedules_are_valid():
         for p in model_problems(model, batch, "implicit"):
             assert problem_key(p) in cache.entries, (model, batch, problem_key(p))
     assert DEFAULT_GEMM.is_valid() and DEFAULT_GEMM.conv_valid()
+
+
+@pytest.mark.gpu
+def test_measured_tuning_picks_a_correct_schedule(hip_ctx):
+    """The measured tuner on one small convolution: every candidate is timed
+    on the device and checked against the default schedule's output, and
+    the chosen schedule's module matches the oracle."""
+    from gpu_util import assert_close, device_run
+    from mdlc_amd.autotuner.tuner import _problem_graph, tune_problem
+
+    problem = {"kind": "conv", "mode": "implicit", "M": 32, "N": 2 * 14 * 14, "K": 16 * 9,
+               "batch": 2, "bias": False, "act": None, "C": 16, "H": 14, "W": 14, "KH": 3, "KW": 3,
+               "SH": 1, "SW": 1, "DH": 1, "DW": 1, "PT": 1, "PB": 1, "PL": 1, "PR": 1, "OH": 14, "OW": 14}
+    res = tune_problem(problem, budget=4, ctx=hip_ctx)
+    assert res.measured and res.n_evaluated >= 4 and res.rejected == []
+    assert all(ms > 0 for _, ms in res.ranking)
+    assert res.best.conv_valid()
+    g, feeds = _problem_graph(problem)
+    _, got, want = device_run(g, feeds, ctx=hip_ctx, schedule_fn=lambda n, mnk: res.best,
+                              small_conv=False)
+    assert_close("y", got["y"], want["y"])

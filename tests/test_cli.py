@@ -50,6 +50,23 @@ def test_unknown_model_name():
 
 
 @pytest.mark.gpu
-def test_run_on_the_device(capsys):
-    assert cli.main(["micro:49x512x4608", "--run"]) == 0
+@pytest.mark.parametrize("model", ["micro:49x512x4608", "resnet18"])
+def test_run_on_the_device_matches_the_oracle(model, tmp_path, capsys):
+    """``--run`` compiles, runs on the device and writes the outputs, which
+    match the oracle on the same feeds (network tier for the whole model)."""
+    import numpy as np
+
+    from mdlc_amd.compiler import compile_graph
+    from mdlc_amd.testing import FP32_NETWORK, compare_arrays
+    from oracle.reference import run_reference
+
+    path = tmp_path / "out.npz"
+    assert cli.main([model, "--run", "--save-outputs", str(path)]) == 0
     assert "ran on the device" in capsys.readouterr().out
+    saved = np.load(path)
+    feeds = {k[3:]: saved[k] for k in saved.files if k.startswith("in:")}
+    graph, _ = cli.build_model(model, 1)
+    want = run_reference(compile_graph(graph, feeds=feeds).graph, feeds)
+    for name, ref in want.items():
+        r = compare_arrays(name, saved[f"out:{name}"], ref, rtol=FP32_NETWORK.rtol, atol=FP32_NETWORK.atol)
+        assert r.ok, str(r)

@@ -13,6 +13,7 @@ import pytest
 
 from mdlc_amd.codegen.hip import hiprtc_runtime as R
 from mdlc_amd.codegen.hip.hip_executor import HipExecutor
+from mdlc_amd.codegen.schedule import MfmaSchedule
 from mdlc_amd.compiler import compile_graph
 from mdlc_amd.tools.build_resnet18 import build_resnet18, make_input
 from mdlc_amd.tools.micro_gemm import build_micro_gemm
@@ -50,7 +51,7 @@ def test_static_scratch_matches_the_arena_workspace(hip_ctx):
 
     # second call, smaller: one micro GEMM with a split-K workspace
     g, feeds = build_micro_gemm(784, 128, 1152)
-    c2 = compile_graph(g, feeds=feeds)
+    c2 = compile_graph(g, feeds=feeds, schedule_fn=lambda n, mnk: MfmaSchedule(64, 64, 16, 2, 2, 32, True, 4))
     assert "splitk_reduce" in {l.kind for l in c2.module.plan}
     (ca, ea), (cs, es) = _both(c2, feeds, hip_ctx)
     np.testing.assert_array_equal(cs["C"], ca["C"])
@@ -66,8 +67,9 @@ def test_static_scratch_limits_are_host_errors(hip_ctx):
     # ... and by the entry point itself, before any launch; a plan without a
     # workspace of its own is refused by the arena runner
     g, feeds = build_micro_gemm(784, 128, 1152)
-    c2 = compile_graph(g, feeds=feeds)
+    c2 = compile_graph(g, feeds=feeds, schedule_fn=lambda n, mnk: MfmaSchedule(64, 64, 16, 2, 2, 32, True, 4))
     ex = HipExecutor(c2.module, hip_ctx, static_scratch=True)
+    assert ex.ws_bytes > 0
     try:
         recs = ex.launch_records
         big = R.Plan(recs, (0, R.STATIC_SCRATCH_BYTES + 256))
