@@ -259,7 +259,7 @@ def compile_network(args, name: str, batch: int):
     t0 = time.perf_counter()
     folds = dict(fuse_residual=False, fuse_int8_epilogues=False) if args.no_fold else {}
     c = compile_graph(build(batch=batch), feeds={"input": x}, conv_mode=args.conv_mode,
-                      schedule_fn=schedule_source(args), **folds)
+                      schedule_fn=schedule_source(args), winograd=args.winograd, **folds)
     log(f"{name} b={batch}: compiled in {time.perf_counter() - t0:.1f} s, {len(c.module.plan)} launches")
     return c, {"input": x}
 
@@ -432,6 +432,8 @@ def main(argv=None) -> int:
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--size", type=int, default=4096, help="int8_gemm M = N = K")
     ap.add_argument("--conv-mode", default="implicit", choices=["implicit", "im2col"])
+    ap.add_argument("--winograd", action="store_true",
+                    help="3x3 stride-1 convs as Winograd F(2x2, 3x3)")
     ap.add_argument("--schedules", default="", help="tuner JSON cache to use instead of the "
                     "shipped mdlc_amd/autotuner/tuned_gfx950.json")
     ap.add_argument("--graph", action="store_true", help="replay the plan as a hipGraph")
@@ -462,7 +464,8 @@ def main(argv=None) -> int:
             part["cpu_baseline"] = base
         line = full_line(args, part, scaling="weak", data=data_text(w),
                          config={"batch": args.batch, "image": [3, 224, 224],
-                                 "conv_mode": args.conv_mode, "backend_folds": not args.no_fold})
+                                 "conv_mode": args.conv_mode, "winograd": args.winograd,
+                                 "backend_folds": not args.no_fold})
         if w == "resnet18" and args.batch == 32 and not args.no_secondary:
             line["config"]["secondary"] = secondary(args)
     print(json.dumps(line), flush=True)

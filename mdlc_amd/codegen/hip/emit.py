@@ -12,6 +12,7 @@ extended because nothing runs on the host here:
   gemm_ws     dense GEMM with the K range split over the waves of a workgroup
               (small M x N, deep K: one launch, no split-K workspace)
   conv        implicit-GEMM convolution (no column buffer)
+  wino        3x3 stride-1 convolution by Winograd F(2x2, 3x3), transforms fused
   gconv       grouped convolution: the implicit GEMM with one grid row per group
   conv_smallc direct convolution for few input channels (stems): input patch
               in LDS, weights in registers, matrix cores
@@ -45,8 +46,9 @@ import numpy as np
 from mdlc_amd.codegen.hip import templates as T
 from mdlc_amd.codegen.hip.emit_int8 import Int8LoweringMixin
 from mdlc_amd.codegen.hip.plan import LIBRARY_PARTS, QUANT_OPS, HipModule, Launch, round4, round16  # noqa: F401
-from mdlc_amd.codegen.schedule import (MfmaSchedule, default_schedule, smallc_fits, smallc_pairs,
-                                      smallc_tile, split_slices)
+from mdlc_amd.codegen.schedule import (WINO_BK, WINO_BM, WINO_BN, MfmaSchedule, default_schedule,
+                                      smallc_fits, smallc_pairs, smallc_tile, split_slices, wino_fits,
+                                      wino_patch, wino_slices)
 from mdlc_amd.ir import DType, Graph, Node
 from mdlc_amd.passes.fuse_elementwise import ELEMENTWISE
 from mdlc_amd.passes.shape_inference import conv_geometry
@@ -69,11 +71,13 @@ def dw_rows_per_thread(oh: int) -> int:
 
 class HipCodegen(Int8LoweringMixin):
     def __init__(self, schedule_fn: Optional[ScheduleFn] = None, *, conv_mode: str = "implicit",
-                 int8_depthwise: str = "mfma", small_conv: bool = True) -> None:
+                 int8_depthwise: str = "mfma", small_conv: bool = True,
+                 winograd: bool = False) -> None:
         """``int8_depthwise``: "mfma" runs 16-channel-aligned int8 depthwise
         convs as block-diagonal GEMMs on the matrix cores, "vector" keeps
         them on the per-pixel vector kernel. ``small_conv``: convs with few
-        input channels take the direct kernel (implicit mode)."""
+        input channels take the direct kernel (implicit mode). ``winograd``:
+        3x3 stride-1 convs run as Winograd F(2x2, 3x3) (implicit mode)."""
         if conv_mode not in ("implicit", "im2col"):
             raise ValueError(f"conv_mode must be 'implicit' or 'im2col', not {conv_mode!r}")
         if int8_depthwise not in ("mfma", "vector"):
@@ -86,6 +90,7 @@ class HipCodegen(Int8LoweringMixin):
         self.schedule_fn = schedule_fn
         self.conv_mode = conv_mode
         self.small_conv = small_conv
+        self.winograd = winograd
         self.kernels: dict = {}
         self.plan: list = []
         self.scratch: dict = {}
@@ -204,6 +209,10 @@ class HipCodegen(Int8LoweringMixin):
                                                         geo["DW"]):
             self._lower_conv_smallc(g, node, geo, has_bias)
             return
+        if (self.conv_mode == "implicit" and self.winograd and wino_fits(geo)
+                and geo["N"] * geo["C"] * geo["H"] * geo["W"] < 2 ** 31):
+            self._lower_wino(g, node, geo, has_bias)
+            return
         OC, K = geo["OC"], geo["C"] * geo["KH"] * geo["KW"]
         OH, OW, N = geo["OH"], geo["OW"], geo["N"]
         P = N * OH * OW
@@ -313,6 +322,74 @@ class HipCodegen(Int8LoweringMixin):
              "flops": 2 * OC * P * K,
              "bytes": 4 * (N * C * geo["H"] * geo["W"] + OC * K + P * OC * (1 + len(extra))
                            + (OC if has_bias else 0))}))
+
+    def _lower_wino(self, g: Graph, node: Node, geo: dict, has_bias: bool) -> None:
+        """3x3 stride-1 conv as Winograd F(2x2, 3x3): the filters are
+        transformed here (``wino_filter_transform``), the input and output
+        transforms run inside the kernel. Grids too small for the chip split
+        the channel sum over ``wino_slices`` slices, added by the split-K
+        reduce, which then applies bias, activation and residual."""
+        N, C, H, W = geo["N"], geo["C"], geo["H"], geo["W"]
+        OC, OH, OW = geo["OC"], geo["OH"], geo["OW"]
+        TH, TW = -(-OH // 2), -(-OW // 2)
+        tiles = N * TH * TW
+        chunks = -(-C // WINO_BK)
+        nchunk = -(-chunks // wino_slices(OC, tiles, C))
+        slices = -(-chunks // nchunk)              # no empty slice
+        CP, OCP = slices * nchunk * WINO_BK, -(-OC // WINO_BM) * WINO_BM
+        w, x, y = node.inputs[1], node.inputs[0], node.outputs[0]
+        u = wino_pack_filters(wino_filter_transform(np.asarray(g.initializers[w])), OCP, CP)
+        udev = self._pack(f"{w}__dev_wino", u)
+        a = node.attrs
+        act = a.get("activation")
+        epi = dict(act_sig=self._act_sig(a), attrs=self._act_attrs(a), **self._residual_epilogue(g, node))
+        residual, res = epi["residual"], epi["res_input"]
+        bias = [node.inputs[2]] if has_bias else []
+        extra = [res] if res else []
+        P = N * OH * OW
+        split = slices > 1
+        grid = (-(-OC // WINO_BM) * -(-tiles // WINO_BN), slices, 1)
+        meta = {"N": N, "C": C, "H": H, "W": W, "OC": OC, "OH": OH, "OW": OW, "TH": TH, "TW": TW,
+                "CP": CP, "OCP": OCP, "PT": geo["PT"], "PL": geo["PL"], "nchunk": nchunk,
+                "node": node, "ksplit": slices, "out_4d": (N, OC, OH, OW),
+                # the multiply-adds this algorithm performs (16 per tile, channel
+                # pair), and those of the direct convolution it replaces
+                "flops": 2 * 16 * OC * C * tiles, "direct_flops": 2 * 9 * OC * C * P,
+                "bytes": 4 * (N * C * H * W + 16 * OC * C + OC * P)}
+        rtag = "_res" if residual and not split else ""
+        ploads = -(-wino_patch(N, H, W, geo["PT"], OH, OW)[0] // 64)
+        meta["ploads"] = ploads
+        sig = ("wino", split, ploads, bool(bias) and not split, None if split else epi["act_sig"],
+               None if split else residual)
+        kname = self._kernel(sig, lambda i: T.wino_kernel(
+            f"conv_wino{'_SK' if split else ''}_P{ploads}_{'none' if split else act or 'none'}{rtag}_{i}",
+            split=split, ploads=ploads, with_bias=bool(bias), activation=act, attrs=epi["attrs"],
+            residual=residual))
+        if not split:
+            if res:
+                meta["bytes"] += 4 * OC * P
+            if bias:
+                meta["bytes"] += 4 * OC
+            self.plan.append(Launch("wino", kname, [udev, x] + bias + extra, [y], grid, (512, 1, 1),
+                                    meta))
+            return
+        ws = y + "__splitk"
+        self.scratch[ws] = (slices * OC, P)
+        self.scratch_class[ws] = "splitk"
+        meta["bytes"] += 4 * (slices - 1) * OC * P
+        self.plan.append(Launch("wino", kname, [udev, x], [ws], grid, (512, 1, 1),
+                                dict(meta, partial=True)))
+        vec = REDUCE_VEC if P % 4 == 0 and (OH * OW) % 4 == 0 else 1
+        rsig = ("splitk_reduce", bool(bias), "row", epi["act_sig"], 1.0, 1.0, residual, vec)
+        rname = self._kernel(rsig, lambda i: T.splitk_reduce_kernel(
+            f"splitk_reduce{'4' if vec == 4 else ''}_{act or 'none'}_row{'_res' if residual else ''}_{i}",
+            with_bias=bool(bias), bias_mode="row", activation=act, attrs=epi["attrs"],
+            residual=residual, vec=vec))
+        self.plan.append(Launch(
+            "splitk_reduce", rname, [ws] + bias + extra, [y], (-(-(OC * P) // (256 * vec)), 1, 1),
+            (256, 1, 1),
+            {"S": slices, "M": OC, "N": P, "ldc": 0, "hw": OH * OW, "node": node,
+             "bytes": 4 * (slices + 1 + len(extra)) * OC * P}))
 
     def _lower_conv_smallc(self, g: Graph, node: Node, geo: dict, has_bias: bool) -> None:
         """A conv with few input channels (a network's stem): the direct
@@ -762,8 +839,33 @@ class HipCodegen(Int8LoweringMixin):
             off += s[ax]
 
 
+_WINO_G = np.array([[1.0, 0.0, 0.0], [0.5, 0.5, 0.5], [0.5, -0.5, 0.5], [0.0, 0.0, 1.0]])
+
+
+def wino_filter_transform(w: np.ndarray) -> np.ndarray:
+    """[OC][C][3][3] filters -> U[16][OC][C] float32, U[4a + b] = (G g G^T)[a][b],
+    computed in float64 and rounded once."""
+    w = np.asarray(w, np.float64)
+    u = np.einsum("ai,ocij,bj->aboc", _WINO_G, w, _WINO_G)
+    return u.reshape(16, w.shape[0], w.shape[1]).astype(np.float32)
+
+
+def wino_pack_filters(u: np.ndarray, OCP: int, CP: int) -> np.ndarray:
+    """U[16][OC][C] -> the Winograd kernel's LDS images, [OCP/64][CP/8][16][64][8]
+    (zero padded): one contiguous 32 KB block per (64-channel output block,
+    8-channel chunk), row oc's two 4-channel halves swapped when bits 2 and 3
+    of oc differ."""
+    full = np.zeros((16, OCP, CP), np.float32)
+    full[:, :u.shape[1], :u.shape[2]] = u
+    img = full.reshape(16, OCP // 64, 64, CP // 8, 2, 4).transpose(1, 3, 0, 2, 4, 5).copy()
+    rows = np.arange(64)
+    swap = (((rows >> 2) ^ (rows >> 3)) & 1).astype(bool)
+    img[:, :, :, swap] = img[:, :, :, swap][:, :, :, :, ::-1]
+    return np.ascontiguousarray(img)
+
+
 def emit_hip_module(graph: Graph, schedule_fn: Optional[ScheduleFn] = None, *,
                     conv_mode: str = "implicit", int8_depthwise: str = "mfma",
-                    small_conv: bool = True) -> HipModule:
+                    small_conv: bool = True, winograd: bool = False) -> HipModule:
     return HipCodegen(schedule_fn, conv_mode=conv_mode, int8_depthwise=int8_depthwise,
-                      small_conv=small_conv).lower(graph)
+                      small_conv=small_conv, winograd=winograd).lower(graph)

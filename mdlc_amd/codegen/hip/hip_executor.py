@@ -155,6 +155,10 @@ class HipExecutor:
             args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
             args += [I(m[f]) for f in ("M", "N", "K", "lda", "Cin", "H", "W", "OH", "OW", "ksplit",
                                        "kchunk", "ximg", "cimg")]
+        elif k == "wino":
+            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+            args += [I(m[f]) for f in ("N", "C", "H", "W", "OC", "OH", "OW", "TH", "TW", "CP", "OCP",
+                                       "PT", "PL", "nchunk")]
         elif k == "conv_smallc":
             args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
             args += [I(m[f]) for f in ("batch", "H", "W", "OC", "OH", "OW")]

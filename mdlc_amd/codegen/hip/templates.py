@@ -284,6 +284,34 @@ def conv_smallc_kernel(name: str, win: tuple, tile: tuple, *, with_bias: bool,
         f"{'res' if residual else 'nullptr'}, y, N, H, W, OC, OH, OW);\n}}\n")
 
 
+def wino_kernel(name: str, *, split: bool, ploads: int, with_bias: bool,
+                activation: Optional[str], attrs: dict, residual: Optional[str] = None) -> tuple:
+    """3x3 stride-1 convolution by Winograd F(2x2, 3x3) on the matrix cores.
+    ABI: (U, x, [bias], [res], y, int N, int C, int H, int W, int OC, int OH,
+    int OW, int TH, int TW, int CP, int OCP, int PT, int PL, int nchunk) with
+    U the packed transformed filters; 512 threads, grid x = output
+    channel blocks of 64 x tile blocks of 64 (tiles fastest), grid y = the
+    channel slices. ``split``: y is the split-K workspace and the kernel
+    takes no bias or residual (``splitk_reduce_kernel`` finishes).
+    ``ploads``: input patch loads per lane and channel (``wino_patch``)."""
+    if split:
+        with_bias, residual, activation = False, None, None
+    epi = f"{name}_epi"
+    src = epilogue_struct(epi, bias_mode="row" if with_bias else None, activation=activation,
+                          attrs=attrs, residual=residual)
+    bias_arg = "const float* __restrict__ bias, " if with_bias else ""
+    res_arg = "const float* __restrict__ res, " if residual else ""
+    return name, src + (
+        f'extern "C" __global__ __launch_bounds__(512) void {name}(\n'
+        f"    const float* __restrict__ U, const float* __restrict__ x, {bias_arg}{res_arg}"
+        "float* __restrict__ y,\n    int N, int C, int H, int W, int OC, int OH, int OW, int TH, "
+        "int TW, int CP, int OCP,\n    int PT, int PL, int nchunk) {\n"
+        f"  mdlc::WinoArgs g{{U, x, {'bias' if with_bias else 'nullptr'}, "
+        f"{'res' if residual else 'nullptr'}, y, N, C, H, W, OC, OH, OW, TH, TW, CP, OCP, PT, PL, "
+        "nchunk};\n"
+        f"  mdlc::conv_wino_f32<{'true' if split else 'false'}, {int(ploads)}, {epi}>(g);\n}}\n")
+
+
 def im2col_kernel(name: str = "im2col") -> tuple:
     """ABI: the reference's (x, cols, C, H, W, KH, KW, OH, OW, SH, SW, PH, PW,
     DH, DW) plus trailing (N, ldc) for the batched column matrix."""

@@ -20,6 +20,8 @@ cross product of a few proven values, as in the reference.
 
 from __future__ import annotations
 
+import numpy as np
+
 from dataclasses import asdict, dataclass
 from typing import Iterator, Optional
 
@@ -370,3 +372,56 @@ def smallc_tile(N: int, OC: int, OH: int, OW: int) -> tuple:
 def smallc_lds_bytes(C: int, KH: int, KW: int, SH: int, SW: int, TR: int, TC: int) -> int:
     return 4 * C * ((TR - 1) * SH + KH) * ((TC - 1) * SW + KW)
 
+
+
+# ----- Winograd F(2x2, 3x3) convolution -------------------------------------
+
+WINO_BM = 64              # output channels per workgroup
+WINO_BN = 64              # 2x2 output tiles per workgroup
+WINO_BK = 8               # input channels per chunk
+WINO_MIN_CHUNKS = 4       # chunks each channel slice keeps at least
+
+
+WINO_PMAX = 704          # input patch floats per channel the kernel's LDS holds
+WINO_NSEG = 6            # images one workgroup's 64 tiles may touch
+
+
+def wino_patch(N: int, H: int, W: int, PT: int, OH: int, OW: int) -> tuple:
+    """(largest input patch in floats per channel, most images touched) over
+    the Winograd kernel's workgroups: for the 64 tiles t0..t0+63 (2x2 output
+    tiles in image-major raster order), the rows their 4x4 windows read in
+    each image, clamped to the image, all W columns (the kernel's own
+    segment computation)."""
+    TH, TW = -(-OH // 2), -(-OW // 2)
+    TT, P = TH * TW, N * TH * TW
+    t0 = np.arange(0, P, WINO_BN)
+    t1 = np.minimum(t0 + WINO_BN - 1, P - 1)
+    nf, nl = t0 // TT, t1 // TT
+    lo = np.maximum(0, 2 * ((t0 - nf * TT) // TW) - PT)
+    hi = np.minimum(H - 1, 2 * ((t1 - nl * TT) // TW) + 3 - PT)
+    rows = np.where(nf == nl, hi - lo + 1, (H - lo) + (nl - nf - 1) * H + hi + 1)
+    return int((rows * W).max()), int((nl - nf + 1).max())
+
+
+def wino_fits(geo: dict) -> bool:
+    """A plain 3x3 stride-1 undilated convolution whose workgroups' input
+    patches fit the kernel's LDS."""
+    if not (geo["group"] == 1 and geo["KH"] == 3 and geo["KW"] == 3 and geo["SH"] == 1
+            and geo["SW"] == 1 and geo["DH"] == 1 and geo["DW"] == 1):
+        return False
+    ps, segs = wino_patch(geo["N"], geo["H"], geo["W"], geo["PT"], geo["OH"], geo["OW"])
+    return ps <= WINO_PMAX and segs <= WINO_NSEG
+
+
+def wino_slices(OC: int, tiles: int, C: int) -> int:
+    """Channel slices of a Winograd convolution: one workgroup per CU runs
+    at a time (the LDS it stages), so grids under 1.5 workgroups per CU are
+    doubled by splitting the channel sum, as long as each slice keeps
+    WINO_MIN_CHUNKS chunks; each extra slice costs one more output-sized
+    workspace pass."""
+    blocks = -(-OC // WINO_BM) * -(-tiles // WINO_BN)
+    chunks = -(-C // WINO_BK)
+    s = 1
+    while blocks * s < CUS * 3 // 2 and chunks // (2 * s) >= WINO_MIN_CHUNKS:
+        s *= 2
+    return s

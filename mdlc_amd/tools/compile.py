@@ -52,6 +52,8 @@ def main(argv=None) -> int:
                     "gfx950 schedules when not tuning, a new cache file when tuning)")
     ap.add_argument("--budget", type=int, default=24, help="candidates measured per problem")
     ap.add_argument("--conv-mode", default="implicit", choices=["implicit", "im2col"])
+    ap.add_argument("--winograd", action="store_true",
+                    help="3x3 stride-1 convs as Winograd F(2x2, 3x3) (implicit mode)")
     ap.add_argument("--no-fold", action="store_true",
                     help="keep the reference's fused groups (no residual / int8 epilogue folds)")
     ap.add_argument("--no-verify", action="store_true",
@@ -75,7 +77,8 @@ def main(argv=None) -> int:
         tuner = Tuner(AutotuneCache(path), ctx=ctx, budget=args.budget, tune_misses=args.tune)
         schedule_fn = tuner
 
-    kw = dict(batch=args.batch, schedule_fn=schedule_fn, conv_mode=args.conv_mode)
+    kw = dict(batch=args.batch, schedule_fn=schedule_fn, conv_mode=args.conv_mode,
+              winograd=args.winograd)
     if args.no_fold:
         kw.update(fuse_residual=False, fuse_int8_epilogues=False)
     if args.model.endswith(".onnx"):

@@ -140,6 +140,33 @@ def test_mobilenetv2_b32_every_group(fold, oracle_b32, hip_ctx):
     _every_group_b32(c, feeds, want, hip_ctx)
 
 
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("fold", [True, False], ids=["residual_folded", "reference_groups"])
+def test_resnet18_b32_winograd_every_group(fold, oracle_b32, hip_ctx):
+    """The headline config with the 3x3 stride-1 convs on the Winograd
+    kernel (13 of the 20 convs, stages 2-4 with channel slices and their
+    reduce): every group in isolation within rtol 1e-4 / atol 1e-5."""
+    feeds, want = oracle_b32("resnet18")
+    c = compile_graph(build_resnet18(batch=32), feeds=feeds, fuse_residual=fold, winograd=True)
+    wino = [l for l in c.module.plan if l.kind == "wino"]
+    assert len(wino) == 13 and any(l.grid[1] > 1 for l in wino)
+    got = _every_group_b32(c, feeds, want, hip_ctx)
+    assert len(got) == (23 if fold else 32)
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_resnet18_winograd_every_group(batch, hip_ctx):
+    g = build_resnet18(batch=batch)
+    feeds = {"input": make_input(batch)}
+    c = compile_graph(g, feeds=feeds, winograd=True)
+    assert sum(l.kind == "wino" for l in c.module.plan) == 13
+    got, want, chained = _isolated(c, feeds, hip_ctx)
+    _report_ratios(got, want)
+    for t, v in got.items():
+        assert_close(t, v, want[t], DEVICE_TENSOR)
+    assert_close("logits", chained["logits"], want["logits"], FP32_NETWORK)
+
+
 def test_resnet18_batch32_rows_match_single_images(hip_ctx):
     """At the benchmark batch the oracle is too slow for every image, so the
     device's batch-32 logits are checked against the oracle on two images

@@ -1,0 +1,114 @@
+"""Host side of the Winograd F(2x2, 3x3) convolution, on the CPU.
+
+The filter transform the emitter packs is pinned by the algorithm's own
+identity: with the textbook input and output transforms (Lavin & Gray,
+"Fast Algorithms for Convolutional Neural Networks", 2016, F(2x2, 3x3)),
+A^T [U (.) (B^T d B)] A summed over channels must equal the direct
+correlation of the reference's Conv (mdlc/runtime/ops.py:56-81), to float64
+rounding, for every 4x4 window. A wrong G row, a swapped (a, b) position
+order or a transposed filter fails it. The emitter's choices (which convs,
+how many channel slices, padded layouts) are checked on the plan.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from mdlc_amd.codegen.hip.emit import wino_filter_transform
+from mdlc_amd.codegen.schedule import wino_slices
+from mdlc_amd.compiler import compile_graph
+from mdlc_amd.tools.graph_builder import GraphBuilder
+
+BT = np.array([[1, 0, -1, 0], [0, 1, 1, 0], [0, -1, 1, 0], [0, 1, 0, -1]], np.float64)
+AT = np.array([[1, 1, 1, 0], [0, 1, -1, -1]], np.float64)
+
+
+def _direct(x, w):
+    """Valid 3x3 correlation, float64: y[o, i, j] = sum_c,u,v w[o,c,u,v] x[c,i+u,j+v]."""
+    C, H, W = x.shape
+    y = np.zeros((w.shape[0], H - 2, W - 2))
+    for u in range(3):
+        for v in range(3):
+            y += np.einsum("oc,chw->ohw", w[:, :, u, v], x[:, u:u + H - 2, v:v + W - 2])
+    return y
+
+
+@pytest.mark.parametrize("oc,c", [(1, 1), (3, 5), (8, 16)])
+def test_filter_transform_reproduces_direct_conv(oc, c):
+    rng = np.random.default_rng(oc * 10 + c)
+    w = rng.standard_normal((oc, c, 3, 3))
+    x = rng.standard_normal((c, 8, 6))
+    u = wino_filter_transform(w.astype(np.float32)).astype(np.float64).reshape(4, 4, oc, c)
+    # recompute U in float64 so the identity is checked to float64 rounding;
+    # the packed float32 U must be that, rounded once
+    w32 = w.astype(np.float32).astype(np.float64)
+    G = np.array([[1, 0, 0], [0.5, 0.5, 0.5], [0.5, -0.5, 0.5], [0, 0, 1]])
+    u64 = np.einsum("ai,ocij,bj->aboc", G, w32, G)
+    assert np.array_equal(u, u64.astype(np.float32).astype(np.float64))
+    want = _direct(x, w32)
+    got = np.zeros_like(want)
+    for ty in range(3):
+        for tx in range(2):
+            d = x[:, 2 * ty:2 * ty + 4, 2 * tx:2 * tx + 4]                  # [c][4][4]
+            v = np.einsum("ai,cij,bj->abc", BT, d, BT)                       # B^T d B
+            m = np.einsum("aboc,abc->abo", u64, v)                           # sum over c
+            got[:, 2 * ty:2 * ty + 2, 2 * tx:2 * tx + 2] = np.einsum("ia,abo,jb->oij", AT, m, AT)
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-12 * max(1.0, np.abs(want).max()))
+
+
+def test_slices_fill_the_chip_without_starving_slices():
+    # ResNet-18 at batch 32: stage 1 fills the chip, later stages split
+    assert [wino_slices(oc, t, oc) for oc, t in
+            [(64, 25088), (128, 6272), (256, 1568), (512, 512)]] == [1, 2, 4, 8]
+    assert wino_slices(512, 16, 512) == 16                  # batch 1: 4 chunks per slice
+    assert wino_slices(64, 10, 24) == 1                      # too few chunks to split
+
+
+def _graph(c, oc, h, w, k=3, s=1, d=1, group=1):
+    rng = np.random.default_rng(0)
+    b = GraphBuilder("g")
+    b.input("x", (1, c, h, w))
+    b.const("w", rng.standard_normal((oc, c // group, k, k)).astype(np.float32))
+    p = d * (k // 2)
+    b.node("Conv", ["x", "w"], "y", kernel_shape=[k, k], strides=[s, s], dilations=[d, d],
+           pads=[p] * 4, group=group)
+    b.output("y")
+    return b.graph(), {"x": rng.standard_normal((1, c, h, w)).astype(np.float32)}
+
+
+@pytest.mark.parametrize("k,s,d,group,wino", [(3, 1, 1, 1, True), (3, 2, 1, 1, False),
+                                             (3, 1, 2, 1, False), (5, 1, 1, 1, False),
+                                             (3, 1, 1, 2, False)])
+def test_only_plain_3x3_stride1_convs_take_winograd(k, s, d, group, wino):
+    g, feeds = _graph(16, 16, 9, 9, k, s, d, group)
+    kinds = [l.kind for l in compile_graph(g, feeds=feeds, winograd=True).module.plan]
+    assert ("wino" in kinds) == wino, kinds
+    g, feeds = _graph(16, 16, 9, 9, k, s, d, group)
+    assert "wino" not in [l.kind for l in compile_graph(g, feeds=feeds).module.plan]
+
+
+def test_packed_filters_are_padded_to_whole_blocks_and_slices():
+    g, feeds = _graph(200, 130, 6, 10)
+    c = compile_graph(g, feeds=feeds, winograd=True)
+    (l,) = [l for l in c.module.plan if l.kind == "wino"]
+    m = l.meta
+    assert (m["OCP"], m["nchunk"], l.grid[1], m["CP"]) == (192, 7, 4, 224)
+    img = c.module.device_constants[l.inputs[0]]
+    assert img.shape == (3, 28, 16, 64, 2, 4)
+    # undo the half swap (rows whose bits 2 and 3 differ), then back to [16][OCP][CP]
+    img = img.copy()
+    rows = np.arange(64)
+    swap = (((rows >> 2) ^ (rows >> 3)) & 1).astype(bool)
+    img[:, :, :, swap] = img[:, :, :, swap][:, :, :, :, ::-1]
+    u = img.transpose(2, 0, 3, 1, 4, 5).reshape(16, 192, 224)
+    assert not u[:, 130:, :].any() and not u[:, :, 200:].any()
+    np.testing.assert_array_equal(u[:, :130, :200],
+                                  wino_filter_transform(c.graph.initializers["w"]))
+    # channels 4-7 of chunk 0 sit in the first half of rows 5 and 9, the second of row 13
+    img0 = c.module.device_constants[l.inputs[0]][0, 0, 3]
+    u0 = wino_filter_transform(c.graph.initializers["w"])[3]
+    for row, half in ((5, 0), (9, 0), (13, 1), (1, 1)):
+        np.testing.assert_array_equal(img0[row, half], u0[row, 4:8])
+    (r,) = [r for r in c.module.plan if r.kind == "splitk_reduce"]
+    assert r.meta["S"] == 4 and c.module.scratch_shapes[r.inputs[0]] == (4 * 130, 60)
