@@ -432,8 +432,8 @@ def main(argv=None) -> int:
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--size", type=int, default=4096, help="int8_gemm M = N = K")
     ap.add_argument("--conv-mode", default="implicit", choices=["implicit", "im2col"])
-    ap.add_argument("--winograd", action="store_true",
-                    help="3x3 stride-1 convs as Winograd F(2x2, 3x3)")
+    ap.add_argument("--no-winograd", dest="winograd", action="store_false",
+                    help="3x3 stride-1 convs on the implicit GEMM instead of Winograd F(2x2, 3x3)")
     ap.add_argument("--schedules", default="", help="tuner JSON cache to use instead of the "
                     "shipped mdlc_amd/autotuner/tuned_gfx950.json")
     ap.add_argument("--graph", action="store_true", help="replay the plan as a hipGraph")

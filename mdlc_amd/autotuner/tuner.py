@@ -320,7 +320,9 @@ def _compile_for(problem: dict, sched: Optional[MfmaSchedule]):
 
     g, feeds = _problem_graph(problem)
     fn = None if sched is None else (lambda node, mnk: sched)
-    c = compile_graph(g, feeds=feeds, schedule_fn=fn, conv_mode=problem.get("mode", "implicit"))
+    # the GEMM schedule is what is measured: convs stay on the implicit GEMM
+    c = compile_graph(g, feeds=feeds, schedule_fn=fn, conv_mode=problem.get("mode", "implicit"),
+                      winograd=False)
     return c, feeds
 
 

@@ -72,7 +72,7 @@ def dw_rows_per_thread(oh: int) -> int:
 class HipCodegen(Int8LoweringMixin):
     def __init__(self, schedule_fn: Optional[ScheduleFn] = None, *, conv_mode: str = "implicit",
                  int8_depthwise: str = "mfma", small_conv: bool = True,
-                 winograd: bool = False) -> None:
+                 winograd: bool = True) -> None:
         """``int8_depthwise``: "mfma" runs 16-channel-aligned int8 depthwise
         convs as block-diagonal GEMMs on the matrix cores, "vector" keeps
         them on the per-pixel vector kernel. ``small_conv``: convs with few
@@ -357,7 +357,7 @@ class HipCodegen(Int8LoweringMixin):
                 "flops": 2 * 16 * OC * C * tiles, "direct_flops": 2 * 9 * OC * C * P,
                 "bytes": 4 * (N * C * H * W + 16 * OC * C + OC * P)}
         rtag = "_res" if residual and not split else ""
-        ploads = -(-wino_patch(N, H, W, geo["PT"], OH, OW)[0] // 64)
+        ploads = -(-wino_patch(N, H, W, geo["PT"], OH, OW) // 64)
         meta["ploads"] = ploads
         sig = ("wino", split, ploads, bool(bias) and not split, None if split else epi["act_sig"],
                None if split else residual)
@@ -866,6 +866,6 @@ def wino_pack_filters(u: np.ndarray, OCP: int, CP: int) -> np.ndarray:
 
 def emit_hip_module(graph: Graph, schedule_fn: Optional[ScheduleFn] = None, *,
                     conv_mode: str = "implicit", int8_depthwise: str = "mfma",
-                    small_conv: bool = True, winograd: bool = False) -> HipModule:
+                    small_conv: bool = True, winograd: bool = True) -> HipModule:
     return HipCodegen(schedule_fn, conv_mode=conv_mode, int8_depthwise=int8_depthwise,
                       small_conv=small_conv, winograd=winograd).lower(graph)

@@ -41,9 +41,9 @@
 // the global loads of chunk c+2: half 0 the input windows (two (tile,
 // channel) windows a thread, transformed), half 1 the filter image, so each
 // SIMD has one wave with the heavy staging and one with the light. One
-// barrier per chunk. Window loads are branch free:
-// rows and columns outside the image are clamped to a valid address and
-// the value replaced by zero when the window is transformed.
+// barrier per chunk. The input reaches the windows through a per-wave LDS
+// patch of the rows the workgroup's tiles read, loaded with coalesced
+// loads, zeros at the padding; windows are then read without bounds checks.
 //
 // MFMA k order: in v_mfma_f32_32x32x2f32 lane l = 32*lk + li supplies
 // A[li][k] and B[k][li] for k = lk of the instruction's two; instruction q
@@ -76,7 +76,6 @@ constexpr int WINO_USTAGE = 16 * 64 * 8;              // floats
 constexpr int WINO_VSTAGE = 16 * 8 * WINO_VLD;
 constexpr int WINO_STAGE = WINO_USTAGE + WINO_VSTAGE; // 68 KB
 constexpr int WINO_PMAX = 704;                        // input patch floats per channel
-constexpr int WINO_NSEG = 6;                          // images one workgroup's tiles may touch
 
 // PL: patch loads per lane and channel, ceil(largest patch / 64) <= WINO_PMAX / 64.
 template <bool SPLIT, int PL, class Epi>
@@ -105,85 +104,68 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
 
   // ---- input patch: the rows the workgroup's windows read -----------------
   // For each image its 64 tiles touch (segment s = image nfirst + s), the
-  // rows the windows of those tiles read, clamped to the image, all columns;
-  // the segments stacked one after another. Segment s holds patch elements
-  // [pe[s], pe[s+1]); element e of it is channel c's x at c*HW + e + pd[s].
+  // rows its tiles' windows read (image coordinates, padding rows included),
+  // each WP = 2 TW + 2 columns wide starting at column -PL; positions outside
+  // the image hold zero, so windows are read without bounds checks. The
+  // segments are stacked: segment 0 holds rows rlo0 .. (its last), the
+  // others rows -PT .. (their last), whole images 2 TH + 2 rows.
   const int TT = g.TH * g.TW;
-  int pe[WINO_NSEG + 1], pd[WINO_NSEG];
-  {
-    const int pfirst = t0, plast = min(t0 + 63, P - 1);
-    const int nfirst = pfirst / TT, nlast = plast / TT;
-    const int lo0 = max(0, 2 * ((pfirst - nfirst * TT) / g.TW) - g.PT);
-    const int hil = min(g.H - 1, 2 * ((plast - nlast * TT) / g.TW) + 3 - g.PT);
-    int e = 0;
-#pragma unroll
-    for (int sg = 0; sg < WINO_NSEG; ++sg) {
-      const int n = nfirst + sg;
-      const int lo = sg == 0 ? lo0 : 0;
-      const int hi = n == nlast ? hil : g.H - 1;
-      pe[sg] = e;
-      pd[sg] = n * g.C * HW + lo * g.W - e;
-      e += n <= nlast ? (hi - lo + 1) * g.W : 0;
-    }
-    pe[WINO_NSEG] = e;
-  }
-  const int PS = pe[WINO_NSEG];                     // patch floats per channel (host: <= WINO_PMAX)
+  const int WP = 2 * g.TW + 2;
+  const int nfirst = t0 / TT;
+  const int plast = min(t0 + 63, P - 1);
+  const int nlast = plast / TT;
+  const int rlo0 = 2 * ((t0 - nfirst * TT) / g.TW) - g.PT;
+  const int rhil = 2 * ((plast - nlast * TT) / g.TW) + 3 - g.PT;
+  const int rows0 = (nlast == nfirst ? rhil : 2 * g.TH + 1 - g.PT) - rlo0 + 1;
+  const int seg = (2 * g.TH + 2) * WP;              // elements of a whole image's segment
+  const int PS = rows0 * WP + (nlast > nfirst ? (nlast - nfirst - 1) * seg + (rhil + g.PT + 1) * WP : 0);
 
   // ---- staging: half 0 transforms the input windows, each thread those of
   // tile t0 + lane for channels wq and wq + 4 of a chunk, read from its
   // wave's patch of the two channels; half 1 copies the filter image, eight
-  // 16-byte pieces a thread. Per lane: the window's patch offsets (row: the
-  // segment's start plus the clamped row, times W; column: clamped) and the
-  // mask of window positions inside the image (bit 4a + b), fixed across
-  // chunks.
+  // 16-byte pieces a thread.
   const int wq = wave & 3;
   const int lt = tid & 255;
-  int roff[4], coff[4], inside;
+  int wbase;                                        // the lane's window in the patch
   {
     const int p = t0 + lane;
-    const int pc = p < P ? p : t0;
+    const int pc = p < P ? p : t0;                  // tiles past the batch: any window, never stored
     const int n = pc / TT;
     const int r = pc - n * TT;
     const int ty = r / g.TW;
     const int tx = r - ty * g.TW;
-    const int iy0 = 2 * ty - g.PT, ix0 = 2 * tx - g.PL;
-    const int sg = n - t0 / TT;
-    int seg0 = 0;
-#pragma unroll
-    for (int k = 0; k < WINO_NSEG; ++k) seg0 = sg == k ? pe[k] : seg0;
-    const int lo = sg == 0 ? max(0, 2 * ((t0 - (t0 / TT) * TT) / g.TW) - g.PT) : 0;
-    int rows = 0, cols = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int iy = iy0 + q, ix = ix0 + q;
-      rows |= ((unsigned)iy < (unsigned)g.H) << q;
-      cols |= ((unsigned)ix < (unsigned)g.W) << q;
-      roff[q] = seg0 + (min(max(iy, 0), g.H - 1) - lo) * g.W;
-      coff[q] = min(max(ix, 0), g.W - 1);
-    }
-    inside = 0;
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) inside |= ((rows >> a) & (cols >> b) & 1) << (4 * a + b);
-    if (p >= P) inside = 0;
+    const int sg = n - nfirst;
+    wbase = (sg == 0 ? (2 * ty - g.PT - rlo0) * WP : rows0 * WP + (sg - 1) * seg + 2 * ty * WP) + 2 * tx;
   }
-
-  // registers of the chunk in flight: half 0 the two channels' patch
-  // elements lane + 64 i (i < PL), half 1 the filter image pieces. The
-  // elements' offsets from a channel's plane are fixed across chunks
-  // (elements past the patch read its first element, never used).
-  float4 ur[8];
-  float pv[2][PL];
+  // the lane's patch elements lane + 64 i: offset of the channel-0 value, or
+  // a zero (bit i of pzero) outside the image or past the patch
   int poff[PL];
+  unsigned pzero = 0;
 #pragma unroll
   for (int i = 0; i < PL; ++i) {
     const int e = i * 64 + lane;
-    int d = pd[0];
-#pragma unroll
-    for (int k = 1; k < WINO_NSEG; ++k) d = e >= pe[k] ? pd[k] : d;
-    poff[i] = e < PS ? e + d : pd[0];
+    int sg, row, col;
+    if (e < rows0 * WP) {
+      sg = 0;
+      row = rlo0 + e / WP;
+      col = e - (e / WP) * WP;
+    } else {
+      const int e1 = e - rows0 * WP;
+      sg = 1 + e1 / seg;
+      const int e2 = e1 - (e1 / seg) * seg;
+      row = e2 / WP - g.PT;
+      col = e2 - (e2 / WP) * WP;
+    }
+    const int ix = col - g.PL;
+    const bool ok = e < PS && (unsigned)row < (unsigned)g.H && (unsigned)ix < (unsigned)g.W;
+    poff[i] = ok ? (nfirst + sg) * g.C * HW + row * g.W + ix : 0;
+    pzero |= (ok ? 0u : 1u) << i;
   }
+
+  // registers of the chunk in flight: half 0 the two channels' patch
+  // elements, half 1 the filter image pieces
+  float4 ur[8];
+  float pv[2][PL];
   int held = chunk0;                                // chunk the patch registers hold
   float* pw = patch + wq * (2 * WINO_PMAX);
   auto load_x = [&](int chunk) {
@@ -196,42 +178,49 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
     }
   };
   auto store_x = [&](float* st) {
+    // the patch, zeros written with a bit mask (no select: it would branch)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int i = 0; i < PL; ++i) pw[j * WINO_PMAX + i * 64 + lane] = pv[j][i];
+      for (int i = 0; i < PL; ++i)
+        pw[j * WINO_PMAX + i * 64 + lane] =
+            __uint_as_float(__float_as_uint(pv[j][i]) & ((pzero >> i & 1u) - 1u));
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const bool cok = held * 8 + wq + 4 * j < g.C;
-      const float* pj = pw + j * WINO_PMAX;
-      // every read is issued, then positions outside the image (or past the
-      // last channel) are cleared with a bit mask: a select here becomes one
-      // branch and one exposed LDS latency per position
-      const unsigned cm = cok ? 0xffffffffu : 0u;
-      float d[16];
+      // V of channel wq + 4j; zero past the last channel (its filters are
+      // zero too, but the window would repeat the last channel's values)
+      float v[16];
+      if (held * 8 + wq + 4 * j < g.C) {
+        const float* pj = pw + j * WINO_PMAX + wbase;
+        float d[16];
 #pragma unroll
-      for (int a = 0; a < 4; ++a)
+        for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int b = 0; b < 4; ++b) d[4 * a + b] = pj[roff[a] + coff[b]];
+          for (int b = 0; b < 4; ++b) d[4 * a + b] = pj[a * WP + b];
+        float t[16];                                // t = B^T d, row by row
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        d[e] = __uint_as_float(__float_as_uint(d[e]) & (cm & (0u - ((unsigned)inside >> e & 1u))));
-      float t[16];                                  // t = B^T d, row by row
+        for (int b = 0; b < 4; ++b) {
+          t[b] = d[b] - d[8 + b];
+          t[4 + b] = d[4 + b] + d[8 + b];
+          t[8 + b] = d[8 + b] - d[4 + b];
+          t[12 + b] = d[4 + b] - d[12 + b];
+        }
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        t[b] = d[b] - d[8 + b];
-        t[4 + b] = d[4 + b] + d[8 + b];
-        t[8 + b] = d[8 + b] - d[4 + b];
-        t[12 + b] = d[4 + b] - d[12 + b];
+        for (int a = 0; a < 4; ++a) {               // V = t B
+          v[4 * a + 0] = t[4 * a] - t[4 * a + 2];
+          v[4 * a + 1] = t[4 * a + 1] + t[4 * a + 2];
+          v[4 * a + 2] = t[4 * a + 2] - t[4 * a + 1];
+          v[4 * a + 3] = t[4 * a + 1] - t[4 * a + 3];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = 0.f;
       }
-      float* v = st + WINO_USTAGE + (wq + 4 * j) * WINO_VLD + lane;
+      // all 16 values in their own registers before the stores, so a store
+      // waiting for the LDS does not hold up the transform of the next window
+      float* vs = st + WINO_USTAGE + (wq + 4 * j) * WINO_VLD + lane;
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {                 // V = t B; V[4a + b] at plane 4a + b
-        v[(4 * a + 0) * 8 * WINO_VLD] = t[4 * a] - t[4 * a + 2];
-        v[(4 * a + 1) * 8 * WINO_VLD] = t[4 * a + 1] + t[4 * a + 2];
-        v[(4 * a + 2) * 8 * WINO_VLD] = t[4 * a + 2] - t[4 * a + 1];
-        v[(4 * a + 3) * 8 * WINO_VLD] = t[4 * a + 1] - t[4 * a + 3];
-      }
+      for (int e = 0; e < 16; ++e) vs[e * 8 * WINO_VLD] = v[e];
     }
   };
   auto load_u = [&](int chunk) {

@@ -383,24 +383,26 @@ WINO_MIN_CHUNKS = 4       # chunks each channel slice keeps at least
 
 
 WINO_PMAX = 704          # input patch floats per channel the kernel's LDS holds
-WINO_NSEG = 6            # images one workgroup's 64 tiles may touch
 
 
-def wino_patch(N: int, H: int, W: int, PT: int, OH: int, OW: int) -> tuple:
-    """(largest input patch in floats per channel, most images touched) over
-    the Winograd kernel's workgroups: for the 64 tiles t0..t0+63 (2x2 output
-    tiles in image-major raster order), the rows their 4x4 windows read in
-    each image, clamped to the image, all W columns (the kernel's own
-    segment computation)."""
+def wino_patch(N: int, H: int, W: int, PT: int, OH: int, OW: int) -> int:
+    """Largest input patch (floats per channel) over the Winograd kernel's
+    workgroups: for the 64 tiles t0..t0+63 (2x2 output tiles in image-major
+    raster order), in each image they touch the rows their 4x4 windows read
+    (padding rows included), 2 TW + 2 columns wide (the kernel's own layout:
+    the first image from its first tile's row, whole images 2 TH + 2 rows,
+    the last up to its last tile's row)."""
     TH, TW = -(-OH // 2), -(-OW // 2)
     TT, P = TH * TW, N * TH * TW
+    WP = 2 * TW + 2
     t0 = np.arange(0, P, WINO_BN)
     t1 = np.minimum(t0 + WINO_BN - 1, P - 1)
     nf, nl = t0 // TT, t1 // TT
-    lo = np.maximum(0, 2 * ((t0 - nf * TT) // TW) - PT)
-    hi = np.minimum(H - 1, 2 * ((t1 - nl * TT) // TW) + 3 - PT)
-    rows = np.where(nf == nl, hi - lo + 1, (H - lo) + (nl - nf - 1) * H + hi + 1)
-    return int((rows * W).max()), int((nl - nf + 1).max())
+    rlo0 = 2 * ((t0 - nf * TT) // TW) - PT
+    rhil = 2 * ((t1 - nl * TT) // TW) + 3 - PT
+    rows0 = np.where(nl == nf, rhil, 2 * TH + 1 - PT) - rlo0 + 1
+    rows = rows0 + np.where(nl > nf, (nl - nf - 1) * (2 * TH + 2) + rhil + PT + 1, 0)
+    return int((rows * WP).max())
 
 
 def wino_fits(geo: dict) -> bool:
@@ -409,19 +411,22 @@ def wino_fits(geo: dict) -> bool:
     if not (geo["group"] == 1 and geo["KH"] == 3 and geo["KW"] == 3 and geo["SH"] == 1
             and geo["SW"] == 1 and geo["DH"] == 1 and geo["DW"] == 1):
         return False
-    ps, segs = wino_patch(geo["N"], geo["H"], geo["W"], geo["PT"], geo["OH"], geo["OW"])
-    return ps <= WINO_PMAX and segs <= WINO_NSEG
+    return wino_patch(geo["N"], geo["H"], geo["W"], geo["PT"], geo["OH"], geo["OW"]) <= WINO_PMAX
 
 
 def wino_slices(OC: int, tiles: int, C: int) -> int:
-    """Channel slices of a Winograd convolution: one workgroup per CU runs
-    at a time (the LDS it stages), so grids under 1.5 workgroups per CU are
-    doubled by splitting the channel sum, as long as each slice keeps
-    WINO_MIN_CHUNKS chunks; each extra slice costs one more output-sized
-    workspace pass."""
+    """Channel slices of a Winograd convolution. One workgroup runs per CU
+    (the LDS it stages), so the kernel takes about (rounds of workgroups) x
+    (chunks per slice) chunk times; the slice count minimising that wins,
+    the smallest on ties (each extra slice costs a workspace pass and the
+    reduce), with at least WINO_MIN_CHUNKS chunks per slice."""
     blocks = -(-OC // WINO_BM) * -(-tiles // WINO_BN)
     chunks = -(-C // WINO_BK)
+    best, best_cost = 1, None
     s = 1
-    while blocks * s < CUS * 3 // 2 and chunks // (2 * s) >= WINO_MIN_CHUNKS:
+    while s == 1 or -(-chunks // s) >= WINO_MIN_CHUNKS:
+        cost = -(-blocks * s // CUS) * -(-chunks // s)
+        if best_cost is None or cost < best_cost:
+            best, best_cost = s, cost
         s *= 2
-    return s
+    return best

@@ -52,8 +52,8 @@ def main(argv=None) -> int:
                     "gfx950 schedules when not tuning, a new cache file when tuning)")
     ap.add_argument("--budget", type=int, default=24, help="candidates measured per problem")
     ap.add_argument("--conv-mode", default="implicit", choices=["implicit", "im2col"])
-    ap.add_argument("--winograd", action="store_true",
-                    help="3x3 stride-1 convs as Winograd F(2x2, 3x3) (implicit mode)")
+    ap.add_argument("--no-winograd", dest="winograd", action="store_false",
+                    help="3x3 stride-1 convs on the implicit GEMM instead of Winograd F(2x2, 3x3)")
     ap.add_argument("--no-fold", action="store_true",
                     help="keep the reference's fused groups (no residual / int8 epilogue folds)")
     ap.add_argument("--no-verify", action="store_true",

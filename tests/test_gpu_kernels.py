@@ -138,17 +138,20 @@ CONV_CASES = [
 ]
 
 
-@pytest.mark.parametrize("mode", ["implicit", "im2col", "implicit-gemm"])
+@pytest.mark.parametrize("mode", ["implicit", "im2col", "implicit-gemm", "winograd"])
 @pytest.mark.parametrize("case", CONV_CASES, ids=lambda c: "x".join(map(str, c)))
 def test_conv_matches_oracle(case, mode, hip_ctx):
     """Implicit mode takes the direct small-channel kernel for C <= 4;
-    "implicit-gemm" keeps those convs on the implicit-GEMM gather."""
+    "implicit-gemm" keeps those convs on the implicit-GEMM gather; "winograd"
+    (the default) runs 3x3 stride-1 convs of more channels as Winograd."""
     g, feeds = _conv_graph(*case)
-    c, got, want = device_run(g, feeds, conv_mode=mode.split("-")[0], ctx=hip_ctx,
-                              small_conv=mode != "implicit-gemm")
+    c, got, want = device_run(g, feeds, conv_mode="im2col" if mode == "im2col" else "implicit",
+                              ctx=hip_ctx, small_conv=mode != "implicit-gemm",
+                              winograd=mode == "winograd")
     assert [n.op_type for n in c.graph.nodes] == ["FusedConvAct"]
     kinds = [l.kind for l in c.module.plan]
-    assert ("conv_smallc" in kinds) == (mode == "implicit" and case[1] <= 4)
+    assert ("conv_smallc" in kinds) == (mode in ("implicit", "winograd") and case[1] <= 4)
+    assert ("wino" in kinds) == (mode == "winograd" and case[1] > 4 and case[5] == 3 and case[6] == 1)
     assert_close("y", got["y"], want["y"])
 
 
@@ -238,7 +241,7 @@ def test_conv_split_k(case, sk, mode, hip_ctx):
     sched = MfmaSchedule(64, 64, 16, 2, 2, 32, True, sk)
     g, feeds = _conv_graph(*case)
     c = compile_graph(g, feeds=feeds, conv_mode=mode, schedule_fn=lambda n, mnk: sched,
-                      small_conv=False)
+                      small_conv=False, winograd=False)
     (launch,) = [l for l in c.module.plan if l.kind in ("conv", "gemm")]
     assert launch.meta["ksplit"] > 1 and launch.grid[0] % launch.meta["ksplit"] == 0
     assert [l.kind for l in c.module.plan][-1] == "splitk_reduce"
@@ -273,7 +276,7 @@ def test_conv_gather_schedules(case, sched, hip_ctx):
     assert sched.conv_valid()
     g, feeds = _conv_graph(*case)
     c, got, want = device_run(g, feeds, conv_mode="implicit", ctx=hip_ctx,
-                              schedule_fn=lambda n, mnk: sched, small_conv=False)
+                              schedule_fn=lambda n, mnk: sched, small_conv=False, winograd=False)
     (launch,) = [l for l in c.module.plan if l.kind == "conv"]
     assert launch.meta["k_order"] == ("tap" if case[1] % sched.BK == 0 else "channel")
     assert_close("y", got["y"], want["y"])
@@ -315,13 +318,13 @@ def test_conv_residual_epilogue(post, res_first, sk, mode, hip_ctx):
              else MfmaSchedule(64, 64, 16, 2, 2, 32, True, sk))
     g, feeds = _conv_residual_graph(post, res_first)
     c, got, want = device_run(g, feeds, conv_mode=mode, ctx=hip_ctx,
-                              schedule_fn=lambda n, mnk: sched)
+                              schedule_fn=lambda n, mnk: sched, winograd=False)
     assert sum(1 for n in c.graph.nodes if n.attrs.get("residual_subgraph")) == 1
     assert "elementwise" not in {l.kind for l in c.module.plan}
     assert_close("z", got["z"], want["z"])
     g2, _ = _conv_residual_graph(post, res_first)
     c2, got2, _ = device_run(g2, feeds, conv_mode=mode, ctx=hip_ctx,
-                             schedule_fn=lambda n, mnk: sched, fuse_residual=False)
+                             schedule_fn=lambda n, mnk: sched, fuse_residual=False, winograd=False)
     assert not any(n.attrs.get("residual_subgraph") for n in c2.graph.nodes)
     np.testing.assert_array_equal(got["z"], got2["z"])
 
@@ -342,7 +345,8 @@ def test_conv_stream_k(case, mode, hip_ctx):
 
     sched = MfmaSchedule(64, 64, 16, 2, 2, 32, True).with_stream_k()
     g, feeds = _conv_graph(*case)
-    c = compile_graph(g, feeds=feeds, conv_mode=mode, schedule_fn=lambda n, mnk: sched)
+    c = compile_graph(g, feeds=feeds, conv_mode=mode, schedule_fn=lambda n, mnk: sched,
+                      winograd=False)
     kinds = [l.kind for l in c.module.plan]
     assert kinds[-1] == "streamk_fixup"
     main = c.module.plan[-2]
@@ -368,13 +372,15 @@ def test_splitk_reduce_vector_and_scalar_forms_agree(case, hip_ctx, monkeypatch)
 
     sched = MfmaSchedule(64, 64, 16, 2, 2, 32, True, 5)
     g, feeds = _conv_graph(*case)
-    c, got, want = device_run(g, feeds, ctx=hip_ctx, schedule_fn=lambda n, mnk: sched)
+    c, got, want = device_run(g, feeds, ctx=hip_ctx, schedule_fn=lambda n, mnk: sched,
+                              winograd=False)
     (red,) = [l for l in c.module.plan if l.kind == "splitk_reduce"]
     assert red.kernel_name.startswith("splitk_reduce4_")
     assert_close("y", got["y"], want["y"])
     monkeypatch.setattr(emit, "REDUCE_VEC", 1)
     g2, _ = _conv_graph(*case)
-    c2, got2, _ = device_run(g2, feeds, ctx=hip_ctx, schedule_fn=lambda n, mnk: sched)
+    c2, got2, _ = device_run(g2, feeds, ctx=hip_ctx, schedule_fn=lambda n, mnk: sched,
+                             winograd=False)
     assert not any(l.kernel_name.startswith("splitk_reduce4_") for l in c2.module.plan)
     np.testing.assert_array_equal(got["y"], got2["y"])
 

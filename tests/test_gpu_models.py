@@ -58,14 +58,15 @@ def _isolated(c, feeds, ctx):
 
 @pytest.mark.parametrize("fold", [True, False], ids=["residual_folded", "reference_groups"])
 @pytest.mark.parametrize("batch", [1, 2])
-@pytest.mark.parametrize("mode", ["implicit", "im2col"])
+@pytest.mark.parametrize("mode", ["implicit", "implicit-gemm", "im2col"])
 def test_resnet18_every_group(batch, mode, fold, hip_ctx):
     """Every fused group run in isolation on the oracle's inputs: the
     reference's 32 groups, or 23 once the 8 residual Add+Relu groups are
     folded into their convs and the pool writes the flattened logits input."""
     g = build_resnet18(batch=batch)
     feeds = {"input": make_input(batch)}
-    c = compile_graph(g, feeds=feeds, conv_mode=mode, fuse_residual=fold)
+    c = compile_graph(g, feeds=feeds, conv_mode=mode.split("-")[0], fuse_residual=fold,
+                      winograd=mode == "implicit")
     assert c.module.fallbacks() == []
     got, want, chained = _isolated(c, feeds, hip_ctx)
     assert len(got) == (23 if fold else 32)
@@ -112,13 +113,13 @@ def _every_group_b32(c, feeds, want, ctx):
 @pytest.mark.timeout(600)
 @pytest.mark.parametrize("fold", [True, False], ids=["residual_folded", "reference_groups"])
 def test_resnet18_b32_every_group(fold, oracle_b32, hip_ctx):
-    """The headline config (batch 32, the shipped gfx950 schedules bench.py
-    runs): every fused group in isolation on the oracle's inputs within rtol
-    1e-4 / atol 1e-5. The batch-32 plan holds kernels batch 1 and 2 never
-    build: split-K slices with their ordered reduce, stream-K convs with
-    their fix-up, and the stem on 512 workgroups."""
+    """The headline config on the implicit GEMM (batch 32, the shipped gfx950
+    schedules): every fused group in isolation on the oracle's inputs within
+    rtol 1e-4 / atol 1e-5. The batch-32 plan holds kernels batch 1 and 2
+    never build: split-K slices with their ordered reduce, stream-K convs
+    with their fix-up, and the stem on 512 workgroups."""
     feeds, want = oracle_b32("resnet18")
-    c = compile_graph(build_resnet18(batch=32), feeds=feeds, fuse_residual=fold)
+    c = compile_graph(build_resnet18(batch=32), feeds=feeds, fuse_residual=fold, winograd=False)
     kinds = {l.kind for l in c.module.plan}
     assert {"splitk_reduce", "streamk_fixup", "conv_smallc"} <= kinds, kinds
     assert any("_SK_" in l.kernel_name and l.kind == "conv" for l in c.module.plan)

@@ -49,7 +49,7 @@ CASES = [
     (1, 36, 5, 5, 64, (0, 0, 0, 0), 1),       # valid conv, 3x3 output (odd tile edge)
     (1, 5, 8, 8, 7, (1, 1, 1, 1), 1),         # one partial chunk
     (2, 256, 7, 7, 72, (1, 1, 1, 1), 8),      # small grid: channel sum over 8 slices
-    (1, 200, 6, 10, 130, (2, 1, 0, 2), 4),    # slices with a partial last chunk
+    (1, 200, 6, 10, 130, (2, 1, 0, 2), 7),    # slices with a partial last chunk
 ]
 
 

@@ -122,7 +122,7 @@ def test_which_convs_take_the_direct_kernel():
     g, feeds = _graph(1, 3, 16, 16, 8, 3, 1, 1)
     kinds = [l.kind for l in compile_graph(g, feeds=feeds, conv_mode="im2col").module.plan]
     assert "conv_smallc" not in kinds
-    kinds = [l.kind for l in compile_graph(g, feeds=feeds, small_conv=False).module.plan]
+    kinds = [l.kind for l in compile_graph(g, feeds=feeds, small_conv=False, winograd=False).module.plan]
     assert kinds == ["conv"]
 
 
