@@ -174,9 +174,10 @@ def roofline(prof, *, traffic_json: str = "", verbose: bool = True) -> tuple:
     per: dict = {}
     for launch, ms in prof:
         d = per.setdefault(launch.kernel_name, {"ms": 0.0, "flops": 0, "ops": 0, "bytes": 0,
-                                                "launches": 0})
+                                                "launches": 0, "direct_flops": 0})
         d["ms"] += ms
         d["flops"] += launch.meta.get("flops", 0)
+        d["direct_flops"] += launch.meta.get("direct_flops", 0)
         d["ops"] += launch.meta.get("ops", 0)
         d["bytes"] += launch.meta.get("bytes", 0)
         d["launches"] += 1
@@ -208,6 +209,12 @@ def roofline(prof, *, traffic_json: str = "", verbose: bool = True) -> tuple:
             roof["traffic"] = m["traffic_bytes"]
     roof.update({"kernel": name, "launches_per_step": d["launches"], "avg_launch_ms": avg,
                  "share_of_step": d["ms"] / total})
+    if d["direct_flops"]:
+        # a Winograd convolution: "achieved" counts the multiply-adds it
+        # performs (16 per 2x2 tile and channel pair); the direct
+        # convolution's count over the same time is reported beside it
+        roof["algorithm"] = "winograd F(2x2,3x3)"
+        roof["direct_conv_equivalent"] = d["direct_flops"] / d["launches"] / (avg * 1e-3) / 1e12
     # the launches that finish this kernel's output (same graph node, next in the plan)
     group_ms, finishers = [], set()
     for i, (launch, ms) in enumerate(prof):
