@@ -266,7 +266,8 @@ def compile_network(args, name: str, batch: int):
     t0 = time.perf_counter()
     folds = dict(fuse_residual=False, fuse_int8_epilogues=False) if args.no_fold else {}
     c = compile_graph(build(batch=batch), feeds={"input": x}, conv_mode=args.conv_mode,
-                      schedule_fn=schedule_source(args), winograd=args.winograd, **folds)
+                      schedule_fn=schedule_source(args),
+                      winograd={"auto": "auto", "always": True, "never": False}[args.winograd], **folds)
     log(f"{name} b={batch}: compiled in {time.perf_counter() - t0:.1f} s, {len(c.module.plan)} launches")
     return c, {"input": x}
 
@@ -439,8 +440,9 @@ def main(argv=None) -> int:
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--size", type=int, default=4096, help="int8_gemm M = N = K")
     ap.add_argument("--conv-mode", default="implicit", choices=["implicit", "im2col"])
-    ap.add_argument("--no-winograd", dest="winograd", action="store_false",
-                    help="3x3 stride-1 convs on the implicit GEMM instead of Winograd F(2x2, 3x3)")
+    ap.add_argument("--winograd", default="auto", choices=["auto", "always", "never"],
+                    help="3x3 stride-1 convs as Winograd F(2x2, 3x3): where its grid fills half "
+                         "the CUs (auto), always, or never (the implicit GEMM)")
     ap.add_argument("--schedules", default="", help="tuner JSON cache to use instead of the "
                     "shipped mdlc_amd/autotuner/tuned_gfx950.json")
     ap.add_argument("--graph", action="store_true", help="replay the plan as a hipGraph")

@@ -48,7 +48,7 @@ from mdlc_amd.codegen.hip.emit_int8 import Int8LoweringMixin
 from mdlc_amd.codegen.hip.plan import LIBRARY_PARTS, QUANT_OPS, HipModule, Launch, round4, round16  # noqa: F401
 from mdlc_amd.codegen.schedule import (WINO_BK, WINO_BM, WINO_BN, MfmaSchedule, default_schedule,
                                       smallc_fits, smallc_pairs, smallc_tile, split_slices, wino_fits,
-                                      wino_patch, wino_slices)
+                                      wino_patch, wino_pays, wino_slices)
 from mdlc_amd.ir import DType, Graph, Node
 from mdlc_amd.passes.fuse_elementwise import ELEMENTWISE
 from mdlc_amd.passes.shape_inference import conv_geometry
@@ -72,12 +72,16 @@ def dw_rows_per_thread(oh: int) -> int:
 class HipCodegen(Int8LoweringMixin):
     def __init__(self, schedule_fn: Optional[ScheduleFn] = None, *, conv_mode: str = "implicit",
                  int8_depthwise: str = "mfma", small_conv: bool = True,
-                 winograd: bool = True) -> None:
+                 winograd="auto") -> None:
         """``int8_depthwise``: "mfma" runs 16-channel-aligned int8 depthwise
         convs as block-diagonal GEMMs on the matrix cores, "vector" keeps
         them on the per-pixel vector kernel. ``small_conv``: convs with few
         input channels take the direct kernel (implicit mode). ``winograd``:
-        3x3 stride-1 convs run as Winograd F(2x2, 3x3) (implicit mode)."""
+        3x3 stride-1 convs run as Winograd F(2x2, 3x3) (implicit mode): True
+        always, "auto" where its grid fills at least half the CUs
+        (``wino_pays``), False never."""
+        if winograd not in (True, False, "auto"):
+            raise ValueError(f"winograd must be True, False or 'auto', not {winograd!r}")
         if conv_mode not in ("implicit", "im2col"):
             raise ValueError(f"conv_mode must be 'implicit' or 'im2col', not {conv_mode!r}")
         if int8_depthwise not in ("mfma", "vector"):
@@ -210,7 +214,9 @@ class HipCodegen(Int8LoweringMixin):
             self._lower_conv_smallc(g, node, geo, has_bias)
             return
         if (self.conv_mode == "implicit" and self.winograd and wino_fits(geo)
-                and geo["N"] * geo["C"] * geo["H"] * geo["W"] < 2 ** 31):
+                and geo["N"] * geo["C"] * geo["H"] * geo["W"] < 2 ** 31
+                and (self.winograd is True or wino_pays(
+                    geo["OC"], geo["N"] * -(-geo["OH"] // 2) * -(-geo["OW"] // 2), geo["C"]))):
             self._lower_wino(g, node, geo, has_bias)
             return
         OC, K = geo["OC"], geo["C"] * geo["KH"] * geo["KW"]
@@ -866,6 +872,6 @@ def wino_pack_filters(u: np.ndarray, OCP: int, CP: int) -> np.ndarray:
 
 def emit_hip_module(graph: Graph, schedule_fn: Optional[ScheduleFn] = None, *,
                     conv_mode: str = "implicit", int8_depthwise: str = "mfma",
-                    small_conv: bool = True, winograd: bool = True) -> HipModule:
+                    small_conv: bool = True, winograd="auto") -> HipModule:
     return HipCodegen(schedule_fn, conv_mode=conv_mode, int8_depthwise=int8_depthwise,
                       small_conv=small_conv, winograd=winograd).lower(graph)

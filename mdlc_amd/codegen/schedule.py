@@ -405,6 +405,17 @@ def wino_patch(N: int, H: int, W: int, PT: int, OH: int, OW: int) -> int:
     return int((rows * WP).max())
 
 
+def wino_pays(OC: int, tiles: int, C: int) -> bool:
+    """Whether the Winograd kernel is expected to beat the implicit GEMM:
+    its workgroups (one per CU at a time) must fill at least half the CUs
+    with at least 8 chunks each (the two-stage pipeline's fill and the
+    epilogue amortized); smaller problems (batch-1 layers) leave most of the
+    chip idle, where the tuned GEMM schedules split the work finer."""
+    blocks = -(-OC // WINO_BM) * -(-tiles // WINO_BN)
+    s = wino_slices(OC, tiles, C)
+    return blocks * s >= CUS // 2 and -(-C // WINO_BK) // s >= 8
+
+
 def wino_fits(geo: dict) -> bool:
     """A plain 3x3 stride-1 undilated convolution whose workgroups' input
     patches fit the kernel's LDS."""

@@ -59,7 +59,7 @@ def compile_graph(graph: Graph, *, batch: int = 1, feeds: Optional[dict] = None,
                   schedule_fn=None, verify: Optional[Callable] = None,
                   conv_mode: str = "implicit", fuse_int8_epilogues: bool = True,
                   int8_depthwise: str = "mfma", fuse_residual: bool = True,
-                  fuse_int8_mlp=True, small_conv: bool = True, winograd: bool = True) -> Compiled:
+                  fuse_int8_mlp=True, small_conv: bool = True, winograd="auto") -> Compiled:
     """Optimize, plan and lower ``graph``. The reference pipeline runs first,
     unchanged. Then backend epilogue folds: ``fuse_int8_epilogues`` folds a
     QLut or QAdd into the QConv that feeds it; ``fuse_residual`` folds a
@@ -73,8 +73,8 @@ def compile_graph(graph: Graph, *, batch: int = 1, feeds: Optional[dict] = None,
     output of a Flatten that follows it. ``int8_depthwise`` picks the int8 depthwise kernel
     ("mfma" or "vector"). ``small_conv`` runs convs with at most four input
     channels (stems) on the direct small-channel kernel in implicit mode. ``winograd``
-    runs 3x3 stride-1 convs as Winograd F(2x2, 3x3) in implicit mode (False: the
-    implicit GEMM)."""
+    runs 3x3 stride-1 convs as Winograd F(2x2, 3x3) in implicit mode: "auto" where its
+    grid fills at least half the CUs, True always, False never (the implicit GEMM)."""
     original = graph.clone()
     if feeds is None:
         feeds = make_dummy_feeds(graph, batch=batch)

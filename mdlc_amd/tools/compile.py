@@ -52,8 +52,9 @@ def main(argv=None) -> int:
                     "gfx950 schedules when not tuning, a new cache file when tuning)")
     ap.add_argument("--budget", type=int, default=24, help="candidates measured per problem")
     ap.add_argument("--conv-mode", default="implicit", choices=["implicit", "im2col"])
-    ap.add_argument("--no-winograd", dest="winograd", action="store_false",
-                    help="3x3 stride-1 convs on the implicit GEMM instead of Winograd F(2x2, 3x3)")
+    ap.add_argument("--winograd", default="auto", choices=["auto", "always", "never"],
+                    help="3x3 stride-1 convs as Winograd F(2x2, 3x3): where its grid fills half "
+                         "the CUs (auto), always, or never (the implicit GEMM)")
     ap.add_argument("--no-fold", action="store_true",
                     help="keep the reference's fused groups (no residual / int8 epilogue folds)")
     ap.add_argument("--no-verify", action="store_true",
@@ -78,7 +79,7 @@ def main(argv=None) -> int:
         schedule_fn = tuner
 
     kw = dict(batch=args.batch, schedule_fn=schedule_fn, conv_mode=args.conv_mode,
-              winograd=args.winograd)
+              winograd={"auto": "auto", "always": True, "never": False}[args.winograd])
     if args.no_fold:
         kw.update(fuse_residual=False, fuse_int8_epilogues=False)
     if args.model.endswith(".onnx"):

@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 from mdlc_amd.codegen.hip.emit import wino_filter_transform
-from mdlc_amd.codegen.schedule import wino_slices
+from mdlc_amd.codegen.schedule import wino_pays, wino_slices
 from mdlc_amd.compiler import compile_graph
 from mdlc_amd.tools.graph_builder import GraphBuilder
 
@@ -67,6 +67,19 @@ def test_slices_fill_the_chip_without_starving_slices():
     assert wino_slices(64, 10, 24) == 1                      # too few chunks to split
 
 
+def test_auto_choice_takes_winograd_only_for_grids_that_fill_the_chip():
+    # ResNet-18's 3x3 stride-1 layers: every stage at batch 32, none at batch 1
+    layers = [(64, 784, 64), (128, 196, 128), (256, 49, 256), (512, 16, 512)]
+    assert all(wino_pays(oc, 32 * t, c) for oc, t, c in layers)
+    assert not any(wino_pays(oc, t, c) for oc, t, c in layers)
+    from mdlc_amd.tools.build_resnet18 import build_resnet18, make_input
+    for batch, n in ((32, 13), (1, 0)):
+        c = compile_graph(build_resnet18(batch=batch), feeds={"input": make_input(batch)})
+        assert sum(l.kind == "wino" for l in c.module.plan) == n
+    with pytest.raises(ValueError, match="winograd"):
+        compile_graph(build_resnet18(batch=1), winograd="yes")
+
+
 def _graph(c, oc, h, w, k=3, s=1, d=1, group=1):
     rng = np.random.default_rng(0)
     b = GraphBuilder("g")
@@ -84,7 +97,7 @@ def _graph(c, oc, h, w, k=3, s=1, d=1, group=1):
                                              (3, 1, 1, 2, False)])
 def test_only_plain_3x3_stride1_convs_take_winograd(k, s, d, group, wino):
     g, feeds = _graph(16, 16, 9, 9, k, s, d, group)
-    kinds = [l.kind for l in compile_graph(g, feeds=feeds).module.plan]
+    kinds = [l.kind for l in compile_graph(g, feeds=feeds, winograd=True).module.plan]
     assert ("wino" in kinds) == wino, kinds
     g, feeds = _graph(16, 16, 9, 9, k, s, d, group)
     assert "wino" not in [l.kind for l in compile_graph(g, feeds=feeds, winograd=False).module.plan]
