@@ -1,14 +1,17 @@
 """Compiler driver: IR graph (or ONNX model) -> optimized, lowered HIP module.
 
-Same pipeline as mdlc/compiler.py:64-95 — passes (optionally verified after
-every change), static shapes, memory plan, codegen — with two differences:
-the frontend is optional (``onnx`` is not part of this stack, so an IR
-``Graph`` is accepted directly), and numerical pass verification is
-injected by the caller (``verify``) instead of running a CPU executor inside
-the compiler. Structural verification always runs.
+Same pipeline as mdlc/compiler.py:64-95 — import, passes (optionally
+verified after every change), static shapes, memory plan, codegen — with two
+differences: ONNX files are read by this package's own protobuf reader
+(``mdlc_amd.frontend``; the ``onnx`` package is not needed) and an IR
+``Graph`` is accepted directly, and numerical pass verification is injected
+by the caller (``verify``) instead of running a CPU executor inside the
+compiler. Structural verification always runs.
 """
 
 from __future__ import annotations
+
+import os
 
 from dataclasses import dataclass, field
 from typing import Callable, Optional
@@ -96,15 +99,26 @@ def compile_graph(graph: Graph, *, batch: int = 1, feeds: Optional[dict] = None,
     return Compiled(original, graph, module, mem_plan, pm, feeds)
 
 
-def compile_onnx(source, **kw) -> Compiled:
-    """Compile an ONNX path/model, or an IR ``Graph``. ONNX input needs the
-    optional ``onnx`` package and an importer; without them pass a Graph."""
+def compile_onnx(source, *, verify_passes: bool = True, **kw) -> Compiled:
+    """Compile an ONNX model (mdlc/compiler.py:64-95): a path to an ``.onnx``
+    file, its bytes, a decoded ``ModelProto`` of ``mdlc_amd.frontend``, or an
+    IR ``Graph``. The model is imported by this package's own protobuf reader
+    (the ``onnx`` package is not needed) and then compiled by
+    ``compile_graph``, which takes the remaining keywords (``batch``,
+    ``feeds``, ``schedule_fn``, backend options). Structural verification runs
+    after every pass; ``verify_passes`` is accepted for the reference's
+    signature (its numerical check against onnxruntime needs the test oracle
+    here, which the product does not import)."""
+    from mdlc_amd.frontend import import_onnx, import_onnx_model
+    from mdlc_amd.frontend.onnx_proto import ModelProto
+
     if isinstance(source, Graph):
-        return compile_graph(source, **kw)
-    try:
-        import onnx  # noqa: F401
-    except ImportError as exc:
-        raise NotImplementedError(
-            "ONNX input needs the `onnx` package, which is not installed; "
-            "build the model as an mdlc_amd.ir.Graph instead") from exc
-    raise NotImplementedError("ONNX import is not part of this backend; pass an IR Graph")
+        graph = source
+    elif isinstance(source, (str, os.PathLike)):
+        graph = import_onnx(source)
+    elif isinstance(source, (bytes, bytearray, memoryview, ModelProto)):
+        graph = import_onnx_model(source)
+    else:
+        raise TypeError(f"compile_onnx takes a path, model bytes, a ModelProto or a Graph, "
+                        f"not {type(source).__name__}")
+    return compile_graph(graph, **kw)

@@ -7,10 +7,9 @@
 
 The reference's CLI (mdlc/tools/compile.py:15-51) takes an ``.onnx`` path and
 offers ``--report``, ``--emit FILE``, ``--tune`` and ``--no-verify``; the same
-flags mean the same here. Models are given by name (the IR-direct builders
-``resnet18``, ``mobilenetv2``, ``repvit_int8``, ``micro:MxNxK``) because the
-``onnx`` package is not part of this stack; an ``.onnx`` path is passed to
-``compile_onnx``, which says so. ``--emit`` writes the hipRTC translation
+flags mean the same here. A model is an ``.onnx`` path (read by the
+package's own protobuf reader) or the name of an IR-direct builder
+(``resnet18``, ``mobilenetv2``, ``repvit_int8``, ``micro:MxNxK``). ``--emit`` writes the hipRTC translation
 unit; ``--tune`` measures schedules on the device when one is visible (the
 cost model ranks them otherwise) and saves the cache; ``--run`` executes one
 forward on the device and prints its time.
@@ -83,9 +82,11 @@ def main(argv=None) -> int:
     if args.no_fold:
         kw.update(fuse_residual=False, fuse_int8_epilogues=False)
     if args.model.endswith(".onnx"):
+        from mdlc_amd.frontend import OnnxDecodeError
+
         try:
             compiled = compile_onnx(args.model, **kw)
-        except NotImplementedError as exc:
+        except (NotImplementedError, OnnxDecodeError, OSError) as exc:
             print(f"error: {exc}", file=sys.stderr)
             return 2
         feeds = compiled.feeds

@@ -1,5 +1,6 @@
 """The compile CLI (reference: mdlc/tools/compile.py:15-51) on the CPU:
-report, emit, cost-model tuning, and the clear error for ONNX input."""
+report, emit, cost-model tuning, ONNX files in (and out, through the
+exporter), and clear errors for missing or malformed files."""
 
 from __future__ import annotations
 
@@ -39,9 +40,30 @@ def test_no_fold_keeps_the_reference_groups(capsys):
     assert "elementwisex8" in out and "im2colx20" in out
 
 
-def test_onnx_input_fails_with_a_clear_message(capsys):
+def test_onnx_file_compiles(capsys):
+    from onnx_fixtures import fixture_path
+
+    assert cli.main([fixture_path("resnet18_w4"), "--report"]) == 0
+    out = capsys.readouterr().out
+    assert "Graph 'main_graph': 69 nodes" in out and "host fallbacks: none" in out
+
+
+def test_exported_model_compiles(tmp_path, capsys):
+    from mdlc_amd.tools import export_onnx
+
+    path = tmp_path / "micro.onnx"
+    assert export_onnx.main(["micro:49x512x4608", "--out", str(path)]) == 0
+    assert cli.main([str(path)]) == 0
+    assert "gemm" in capsys.readouterr().out
+
+
+def test_missing_or_malformed_onnx_fails_with_a_clear_message(tmp_path, capsys):
     assert cli.main(["model.onnx"]) == 2
-    assert "onnx" in capsys.readouterr().err.lower()
+    assert "model.onnx" in capsys.readouterr().err
+    bad = tmp_path / "bad.onnx"
+    bad.write_bytes(b"\x0a\x05ab")
+    assert cli.main([str(bad)]) == 2
+    assert "runs past the message" in capsys.readouterr().err
 
 
 def test_unknown_model_name():

@@ -1,0 +1,171 @@
+"""The ONNX frontend (mdlc/frontend/onnx_importer.py:68-119) without the
+``onnx`` package: this package's protobuf reader and writer, and the importer.
+
+The reader is pinned three ways:
+* the wire format's published examples (the protobuf encoding guide's
+  ``150 -> 08 96 01``, ``"testing"`` under field 2, the packed
+  ``[3, 270, 86942]`` under field 4) and a negative int64;
+* files written by an independent encoder, torch's TorchScript exporter:
+  the imported graph, run by the oracle, reproduces torch's own float32
+  outputs on the fixture's feeds (a wrong field number, dim, attribute or
+  byte order breaks that), and the default-initialized ResNet-18 has the
+  reference's 141 ops with 72 Identity that its pipeline collapses to 32
+  (the reference README's figure);
+* the writer round trip: torch's files re-serialized decode to the same
+  model, and the IR builders' networks exported and imported again give
+  the same graph and bit-identical oracle outputs.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from mdlc_amd.compiler import compile_graph, compile_onnx
+from mdlc_amd.frontend import OnnxDecodeError, import_onnx, import_onnx_model, load_model
+from mdlc_amd.frontend import onnx_proto as P
+from mdlc_amd.frontend.onnx_export import export_onnx
+from mdlc_amd.testing import FP32_NETWORK
+from onnx_fixtures import NAMES, fixture_cases, fixture_path
+from oracle.reference import run_reference
+
+
+def test_wire_format_known_answers():
+    assert list(P._fields(memoryview(bytes.fromhex("089601")))) == [(1, 0, 150)]
+    ((num, wt, v),) = P._fields(memoryview(bytes.fromhex("120774657374696e67")))
+    assert (num, wt, bytes(v)) == (2, 2, b"testing")
+    ((num, wt, v),) = P._fields(memoryview(bytes.fromhex("2206038e029ea705")))
+    out = []
+    P._ints(out, wt, v)
+    assert (num, out) == (4, [3, 270, 86942])
+    w = P._Writer().int(1, 150).str(2, "testing").packed_ints(4, [3, 270, 86942])
+    assert bytes(w.buf).hex() == "089601" + "120774657374696e67" + "2206038e029ea705"
+    neg = bytes(P._Writer().int(3, -1).buf)
+    assert neg.hex() == "18" + "ff" * 9 + "01"
+    ((_, _, v),) = P._fields(memoryview(neg))
+    assert P._signed(v) == -1
+    assert bytes(P._Writer().float(2, 1.0).buf).hex() == "150000803f"
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_torch_exported_models_match_torch(name):
+    g = import_onnx(fixture_path(name))
+    for feeds, want in fixture_cases(name):
+        got = run_reference(g, feeds)
+        assert set(got) == set(want)
+        for k in want:
+            assert got[k].shape == want[k].shape
+            np.testing.assert_allclose(got[k], want[k], rtol=FP32_NETWORK.rtol,
+                                       atol=FP32_NETWORK.atol)
+
+
+def test_a_transposed_weight_is_caught():
+    """The comparison with torch is sensitive to a reader slip of the kind
+    it guards against: one conv weight's elements read in transposed order."""
+    g = import_onnx(fixture_path("conv_bn_relu"))
+    w = next(n for n in g.nodes if n.op_type == "Conv").inputs[1]
+    g.initializers[w] = np.ascontiguousarray(g.initializers[w].reshape(
+        g.initializers[w].shape[::-1]).T)
+    ((feeds, want),) = fixture_cases("conv_bn_relu")
+    got = run_reference(g, feeds)["y"]
+    assert not np.allclose(got, want["y"], rtol=FP32_NETWORK.rtol, atol=FP32_NETWORK.atol)
+
+
+def test_imported_graph_keeps_io_symbolic_dims_and_names():
+    g = import_onnx(fixture_path("mlp"))
+    assert g.runtime_inputs == ["x"] and g.outputs == ["y"]
+    assert g.info("x").shape == ("batch", 16) and g.info("y").shape == ("batch", 8)
+    assert [n.op_type for n in g.nodes] == ["Gemm", "Relu", "Gemm"]
+    assert g.nodes[0].attrs == {"alpha": 1.0, "beta": 1.0, "transB": 1}
+    m = load_model(fixture_path("mlp"))
+    assert m.opset_import == {"": 17} and m.producer_name == "pytorch"
+    assert len(g.topo_sort()) == len(g.nodes)
+
+
+def test_reference_resnet18_export_collapses_141_ops_to_32():
+    g = import_onnx(fixture_path("resnet18_w4_init"))
+    assert len(g.nodes) == 141 and g.op_histogram()["Identity"] == 72
+    c = compile_graph(g, fuse_residual=False)
+    hist = c.graph.op_histogram()
+    assert len(c.graph.nodes) == 32, hist
+    assert hist["FusedConvAct"] == 9 and hist["FusedElementwise"] == 8
+
+
+def test_constant_inputs_of_clip_are_read():
+    """MobileNetV2's ReLU6 is Clip with min/max from Constant nodes whose
+    value is a TENSOR attribute (the reference's clip-bound regression)."""
+    g = import_onnx(fixture_path("mobilenetv2_x0125"))
+    consts = [n for n in g.nodes if n.op_type == "Constant"]
+    vals = sorted({float(n.attrs["value"]) for n in consts})
+    assert vals == [0.0, 6.0] and all(n.attrs["value"].shape == () for n in consts)
+    clip = next(n for n in g.nodes if n.op_type == "Clip")
+    assert len(clip.inputs) == 3
+
+
+def test_rewritten_files_decode_to_the_same_model():
+    for name in NAMES:
+        m = load_model(fixture_path(name))
+        assert P.parse_model(P.serialize_model(m)) == m
+
+
+@pytest.mark.parametrize("model", ["resnet18", "mobilenetv2"])
+def test_builder_graphs_round_trip_through_onnx(model):
+    from mdlc_amd.tools.compile import build_model
+
+    g, feeds = build_model(model, 1)
+    g2 = import_onnx_model(export_onnx(g))
+    assert g2.inputs == g.inputs and g2.outputs == g.outputs
+    assert [(n.op_type, n.inputs, n.outputs) for n in g2.topo_sort()] == \
+        [(n.op_type, n.inputs, n.outputs) for n in g.topo_sort()]
+    for k, v in g.initializers.items():
+        assert g2.initializers[k].dtype == v.dtype and np.array_equal(g2.initializers[k], v)
+    a, b = run_reference(g, feeds), run_reference(g2, feeds)
+    for k in a:
+        np.testing.assert_array_equal(a[k], b[k])
+
+
+def test_compile_onnx_accepts_paths_bytes_models_and_graphs():
+    path = fixture_path("residual_block")
+    data = open(path, "rb").read()
+    plans = [[l.kind for l in compile_onnx(src).module.plan]
+             for src in (path, data, P.parse_model(data), import_onnx(path))]
+    assert all(p == plans[0] for p in plans) and plans[0]
+    with pytest.raises(TypeError):
+        compile_onnx(42)
+
+
+def test_malformed_and_unsupported_inputs_raise():
+    data = open(fixture_path("conv_bn_relu"), "rb").read()
+    with pytest.raises(OnnxDecodeError):
+        P.parse_model(data[:-7])                   # truncated
+    with pytest.raises(OnnxDecodeError, match="no graph"):
+        P.parse_model(b"\x08\x08")                 # ir_version only
+    t = P.TensorProto(name="w", dims=[2], data_type=1, raw_data=b"\x00" * 4)
+    with pytest.raises(OnnxDecodeError, match="raw bytes"):
+        P.tensor_to_array(t)
+    t = P.TensorProto(name="w", dims=[2], data_type=1, external=True)
+    with pytest.raises(OnnxDecodeError, match="external"):
+        P.tensor_to_array(t)
+    m = P.parse_model(data)
+    m.graph.node[0].domain = "com.example"
+    with pytest.raises(NotImplementedError, match="domain"):
+        import_onnx_model(m)
+
+
+def test_typed_tensor_fields():
+    """Tensors stored in the typed repeated fields instead of raw bytes."""
+    cases = [(P.TensorProto(dims=[2, 2], data_type=1, float_data=[1.5, -2, 0, 3]),
+              np.array([[1.5, -2], [0, 3]], np.float32)),
+             (P.TensorProto(dims=[3], data_type=7, int64_data=[-1, 0, 1 << 40]),
+              np.array([-1, 0, 1 << 40], np.int64)),
+             (P.TensorProto(dims=[2], data_type=3, int32_data=[-128, 127]),
+              np.array([-128, 127], np.int8)),
+             (P.TensorProto(dims=[2], data_type=10, int32_data=[0x3C00, 0xC000]),
+              np.array([1.0, -2.0], np.float16)),
+             (P.TensorProto(dims=[], data_type=9, int32_data=[1]), np.array(True))]
+    for t, want in cases:
+        got = P.tensor_to_array(t)
+        assert got.dtype == want.dtype and np.array_equal(got, want)
+        back = P.parse_model(P.serialize_model(P.ModelProto(graph=P.GraphProto(initializer=[
+            P.array_to_tensor("t", got)]))))
+        assert np.array_equal(P.tensor_to_array(back.graph.initializer[0]), want)
