@@ -213,8 +213,10 @@ class HipCodegen(Int8LoweringMixin):
                                                         geo["DW"]):
             self._lower_conv_smallc(g, node, geo, has_bias)
             return
+        # the Winograd kernel reads its input through a buffer resource of
+        # byte offsets below 2^31 (offsets at 0x7ffffff0 read as zeros)
         if (self.conv_mode == "implicit" and self.winograd and wino_fits(geo)
-                and geo["N"] * geo["C"] * geo["H"] * geo["W"] < 2 ** 31
+                and geo["N"] * geo["C"] * geo["H"] * geo["W"] * 4 < 0x7ffffff0
                 and (self.winograd is True or wino_pays(
                     geo["OC"], geo["N"] * -(-geo["OH"] // 2) * -(-geo["OW"] // 2), geo["C"]))):
             self._lower_wino(g, node, geo, has_bias)
@@ -857,16 +859,24 @@ def wino_filter_transform(w: np.ndarray) -> np.ndarray:
 
 
 def wino_pack_filters(u: np.ndarray, OCP: int, CP: int) -> np.ndarray:
-    """U[16][OC][C] -> the Winograd kernel's LDS images, [OCP/64][CP/8][16][64][8]
-    (zero padded): one contiguous 32 KB block per (64-channel output block,
-    8-channel chunk), row oc's two 4-channel halves swapped when bits 2 and 3
-    of oc differ."""
+    """U[16][OC][C] -> the Winograd kernel's LDS images (zero padded): one
+    contiguous 32 KB block per (64-channel output block, 8-channel chunk),
+    laid out as the kernel's A operands are read,
+    [OCP/64][CP/8][og 2][blk 2][j 2][lane 64][slot 4][4]: lane l = 16 lk + li
+    of the wave with channel group og holds U[xi][oc][k] for
+    oc = 32 og + 16 blk + li, k = lk + 4 j, all 16 positions xi = 4 q + e as
+    four 16-byte quartets; quartet q sits in slot q ^ sw(l),
+    sw(l) = ((l >> 1) ^ (l >> 3)) & 3, so that the 16-byte reads of any 8 or
+    16 consecutive lanes hit distinct banks."""
     full = np.zeros((16, OCP, CP), np.float32)
     full[:, :u.shape[1], :u.shape[2]] = u
-    img = full.reshape(16, OCP // 64, 64, CP // 8, 2, 4).transpose(1, 3, 0, 2, 4, 5).copy()
-    rows = np.arange(64)
-    swap = (((rows >> 2) ^ (rows >> 3)) & 1).astype(bool)
-    img[:, :, :, swap] = img[:, :, :, swap][:, :, :, :, ::-1]
+    # axes: q, e, ocb, og, blk, li, chunk, j, lk
+    v = full.reshape(4, 4, OCP // 64, 2, 2, 16, CP // 8, 2, 4)
+    img = v.transpose(2, 6, 3, 4, 7, 8, 5, 0, 1).reshape(OCP // 64, CP // 8, 2, 2, 2, 64, 4, 4)
+    lanes = np.arange(64)
+    sw = ((lanes >> 1) ^ (lanes >> 3)) & 3
+    slot_of = np.arange(4)[None, :] ^ sw[:, None]           # [lane][slot] -> quartet held
+    img = img[:, :, :, :, :, lanes[:, None], slot_of, :]
     return np.ascontiguousarray(img)
 
 

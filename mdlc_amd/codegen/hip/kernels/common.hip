@@ -10,6 +10,13 @@ typedef int intx16 __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
 
+// Raw buffer resource over [p, p + bytes): a load whose offset is at or
+// beyond `bytes` returns zeros instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_over(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+constexpr int kOutside = 0x7ffffff0;   // an offset past every buffer (sizes < 2^31)
+
 // Tile index remap so that consecutive logical tiles run on the same XCD.
 // Workgroup b is dispatched to XCD (b % 8); XCD x owns a contiguous range of
 // logical tiles. The map is a bijection on [0, total).

@@ -15,42 +15,43 @@
 // of the direct convolution's multiply-adds.
 //
 // A workgroup of eight waves (two per SIMD) owns 64 output channels x 64
-// tiles. Wave w = 4h + 2wm + wn owns the 32 x 32 block (wm, wn) of the eight
-// positions of rows a = 2h, 2h + 1 (128 accumulator registers a lane). The
-// output transform is linear in M, so each half h forms its own partial
-// Y_h = A^T M_h A from its two rows; after the channel loop the halves meet
-// in LDS and are added (Y_0 + Y_1, a fixed order) by the whole workgroup,
-// which then applies bias, activation and the folded residual and stores
-// the 2x2 pixels, consecutive threads on consecutive tiles.
+// tiles. Wave w = 2 tg + og owns ALL 16 positions of the 32 output channels
+// 32 og .. 32 og + 31 x the 16 tiles 16 tg .. 16 tg + 15, on
+// v_mfma_f32_16x16x4f32 (16 positions x 2 channel blocks of 16 = 32
+// accumulators of 4, 128 registers a lane). In that instruction lane
+// l = 16 lk + li supplies B[k = lk][li]; k-step j (0, 1) of an 8-channel
+// chunk takes channel lk + 4 j, so a lane's B operands are the V values of
+// ONE window, tile 16 tg + li and channel lk + 4 j: the lane transforms that
+// window itself and feeds the values straight to the matrix core. Its A
+// operand is U[xi][oc = 32 og + 16 blk + li][lk + 4 j]; the filters are
+// transformed on the host (G g G^T, rounded once from float64) and packed
+// per (channel block, chunk) as a 32 KB image in exactly the order the lanes
+// read it, [og][blk][j][lane][16 positions], each lane's 16 values four
+// 16-byte quartets in slots swizzled by lane so that any 8 or 16
+// consecutive lanes' reads hit distinct banks: one chunk's A operands are
+// eight 16-byte LDS reads a lane, and the copy of the image into LDS is a
+// linear 16-byte-per-thread stream. The output transform needs all 16
+// positions of an (oc, tile), which the lane holds (D[4 lk + r][li] of each
+// block), so it runs in registers and the 2x2 pixels are stored directly.
 //
-// The channel sum runs in chunks of 8 channels through two LDS stages:
+// The input reaches the windows through an LDS patch per channel of the
+// rows the workgroup's 64 tiles read, filled with coalesced loads (wave w
+// loads channel w of a chunk), zeros at the padding, so windows are read
+// without bounds checks. The patch of one channel takes WINO_PSTR floats,
+// 32 banks apart from the next channel's, so the four channels a window
+// read touches at once hit distinct banks.
 //
-//   U stage  [16 xi][64 oc][8 k]: the filters, transformed on the host
-//            (G g G^T, rounded once from float64) and packed per (channel
-//            block, chunk) as exactly this 32 KB image, the two 16-byte
-//            halves of row r swapped when bit 2 of r differs from bit 3, so
-//            that any 8 (or 16) consecutive rows' 16-byte fragment reads hit
-//            distinct banks of a 32 (or 64) bank LDS: the copy is a linear
-//            16-byte-per-thread stream.
-//   V stage  [16 xi][8 k][VLD]: the transformed input, tile-contiguous, so
-//            that the transform's stores (64 consecutive tiles of one
-//            channel per wave instruction) are conflict free.
-//
-// Chunk c's MFMAs read stage c % 2 while the waves also fill the other
-// stage with chunk c+1 (loaded into registers one chunk earlier) and issue
-// the global loads of chunk c+2: half 0 the input windows (two (tile,
-// channel) windows a thread, transformed), half 1 the filter image, so each
-// SIMD has one wave with the heavy staging and one with the light. One
-// barrier per chunk. The input reaches the windows through a per-wave LDS
-// patch of the rows the workgroup's tiles read, loaded with coalesced
-// loads, zeros at the padding; windows are then read without bounds checks.
-//
-// MFMA k order: in v_mfma_f32_32x32x2f32 lane l = 32*lk + li supplies
-// A[li][k] and B[k][li] for k = lk of the instruction's two; instruction q
-// (q = 0..3) of a chunk takes k = 4*lk + q, so a lane's four A values are
-// one 16-byte read and its B values four reads of one V row each. The
-// instructions alternate between two positions so consecutive MFMAs are
-// independent.
+// Per chunk c, two phases around one barrier:
+//   J0: transform window (c, j = 1), run the 32 j = 0 MFMAs;
+//   barrier;
+//   J1: transform window (c+1, j = 0), run the 32 j = 1 MFMAs.
+// Each phase computes the V values the next phase needs into the registers
+// the current phase does not read, so V takes 32 registers. The staging
+// (a wave's channel of the patch and its pieces of the filter image, stored
+// from registers into LDS, then the global loads of a later chunk) runs in
+// J0 on waves 0-3 and in J1 on waves 4-7, which share SIMDs with them. Three
+// filter stages and two patch buffers make the one barrier enough: a stage
+// or buffer is rewritten only after the barrier that follows its last reads.
 //
 // With SPLIT the channel chunks are divided among gridDim.y slices and each
 // writes its raw Y to the split-K workspace ws[(slice * OC + oc) * P + pixel],
@@ -71,29 +72,28 @@ struct WinoArgs {
 };
 
 constexpr int WINO_NT = 512;
-constexpr int WINO_VLD = 72;                          // V row: 64 tiles + 8 (bank offset of the k halves)
-constexpr int WINO_USTAGE = 16 * 64 * 8;              // floats
-constexpr int WINO_VSTAGE = 16 * 8 * WINO_VLD;
-constexpr int WINO_STAGE = WINO_USTAGE + WINO_VSTAGE; // 68 KB
+constexpr int WINO_USTAGE = 16 * 64 * 8;              // filter image floats per chunk (32 KB)
 constexpr int WINO_PMAX = 704;                        // input patch floats per channel
+constexpr int WINO_PSTR = WINO_PMAX + 32;             // patch stride per channel (banks apart)
+constexpr int WINO_PBUF = 8 * WINO_PSTR;              // one chunk's patch
 
-// PL: patch loads per lane and channel, ceil(largest patch / 64) <= WINO_PMAX / 64.
+// PL: patch loads per lane (one channel per wave), ceil(largest patch / 64)
+// <= WINO_PMAX / 64.
 template <bool SPLIT, int PL, class Epi>
 __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
   static_assert(PL * 64 <= WINO_PMAX, "patch larger than its LDS");
-  __shared__ __attribute__((aligned(16))) float lds[2 * WINO_STAGE];
-  __shared__ float patch[4 * 2 * WINO_PMAX];         // per half-0 wave, two channels
+  __shared__ __attribute__((aligned(16))) float ust[3 * WINO_USTAGE];
+  __shared__ __attribute__((aligned(16))) float pbuf[2 * WINO_PBUF];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int h = wave >> 2;                          // position rows 2h, 2h + 1
-  const int wm0 = ((wave >> 1) & 1) * 32;
-  const int wn0 = (wave & 1) * 32;
-  const int li = lane & 31;
-  const int lk = lane >> 5;
+  const int og = wave & 1;
+  const int tg = wave >> 1;
+  const int li = lane & 15;
+  const int lk = lane >> 4;
 
-  const int P = g.N * g.TH * g.TW;                  // tiles in the batch
+  const int P = g.N * g.TH * g.TW;
   const int tiles_n = (P + 63) / 64;
   const int ocb = blockIdx.x / tiles_n;
   const int t0 = (blockIdx.x % tiles_n) * 64;
@@ -106,9 +106,9 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
   // For each image its 64 tiles touch (segment s = image nfirst + s), the
   // rows its tiles' windows read (image coordinates, padding rows included),
   // each WP = 2 TW + 2 columns wide starting at column -PL; positions outside
-  // the image hold zero, so windows are read without bounds checks. The
-  // segments are stacked: segment 0 holds rows rlo0 .. (its last), the
-  // others rows -PT .. (their last), whole images 2 TH + 2 rows.
+  // the image hold zero. The segments are stacked: segment 0 holds rows
+  // rlo0 .. (its last), the others rows -PT .. (their last), whole images
+  // 2 TH + 2 rows.
   const int TT = g.TH * g.TW;
   const int WP = 2 * g.TW + 2;
   const int nfirst = t0 / TT;
@@ -117,18 +117,12 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
   const int rlo0 = 2 * ((t0 - nfirst * TT) / g.TW) - g.PT;
   const int rhil = 2 * ((plast - nlast * TT) / g.TW) + 3 - g.PT;
   const int rows0 = (nlast == nfirst ? rhil : 2 * g.TH + 1 - g.PT) - rlo0 + 1;
-  const int seg = (2 * g.TH + 2) * WP;              // elements of a whole image's segment
+  const int seg = (2 * g.TH + 2) * WP;
   const int PS = rows0 * WP + (nlast > nfirst ? (nlast - nfirst - 1) * seg + (rhil + g.PT + 1) * WP : 0);
 
-  // ---- staging: half 0 transforms the input windows, each thread those of
-  // tile t0 + lane for channels wq and wq + 4 of a chunk, read from its
-  // wave's patch of the two channels; half 1 copies the filter image, eight
-  // 16-byte pieces a thread.
-  const int wq = wave & 3;
-  const int lt = tid & 255;
-  int wbase;                                        // the lane's window in the patch
+  const int p = t0 + 16 * tg + li;                  // the lane's tile
+  int wbase;
   {
-    const int p = t0 + lane;
     const int pc = p < P ? p : t0;                  // tiles past the batch: any window, never stored
     const int n = pc / TT;
     const int r = pc - n * TT;
@@ -137,10 +131,10 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
     const int sg = n - nfirst;
     wbase = (sg == 0 ? (2 * ty - g.PT - rlo0) * WP : rows0 * WP + (sg - 1) * seg + 2 * ty * WP) + 2 * tx;
   }
-  // the lane's patch elements lane + 64 i: offset of the channel-0 value, or
-  // a zero (bit i of pzero) outside the image or past the patch
+  // the lane's patch elements lane + 64 i: byte offset of the value from
+  // the channel's plane in image 0, or kOutside (a zero) outside the image
+  // or past the patch
   int poff[PL];
-  unsigned pzero = 0;
 #pragma unroll
   for (int i = 0; i < PL; ++i) {
     const int e = i * 64 + lane;
@@ -158,254 +152,190 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
     }
     const int ix = col - g.PL;
     const bool ok = e < PS && (unsigned)row < (unsigned)g.H && (unsigned)ix < (unsigned)g.W;
-    poff[i] = ok ? (nfirst + sg) * g.C * HW + row * g.W + ix : 0;
-    pzero |= (ok ? 0u : 1u) << i;
+    poff[i] = ok ? ((nfirst + sg) * g.C * HW + row * g.W + ix) * 4 : kOutside;
   }
+  const int xbytes = g.N * g.C * HW * 4;
 
-  // registers of the chunk in flight: half 0 the two channels' patch
-  // elements, half 1 the filter image pieces
-  float4 ur[8];
-  float pv[2][PL];
-  int held = chunk0;                                // chunk the patch registers hold
-  float* pw = patch + wq * (2 * WINO_PMAX);
+  // staging registers: channel `wave` of a chunk's patch, four 16-byte
+  // pieces of its filter image. The loads go through buffer resources: the
+  // patch's zeros (padding, and every element of a channel past the last)
+  // come back from out-of-range offsets, and the chunk's position is in the
+  // resource, so the loop computes no addresses.
+  float pv[PL];
+  float4 ur[4];
   auto load_x = [&](int chunk) {
-    held = chunk;
+    const int c = chunk * 8 + wave;
+    const __amdgpu_buffer_rsrc_t r = buffer_over(g.x + (size_t)min(c, g.C - 1) * HW,
+                                                 c < g.C ? xbytes - c * HW * 4 : 0);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const float* src = g.x + (size_t)min(chunk * 8 + wq + 4 * j, g.C - 1) * HW;
-#pragma unroll
-      for (int i = 0; i < PL; ++i) pv[j][i] = src[(unsigned)poff[i]];
-    }
+    for (int i = 0; i < PL; ++i)
+      pv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, poff[i], 0, 0));
   };
-  auto store_x = [&](float* st) {
-    // the patch, zeros written with a bit mask (no select: it would branch)
+  auto store_x = [&](int buf) {
+    float* pw = pbuf + buf * WINO_PBUF + wave * WINO_PSTR;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int i = 0; i < PL; ++i)
-        pw[j * WINO_PMAX + i * 64 + lane] =
-            __uint_as_float(__float_as_uint(pv[j][i]) & ((pzero >> i & 1u) - 1u));
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      // V of channel wq + 4j; zero past the last channel (its filters are
-      // zero too, but the window would repeat the last channel's values)
-      float v[16];
-      if (held * 8 + wq + 4 * j < g.C) {
-        const float* pj = pw + j * WINO_PMAX + wbase;
-        float d[16];
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-          for (int b = 0; b < 4; ++b) d[4 * a + b] = pj[a * WP + b];
-        float t[16];                                // t = B^T d, row by row
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          t[b] = d[b] - d[8 + b];
-          t[4 + b] = d[4 + b] + d[8 + b];
-          t[8 + b] = d[8 + b] - d[4 + b];
-          t[12 + b] = d[4 + b] - d[12 + b];
-        }
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {               // V = t B
-          v[4 * a + 0] = t[4 * a] - t[4 * a + 2];
-          v[4 * a + 1] = t[4 * a + 1] + t[4 * a + 2];
-          v[4 * a + 2] = t[4 * a + 2] - t[4 * a + 1];
-          v[4 * a + 3] = t[4 * a + 1] - t[4 * a + 3];
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) v[e] = 0.f;
-      }
-      // all 16 values in their own registers before the stores, so a store
-      // waiting for the LDS does not hold up the transform of the next window
-      float* vs = st + WINO_USTAGE + (wq + 4 * j) * WINO_VLD + lane;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) vs[e * 8 * WINO_VLD] = v[e];
-    }
+    for (int i = 0; i < PL; ++i) pw[i * 64 + lane] = pv[i];
   };
   auto load_u = [&](int chunk) {
-    const float* us = ublk + (size_t)chunk * WINO_USTAGE;
+    const __amdgpu_buffer_rsrc_t r = buffer_over(ublk + (size_t)chunk * WINO_USTAGE, WINO_USTAGE * 4);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ur[i] = ld4(us + (lt + i * 256) * 4);
+    for (int i = 0; i < 4; ++i)
+      ur[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (tid + i * WINO_NT) * 16, 0, 0));
   };
-  auto store_u = [&](float* st) {
+  auto store_u = [&](int stage) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) st4(st + (lt + i * 256) * 4, ur[i]);
+    for (int i = 0; i < 4; ++i) st4(ust + stage * WINO_USTAGE + (tid + i * WINO_NT) * 4, ur[i]);
   };
-
-  // acc[i] = M at position xi = 8h + i
-  floatx16 acc[8];
+  // V = B^T d B of the lane's window for channel lk + 4 j of a chunk (zero
+  // past the last channel: its patch is zeros)
+  auto window = [&](float (&v)[16], int buf, int j) {
+    const float* pj = pbuf + buf * WINO_PBUF + (lk + 4 * j) * WINO_PSTR + wbase;
+    float d[16];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+    for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
-
-  // fragment addresses within a stage (floats)
-  const int arow = wm0 + li;
-  const int a_off = arow * 8 + 4 * (lk ^ (((arow >> 2) ^ (arow >> 3)) & 1));
-  const int b_off = WINO_USTAGE + (4 * lk) * WINO_VLD + wn0 + li;
-
-  // MFMA fragments of one group of two positions: A as one 16-byte read,
-  // B as two pairs of V rows per position
-  struct Frag {
-    float4 a[2];
-    float b[2][4];
-  };
-  auto read_frags = [&](Frag& f, const float* st, int xg) {
-#pragma unroll
-    for (int x = 0; x < 2; ++x) {
-      const int xi = 8 * h + 2 * xg + x;
-      f.a[x] = ld4(st + xi * 512 + a_off);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) f.b[x][q] = st[b_off + xi * 8 * WINO_VLD + q * WINO_VLD];
-    }
-  };
-  auto mfma_group = [&](const Frag& f, int xg) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        const float a = q == 0 ? f.a[x].x : q == 1 ? f.a[x].y : q == 2 ? f.a[x].z : f.a[x].w;
-        acc[2 * xg + x] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, f.b[x][q], acc[2 * xg + x], 0, 0, 0);
+      for (int b = 0; b < 4; b += 2) {
+        const float2 q = *reinterpret_cast<const float2*>(pj + a * WP + b);
+        d[4 * a + b] = q.x;
+        d[4 * a + b + 1] = q.y;
       }
-  };
-
-  // Staging is split by half: half 0 loads and transforms the input
-  // windows (the heavy part), half 1 copies the filter image, each into the
-  // stage of the next chunk while the current chunk's MFMAs run, and each
-  // loading the chunk after that; so on every SIMD one wave's MFMAs keep the
-  // matrix core busy while the other wave stages. The two halves run their
-  // own copy of the loop (the same barriers), so each holds only its own
-  // staging registers. Past the last chunk the stores and loads repeat the
-  // last chunk (in bounds, never read); a stage is written only after the
-  // barrier that ends its last reads. The scheduling barriers keep the
-  // global loads ahead of the MFMAs (left to itself the compiler sinks them
-  // to the end of the loop, where their latency shows).
-  auto mfma_chunk = [&](const float* cur) {
-    Frag f0, f1;
-    read_frags(f0, cur, 0);
-    read_frags(f1, cur, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma_group(f0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(f0, cur, 2);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma_group(f1, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(f1, cur, 3);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma_group(f0, 2);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma_group(f1, 3);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  if (h == 0) {
-    load_x(chunk0);
-    store_x(lds);
-    load_x(chunk0 + min(1, g.nchunk - 1));
-    __syncthreads();
-    for (int ch = 0; ch < g.nchunk; ++ch) {
-      __builtin_amdgcn_sched_barrier(0);
-      store_x(lds + ((ch + 1) & 1) * WINO_STAGE);
-      __builtin_amdgcn_sched_barrier(0);
-      load_x(chunk0 + min(ch + 2, g.nchunk - 1));
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_chunk(lds + (ch & 1) * WINO_STAGE);
-      __syncthreads();
-    }
-  } else {
-    load_u(chunk0);
-    store_u(lds);
-    load_u(chunk0 + min(1, g.nchunk - 1));
-    __syncthreads();
-    for (int ch = 0; ch < g.nchunk; ++ch) {
-      __builtin_amdgcn_sched_barrier(0);
-      store_u(lds + ((ch + 1) & 1) * WINO_STAGE);
-      __builtin_amdgcn_sched_barrier(0);
-      load_u(chunk0 + min(ch + 2, g.nchunk - 1));
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_chunk(lds + (ch & 1) * WINO_STAGE);
-      __syncthreads();
-    }
-  }
-
-  // ---- output transform: partial Y of this half, through LDS -------------
-  // acc[4a' + b][r] holds M at row a = 2h + a', column b, for
-  // oc = wm0 + (r/4)*8 + lk*4 + r%4 and tile = wn0 + li (the 32x32x2
-  // accumulator layout). s = A^T M restricted to the two rows, Y = s A.
-  // Layout in LDS: Yp[h][oc][tile][4] (the stages are no longer read).
-  float* yp = lds + h * (64 * 64 * 4);
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int oc = wm0 + (r >> 2) * 8 + lk * 4 + (r & 3);
-    float s0[4], s1[4];
+    float t[16];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      const float m0 = acc[b][r], m1 = acc[4 + b][r];
-      if (h == 0) {                                 // rows 0, 1: A^T columns (1, 0), (1, 1)
-        s0[b] = m0 + m1;
-        s1[b] = m1;
-      } else {                                      // rows 2, 3: (1, -1), (0, -1)
-        s0[b] = m0;
-        s1[b] = -m0 - m1;
-      }
+      t[b] = d[b] - d[8 + b];
+      t[4 + b] = d[4 + b] + d[8 + b];
+      t[8 + b] = d[8 + b] - d[4 + b];
+      t[12 + b] = d[4 + b] - d[12 + b];
     }
-    float4 yv;
-    yv.x = s0[0] + s0[1] + s0[2];
-    yv.y = s0[1] - s0[2] - s0[3];
-    yv.z = s1[0] + s1[1] + s1[2];
-    yv.w = s1[1] - s1[2] - s1[3];
-    st4(yp + (oc * 64 + wn0 + li) * 4, yv);
-  }
-  __syncthreads();
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      v[4 * a + 0] = t[4 * a] - t[4 * a + 2];
+      v[4 * a + 1] = t[4 * a + 1] + t[4 * a + 2];
+      v[4 * a + 2] = t[4 * a + 2] - t[4 * a + 1];
+      v[4 * a + 3] = t[4 * a + 1] - t[4 * a + 3];
+    }
+  };
 
-  // ---- epilogue: Y = Y_0 + Y_1, 8 (channel, tile) pairs a thread ----------
-  const int OHW = g.OH * g.OW;
-  const bool pairs = (g.OW & 1) == 0;               // (ox, ox + 1) 8-byte aligned
-#pragma unroll 2
-  for (int i = 0; i < 8; ++i) {
-    const int idx = tid + i * WINO_NT;
-    const int ocl = idx >> 6, tl = idx & 63;
-    const int oc = ocb * 64 + ocl;
-    const int p = t0 + tl;
-    if (oc >= g.OC || p >= P) continue;
-    const float4 y0 = ld4(lds + (ocl * 64 + tl) * 4);
-    const float4 y1v = ld4(lds + 64 * 64 * 4 + (ocl * 64 + tl) * 4);
-    float out[4] = {y0.x + y1v.x, y0.y + y1v.y, y0.z + y1v.z, y0.w + y1v.w};
-    const int n = p / (g.TH * g.TW);
-    const int rr = p - n * (g.TH * g.TW);
-    const int ty = rr / g.TW;
-    const int tx = rr - ty * g.TW;
-    const int oy = 2 * ty, ox = 2 * tx;
-    const bool yok = oy + 1 < g.OH, xok = ox + 1 < g.OW;
-    float* dst;
-    if (SPLIT) {
-      dst = g.y + ((size_t)slice * g.OC + oc) * ((size_t)g.N * OHW) + (size_t)n * OHW;
-    } else {
-      dst = g.y + ((size_t)n * g.OC + oc) * OHW;
-      const float b = Epi::bias == 1 ? g.bias[oc] : 0.f;
-      const float* res = Epi::residual ? g.R + ((size_t)n * g.OC + oc) * OHW : nullptr;
+  // A operands: the lane's 16 positions of (blk, j) are four 16-byte
+  // quartets of the filter image, quartet q in slot q ^ sw
+  const int sw = ((lane >> 1) ^ (lane >> 3)) & 3;
+  int qoff[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int py = oy + (e >> 1), px = ox + (e & 1);
-        const bool ok = (e & 2 ? yok : true) && (e & 1 ? xok : true);
-        float v = Epi::apply(out[e], b);
-        if (Epi::residual) v = Epi::post(v, ok ? res[py * g.OW + px] : 0.f);
-        out[e] = v;
-      }
-    }
+  for (int q = 0; q < 4; ++q) qoff[q] = (og * 4 * 64 + lane) * 16 + ((q ^ sw) << 2);
+  floatx4 acc[16][2];
 #pragma unroll
-    for (int e2 = 0; e2 < 2; ++e2) {
-      if (e2 == 1 && !yok) break;
-      float* row = dst + (oy + e2) * g.OW + ox;
-      if (pairs && xok) {
-        *reinterpret_cast<float2*>(row) = make_float2(out[2 * e2], out[2 * e2 + 1]);
-      } else {
-        row[0] = out[2 * e2];
-        if (xok) row[1] = out[2 * e2 + 1];
-      }
+  for (int xi = 0; xi < 16; ++xi)
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[xi][blk][r] = 0.f;
+  auto mfma_half = [&](const float* st, int j, const float (&v)[16]) {
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      float4 a[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a[q] = ld4(st + (blk * 2 + j) * 64 * 16 + qoff[q]);
+#pragma unroll
+      for (int xi = 0; xi < 16; ++xi)
+        acc[xi][blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(pick(a[xi >> 2], xi & 3), v[xi],
+                                                             acc[xi][blk], 0, 0, 0);
     }
+  };
+
+  // Waves 0-3 stage in J0, waves 4-7 (their SIMD partners) in J1, so that
+  // on every SIMD one wave's stores and loads overlap the other's MFMAs. A
+  // wave stores its own channel of the patch and its own pieces of the
+  // filter image, so the two groups' stores of one chunk never overlap;
+  // waves 4-7 run one chunk further ahead (they store chunk c+2 in J1 of
+  // chunk c, into the patch buffer and filter stage the barrier before J1
+  // has freed).
+  const bool early = wave < 4;
+  auto stage = [&](int buf, int ustage, int next) {
+    __builtin_amdgcn_sched_barrier(0);
+    store_x(buf);
+    store_u(ustage);
+    __builtin_amdgcn_sched_barrier(0);
+    load_x(chunk0 + min(next, g.nchunk - 1));
+    load_u(chunk0 + min(next, g.nchunk - 1));
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  load_x(chunk0);
+  load_u(chunk0);
+  store_x(0);
+  store_u(0);
+  load_x(chunk0 + min(1, g.nchunk - 1));
+  load_u(chunk0 + min(1, g.nchunk - 1));
+  if (!early) stage(1, 1, 2);
+  __syncthreads();
+  float v0[16], v1[16];
+  window(v0, 0, 0);
+  int us = 0;                                       // filter stage of chunk ch
+  for (int ch = 0; ch < g.nchunk; ++ch) {
+    const int pb = ch & 1;                          // patch buffer of chunk ch
+    const int u1 = us == 2 ? 0 : us + 1;            // filter stage of chunk ch + 1
+    const int u2 = u1 == 2 ? 0 : u1 + 1;            // and of chunk ch + 2
+    if (early) stage(pb ^ 1, u1, ch + 2);           // chunk ch + 1 in, ch + 2 loaded
+    window(v1, pb, 1);
+    mfma_half(ust + us * WINO_USTAGE, 0, v0);
+    __syncthreads();
+    if (!early) stage(pb, u2, ch + 3);              // chunk ch + 2 in, ch + 3 loaded
+    window(v0, pb ^ 1, 0);                          // past the last chunk: unused
+    mfma_half(ust + us * WINO_USTAGE, 1, v1);
+    us = u1;
   }
+
+  // ---- output transform in registers and store ---------------------------
+  if (p >= P) return;
+  const int OHW = g.OH * g.OW;
+  const int n = p / TT;
+  const int rr = p - n * TT;
+  const int ty = rr / g.TW;
+  const int tx = rr - ty * g.TW;
+  const int oy = 2 * ty, ox = 2 * tx;
+  const bool yok = oy + 1 < g.OH, xok = ox + 1 < g.OW;
+  const bool pairs = (g.OW & 1) == 0;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int oc = ocb * 64 + 32 * og + 16 * blk + 4 * lk + r;
+      if (oc >= g.OC) continue;
+      float s0[4], s1[4];                           // s = A^T M
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        s0[b] = acc[b][blk][r] + acc[4 + b][blk][r] + acc[8 + b][blk][r];
+        s1[b] = acc[4 + b][blk][r] - acc[8 + b][blk][r] - acc[12 + b][blk][r];
+      }
+      float out[4] = {s0[0] + s0[1] + s0[2], s0[1] - s0[2] - s0[3],
+                      s1[0] + s1[1] + s1[2], s1[1] - s1[2] - s1[3]};
+      float* dst;
+      if (SPLIT) {
+        dst = g.y + ((size_t)slice * g.OC + oc) * ((size_t)g.N * OHW) + (size_t)n * OHW;
+      } else {
+        dst = g.y + ((size_t)n * g.OC + oc) * OHW;
+        const float b = Epi::bias == 1 ? g.bias[oc] : 0.f;
+        const float* res = Epi::residual ? g.R + ((size_t)n * g.OC + oc) * OHW : nullptr;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int py = oy + (e >> 1), px = ox + (e & 1);
+          const bool ok = (e & 2 ? yok : true) && (e & 1 ? xok : true);
+          float v = Epi::apply(out[e], b);
+          if (Epi::residual) v = Epi::post(v, ok ? res[py * g.OW + px] : 0.f);
+          out[e] = v;
+        }
+      }
+#pragma unroll
+      for (int e2 = 0; e2 < 2; ++e2) {
+        if (e2 == 1 && !yok) break;
+        float* row = dst + (oy + e2) * g.OW + ox;
+        if (pairs && xok) {
+          *reinterpret_cast<float2*>(row) = make_float2(out[2 * e2], out[2 * e2 + 1]);
+        } else {
+          row[0] = out[2 * e2];
+          if (xok) row[1] = out[2 * e2 + 1];
+        }
+      }
+    }
 }
 
 }  // namespace mdlc

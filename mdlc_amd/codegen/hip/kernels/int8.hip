@@ -43,13 +43,6 @@ struct QGemmArgs {
   float res_mult, acc_mult;       // EPI 2 multipliers of the residual and of the codes
 };
 
-// Raw buffer resource over [p, p + bytes): a load whose offset is at or
-// beyond `bytes` returns zeros instead of touching memory.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_over(const void* p, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
-}
-constexpr int kOutside = 0x7ffffff0;   // an offset past every buffer (sizes < 2^31)
-
 template <int BYTES> __device__ __forceinline__ void buffer_gather(__amdgpu_buffer_rsrc_t r, int off,
                                                                    i8* dst) {
   if (BYTES == 16) {
