@@ -214,9 +214,11 @@ class HipCodegen(Int8LoweringMixin):
             self._lower_conv_smallc(g, node, geo, has_bias)
             return
         # the Winograd kernel reads its input through a buffer resource of
-        # byte offsets below 2^31 (offsets at 0x7ffffff0 read as zeros)
+        # byte offsets below 2^31 (offsets at 0x7ffffff0 read as zeros) and
+        # divides tile indices below 2^21 in float
         if (self.conv_mode == "implicit" and self.winograd and wino_fits(geo)
                 and geo["N"] * geo["C"] * geo["H"] * geo["W"] * 4 < 0x7ffffff0
+                and geo["N"] * -(-geo["OH"] // 2) * -(-geo["OW"] // 2) < 2 ** 21
                 and (self.winograd is True or wino_pays(
                     geo["OC"], geo["N"] * -(-geo["OH"] // 2) * -(-geo["OW"] // 2), geo["C"]))):
             self._lower_wino(g, node, geo, has_bias)

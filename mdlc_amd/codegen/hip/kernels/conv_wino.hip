@@ -77,6 +77,16 @@ constexpr int WINO_PMAX = 704;                        // input patch floats per 
 constexpr int WINO_PSTR = WINO_PMAX + 32;             // patch stride per channel (banks apart)
 constexpr int WINO_PBUF = 8 * WINO_PSTR;              // one chunk's patch
 
+// n / d for 0 <= n < 2^21 and 0 < d < 2^21, given inv = rcp(d): the float
+// quotient is within one of the true one, and one correction each way
+// makes it exact (a 32-bit integer division costs some twenty VALU
+// instructions, several at quarter rate).
+__device__ __forceinline__ int wino_div(int n, int d, float inv) {
+  int q = (int)((float)n * inv);
+  const int r = n - __mul24(q, d);
+  return q + (r >= d) - (r < 0);
+}
+
 // PL: patch loads per lane (one channel per wave), ceil(largest patch / 64)
 // <= WINO_PMAX / 64.
 template <bool SPLIT, int PL, class Epi>
@@ -93,10 +103,10 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
   const int li = lane & 15;
   const int lk = lane >> 4;
 
-  const int P = g.N * g.TH * g.TW;
-  const int tiles_n = (P + 63) / 64;
-  const int ocb = blockIdx.x / tiles_n;
-  const int t0 = (blockIdx.x % tiles_n) * 64;
+  const int P = g.N * g.TH * g.TW;                  // < 2^21 (checked by the host)
+  const int tiles_n = (P + 63) >> 6;
+  const int ocb = wino_div(blockIdx.x, tiles_n, __builtin_amdgcn_rcpf((float)tiles_n));
+  const int t0 = (blockIdx.x - ocb * tiles_n) * 64;
   const int slice = SPLIT ? blockIdx.y : 0;
   const int chunk0 = slice * g.nchunk;
   const int HW = g.H * g.W;
@@ -108,47 +118,46 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
   // each WP = 2 TW + 2 columns wide starting at column -PL; positions outside
   // the image hold zero. The segments are stacked: segment 0 holds rows
   // rlo0 .. (its last), the others rows -PT .. (their last), whole images
-  // 2 TH + 2 rows.
+  // SR = 2 TH + 2 rows.
   const int TT = g.TH * g.TW;
   const int WP = 2 * g.TW + 2;
-  const int nfirst = t0 / TT;
+  const int SR = 2 * g.TH + 2;
+  const float iTT = __builtin_amdgcn_rcpf((float)TT), iTW = __builtin_amdgcn_rcpf((float)g.TW);
+  const float iWP = __builtin_amdgcn_rcpf((float)WP), iSR = __builtin_amdgcn_rcpf((float)SR);
+  const int nfirst = wino_div(t0, TT, iTT);
   const int plast = min(t0 + 63, P - 1);
-  const int nlast = plast / TT;
-  const int rlo0 = 2 * ((t0 - nfirst * TT) / g.TW) - g.PT;
-  const int rhil = 2 * ((plast - nlast * TT) / g.TW) + 3 - g.PT;
+  const int nlast = wino_div(plast, TT, iTT);
+  const int rlo0 = 2 * wino_div(t0 - nfirst * TT, g.TW, iTW) - g.PT;
+  const int rhil = 2 * wino_div(plast - nlast * TT, g.TW, iTW) + 3 - g.PT;
   const int rows0 = (nlast == nfirst ? rhil : 2 * g.TH + 1 - g.PT) - rlo0 + 1;
-  const int seg = (2 * g.TH + 2) * WP;
+  const int seg = SR * WP;
   const int PS = rows0 * WP + (nlast > nfirst ? (nlast - nfirst - 1) * seg + (rhil + g.PT + 1) * WP : 0);
 
-  const int p = t0 + 16 * tg + li;                  // the lane's tile
-  int wbase;
-  {
-    const int pc = p < P ? p : t0;                  // tiles past the batch: any window, never stored
-    const int n = pc / TT;
-    const int r = pc - n * TT;
-    const int ty = r / g.TW;
-    const int tx = r - ty * g.TW;
-    const int sg = n - nfirst;
-    wbase = (sg == 0 ? (2 * ty - g.PT - rlo0) * WP : rows0 * WP + (sg - 1) * seg + 2 * ty * WP) + 2 * tx;
-  }
+  // the lane's tile: image n, tile row ty, tile column tx
+  const int p = t0 + 16 * tg + li;
+  const int pc = p < P ? p : t0;                    // tiles past the batch: any window, never stored
+  const int n = wino_div(pc, TT, iTT);
+  const int ty = wino_div(pc - n * TT, g.TW, iTW);
+  const int tx = pc - n * TT - ty * g.TW;
+  const int wbase = (n == nfirst ? (2 * ty - g.PT - rlo0) * WP
+                                 : rows0 * WP + (n - nfirst - 1) * seg + 2 * ty * WP) + 2 * tx;
   // the lane's patch elements lane + 64 i: byte offset of the value from
   // the channel's plane in image 0, or kOutside (a zero) outside the image
   // or past the patch
   int poff[PL];
 #pragma unroll
   for (int i = 0; i < PL; ++i) {
+    // element e is row q, column e - q WP of the stacked patch (segments
+    // hold whole rows)
     const int e = i * 64 + lane;
-    int sg, row, col;
-    if (e < rows0 * WP) {
-      sg = 0;
-      row = rlo0 + e / WP;
-      col = e - (e / WP) * WP;
-    } else {
-      const int e1 = e - rows0 * WP;
-      sg = 1 + e1 / seg;
-      const int e2 = e1 - (e1 / seg) * seg;
-      row = e2 / WP - g.PT;
-      col = e2 - (e2 / WP) * WP;
+    const int q = wino_div(e, WP, iWP);
+    const int col = e - q * WP;
+    int sg = 0, row = rlo0 + q;
+    if (q >= rows0) {
+      const int R = q - rows0;
+      const int s1 = wino_div(R, SR, iSR);
+      sg = 1 + s1;
+      row = R - s1 * SR - g.PT;
     }
     const int ix = col - g.PL;
     const bool ok = e < PS && (unsigned)row < (unsigned)g.H && (unsigned)ix < (unsigned)g.W;
@@ -285,20 +294,25 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
   }
 
   // ---- output transform in registers and store ---------------------------
+  // Output channel oc0 + 16 blk + r of the lane's tile; one base address a
+  // lane, channels a fixed stride apart. When every tile has all four
+  // pixels (even OH and OW) the pixel pairs are 8-byte aligned and stored
+  // (and the residual read) without conditions.
   if (p >= P) return;
   const int OHW = g.OH * g.OW;
-  const int n = p / TT;
-  const int rr = p - n * TT;
-  const int ty = rr / g.TW;
-  const int tx = rr - ty * g.TW;
   const int oy = 2 * ty, ox = 2 * tx;
   const bool yok = oy + 1 < g.OH, xok = ox + 1 < g.OW;
-  const bool pairs = (g.OW & 1) == 0;
+  const bool full = ((g.OH | g.OW) & 1) == 0;
+  const int oc0 = ocb * 64 + 32 * og + 4 * lk;
+  const size_t ocs = SPLIT ? (size_t)g.N * OHW : (size_t)OHW;   // stride between channels
+  float* yb = g.y + (SPLIT ? ((size_t)slice * g.OC + oc0) * ocs + (size_t)n * OHW
+                           : ((size_t)n * g.OC + oc0) * OHW) + oy * g.OW + ox;
+  const float* rb = Epi::residual ? g.R + ((size_t)n * g.OC + oc0) * OHW + oy * g.OW + ox : nullptr;
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int oc = ocb * 64 + 32 * og + 16 * blk + 4 * lk + r;
+      const int oc = oc0 + 16 * blk + r;
       if (oc >= g.OC) continue;
       float s0[4], s1[4];                           // s = A^T M
 #pragma unroll
@@ -308,32 +322,37 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
       }
       float out[4] = {s0[0] + s0[1] + s0[2], s0[1] - s0[2] - s0[3],
                       s1[0] + s1[1] + s1[2], s1[1] - s1[2] - s1[3]};
-      float* dst;
-      if (SPLIT) {
-        dst = g.y + ((size_t)slice * g.OC + oc) * ((size_t)g.N * OHW) + (size_t)n * OHW;
-      } else {
-        dst = g.y + ((size_t)n * g.OC + oc) * OHW;
+      float* d = yb + (16 * blk + r) * ocs;
+      if (!SPLIT) {
         const float b = Epi::bias == 1 ? g.bias[oc] : 0.f;
-        const float* res = Epi::residual ? g.R + ((size_t)n * g.OC + oc) * OHW : nullptr;
+        float rv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (Epi::residual) {
+          const float* rr = rb + (16 * blk + r) * OHW;
+          if (full) {
+            const float2 r0 = *reinterpret_cast<const float2*>(rr);
+            const float2 r1 = *reinterpret_cast<const float2*>(rr + g.OW);
+            rv[0] = r0.x; rv[1] = r0.y; rv[2] = r1.x; rv[3] = r1.y;
+          } else {
+            rv[0] = rr[0];
+            if (xok) rv[1] = rr[1];
+            if (yok) rv[2] = rr[g.OW];
+            if (xok && yok) rv[3] = rr[g.OW + 1];
+          }
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int py = oy + (e >> 1), px = ox + (e & 1);
-          const bool ok = (e & 2 ? yok : true) && (e & 1 ? xok : true);
-          float v = Epi::apply(out[e], b);
-          if (Epi::residual) v = Epi::post(v, ok ? res[py * g.OW + px] : 0.f);
-          out[e] = v;
+          out[e] = Epi::apply(out[e], b);
+          if (Epi::residual) out[e] = Epi::post(out[e], rv[e]);
         }
       }
-#pragma unroll
-      for (int e2 = 0; e2 < 2; ++e2) {
-        if (e2 == 1 && !yok) break;
-        float* row = dst + (oy + e2) * g.OW + ox;
-        if (pairs && xok) {
-          *reinterpret_cast<float2*>(row) = make_float2(out[2 * e2], out[2 * e2 + 1]);
-        } else {
-          row[0] = out[2 * e2];
-          if (xok) row[1] = out[2 * e2 + 1];
-        }
+      if (full) {
+        *reinterpret_cast<float2*>(d) = make_float2(out[0], out[1]);
+        *reinterpret_cast<float2*>(d + g.OW) = make_float2(out[2], out[3]);
+      } else {
+        d[0] = out[0];
+        if (xok) d[1] = out[1];
+        if (yok) d[g.OW] = out[2];
+        if (xok && yok) d[g.OW + 1] = out[3];
       }
     }
 }
