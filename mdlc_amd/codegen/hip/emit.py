@@ -864,20 +864,20 @@ def wino_pack_filters(u: np.ndarray, OCP: int, CP: int) -> np.ndarray:
     """U[16][OC][C] -> the Winograd kernel's LDS images (zero padded): one
     contiguous 32 KB block per (64-channel output block, 8-channel chunk),
     laid out as the kernel's A operands are read,
-    [OCP/64][CP/8][og 2][blk 2][j 2][lane 64][slot 4][4]: lane l = 16 lk + li
-    of the wave with channel group og holds U[xi][oc][k] for
-    oc = 32 og + 16 blk + li, k = lk + 4 j, all 16 positions xi = 4 q + e as
-    four 16-byte quartets; quartet q sits in slot q ^ sw(l),
-    sw(l) = ((l >> 1) ^ (l >> 3)) & 3, so that the 16-byte reads of any 8 or
+    [OCP/64][CP/8][h 2][blk 4][j 2][lane 64][slot 2][4]: lane l = 16 lk + li
+    of a wave of half h holds U[xi][oc][k] for oc = 16 blk + li,
+    k = lk + 4 j and the eight positions xi = 8 h + 4 q + e of rows 2h, 2h + 1
+    as two 16-byte quartets; quartet q sits in slot q ^ sw(l),
+    sw(l) = ((l >> 2) ^ (l >> 3)) & 1, so that the 16-byte reads of any 8 or
     16 consecutive lanes hit distinct banks."""
     full = np.zeros((16, OCP, CP), np.float32)
     full[:, :u.shape[1], :u.shape[2]] = u
-    # axes: q, e, ocb, og, blk, li, chunk, j, lk
-    v = full.reshape(4, 4, OCP // 64, 2, 2, 16, CP // 8, 2, 4)
-    img = v.transpose(2, 6, 3, 4, 7, 8, 5, 0, 1).reshape(OCP // 64, CP // 8, 2, 2, 2, 64, 4, 4)
+    # axes: h, q, e, ocb, blk, li, chunk, j, lk
+    v = full.reshape(2, 2, 4, OCP // 64, 4, 16, CP // 8, 2, 4)
+    img = v.transpose(3, 6, 0, 4, 7, 8, 5, 1, 2).reshape(OCP // 64, CP // 8, 2, 4, 2, 64, 2, 4)
     lanes = np.arange(64)
-    sw = ((lanes >> 1) ^ (lanes >> 3)) & 3
-    slot_of = np.arange(4)[None, :] ^ sw[:, None]           # [lane][slot] -> quartet held
+    sw = ((lanes >> 2) ^ (lanes >> 3)) & 1
+    slot_of = np.arange(2)[None, :] ^ sw[:, None]           # [lane][slot] -> quartet held
     img = img[:, :, :, :, :, lanes[:, None], slot_of, :]
     return np.ascontiguousarray(img)
 

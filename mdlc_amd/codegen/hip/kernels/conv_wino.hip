@@ -15,24 +15,27 @@
 // of the direct convolution's multiply-adds.
 //
 // A workgroup of eight waves (two per SIMD) owns 64 output channels x 64
-// tiles. Wave w = 2 tg + og owns ALL 16 positions of the 32 output channels
-// 32 og .. 32 og + 31 x the 16 tiles 16 tg .. 16 tg + 15, on
-// v_mfma_f32_16x16x4f32 (16 positions x 2 channel blocks of 16 = 32
-// accumulators of 4, 128 registers a lane). In that instruction lane
+// tiles. Wave w = 4 h + tg owns the eight positions of rows a = 2h, 2h + 1
+// of all 64 output channels x the 16 tiles 16 tg .. 16 tg + 15, on
+// v_mfma_f32_16x16x4f32 (8 positions x 4 channel blocks of 16 = 32
+// accumulators of 4, 128 registers a lane); waves tg and tg + 4 (the two
+// halves of the same tiles) share a SIMD. In that instruction lane
 // l = 16 lk + li supplies B[k = lk][li]; k-step j (0, 1) of an 8-channel
-// chunk takes channel lk + 4 j, so a lane's B operands are the V values of
-// ONE window, tile 16 tg + li and channel lk + 4 j: the lane transforms that
-// window itself and feeds the values straight to the matrix core. Its A
-// operand is U[xi][oc = 32 og + 16 blk + li][lk + 4 j]; the filters are
-// transformed on the host (G g G^T, rounded once from float64) and packed
-// per (channel block, chunk) as a 32 KB image in exactly the order the lanes
-// read it, [og][blk][j][lane][16 positions], each lane's 16 values four
-// 16-byte quartets in slots swizzled by lane so that any 8 or 16
-// consecutive lanes' reads hit distinct banks: one chunk's A operands are
-// eight 16-byte LDS reads a lane, and the copy of the image into LDS is a
-// linear 16-byte-per-thread stream. The output transform needs all 16
-// positions of an (oc, tile), which the lane holds (D[4 lk + r][li] of each
-// block), so it runs in registers and the 2x2 pixels are stored directly.
+// chunk takes channel lk + 4 j, so a lane's B operands are V values of ONE
+// window, tile 16 tg + li and channel lk + 4 j: the lane transforms that
+// window itself, only the two rows of V its half needs (16 additions), and
+// feeds the values straight to the matrix core. Its A operand is
+// U[xi][oc = 16 blk + li][lk + 4 j]; the filters are transformed on the
+// host (G g G^T, rounded once from float64) and packed per (channel block,
+// chunk) as a 32 KB image in exactly the order the lanes read it,
+// [h][blk][j][lane][8 positions], each lane's 8 values two 16-byte quartets
+// in slots swizzled by lane so that any 8 or 16 consecutive lanes' reads hit
+// distinct banks: one chunk's A operands are sixteen 16-byte LDS reads a
+// lane, and the copy of the image into LDS is a linear 16-byte-per-thread
+// stream. The output transform is linear in M, so each half forms its own
+// partial Y_h = A^T M_h A in registers; after the channel loop the halves
+// exchange partials through LDS (each finishes two of the four channel
+// blocks, adding Y_0 + Y_1 in that order) and store the 2x2 pixels.
 //
 // The input reaches the windows through an LDS patch per channel of the
 // rows the workgroup's 64 tiles read, filled with coalesced loads (wave w
@@ -46,10 +49,10 @@
 //   barrier;
 //   J1: transform window (c+1, j = 0), run the 32 j = 1 MFMAs.
 // Each phase computes the V values the next phase needs into the registers
-// the current phase does not read, so V takes 32 registers. The staging
+// the current phase does not read, so V takes 16 registers. The staging
 // (a wave's channel of the patch and its pieces of the filter image, stored
 // from registers into LDS, then the global loads of a later chunk) runs in
-// J0 on waves 0-3 and in J1 on waves 4-7, which share SIMDs with them. Three
+// J0 on waves 0-3 and in J1 on waves 4-7, their SIMD partners. Three
 // filter stages and two patch buffers make the one barrier enough: a stage
 // or buffer is rewritten only after the barrier that follows its last reads.
 //
@@ -77,6 +80,8 @@ constexpr int WINO_PMAX = 704;                        // input patch floats per 
 constexpr int WINO_PSTR = WINO_PMAX + 32;             // patch stride per channel (banks apart)
 constexpr int WINO_PBUF = 8 * WINO_PSTR;              // one chunk's patch
 
+template <int V> struct WinoHalf { static constexpr int value = V; };
+
 // n / d for 0 <= n < 2^21 and 0 < d < 2^21, given inv = rcp(d): the float
 // quotient is within one of the true one, and one correction each way
 // makes it exact (a 32-bit integer division costs some twenty VALU
@@ -98,8 +103,8 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int og = wave & 1;
-  const int tg = wave >> 1;
+  const int h = wave >> 2;                          // position rows 2h, 2h + 1
+  const int tg = wave & 3;
   const int li = lane & 15;
   const int lk = lane >> 4;
 
@@ -195,166 +200,223 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) st4(ust + stage * WINO_USTAGE + (tid + i * WINO_NT) * 4, ur[i]);
   };
-  // V = B^T d B of the lane's window for channel lk + 4 j of a chunk (zero
-  // past the last channel: its patch is zeros)
-  auto window = [&](float (&v)[16], int buf, int j) {
-    const float* pj = pbuf + buf * WINO_PBUF + (lk + 4 * j) * WINO_PSTR + wbase;
-    float d[16];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int b = 0; b < 4; b += 2) {
-        const float2 q = *reinterpret_cast<const float2*>(pj + a * WP + b);
-        d[4 * a + b] = q.x;
-        d[4 * a + b + 1] = q.y;
-      }
-    float t[16];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      t[b] = d[b] - d[8 + b];
-      t[4 + b] = d[4 + b] + d[8 + b];
-      t[8 + b] = d[8 + b] - d[4 + b];
-      t[12 + b] = d[4 + b] - d[12 + b];
-    }
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      v[4 * a + 0] = t[4 * a] - t[4 * a + 2];
-      v[4 * a + 1] = t[4 * a + 1] + t[4 * a + 2];
-      v[4 * a + 2] = t[4 * a + 2] - t[4 * a + 1];
-      v[4 * a + 3] = t[4 * a + 1] - t[4 * a + 3];
-    }
-  };
-
-  // A operands: the lane's 16 positions of (blk, j) are four 16-byte
-  // quartets of the filter image, quartet q in slot q ^ sw
-  const int sw = ((lane >> 1) ^ (lane >> 3)) & 3;
-  int qoff[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) qoff[q] = (og * 4 * 64 + lane) * 16 + ((q ^ sw) << 2);
-  floatx4 acc[16][2];
-#pragma unroll
-  for (int xi = 0; xi < 16; ++xi)
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[xi][blk][r] = 0.f;
-  auto mfma_half = [&](const float* st, int j, const float (&v)[16]) {
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      float4 a[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) a[q] = ld4(st + (blk * 2 + j) * 64 * 16 + qoff[q]);
-#pragma unroll
-      for (int xi = 0; xi < 16; ++xi)
-        acc[xi][blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(pick(a[xi >> 2], xi & 3), v[xi],
-                                                             acc[xi][blk], 0, 0, 0);
-    }
-  };
-
-  // Waves 0-3 stage in J0, waves 4-7 (their SIMD partners) in J1, so that
-  // on every SIMD one wave's stores and loads overlap the other's MFMAs. A
-  // wave stores its own channel of the patch and its own pieces of the
-  // filter image, so the two groups' stores of one chunk never overlap;
-  // waves 4-7 run one chunk further ahead (they store chunk c+2 in J1 of
-  // chunk c, into the patch buffer and filter stage the barrier before J1
-  // has freed).
-  const bool early = wave < 4;
-  auto stage = [&](int buf, int ustage, int next) {
-    __builtin_amdgcn_sched_barrier(0);
-    store_x(buf);
-    store_u(ustage);
-    __builtin_amdgcn_sched_barrier(0);
-    load_x(chunk0 + min(next, g.nchunk - 1));
-    load_u(chunk0 + min(next, g.nchunk - 1));
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  load_x(chunk0);
-  load_u(chunk0);
-  store_x(0);
-  store_u(0);
-  load_x(chunk0 + min(1, g.nchunk - 1));
-  load_u(chunk0 + min(1, g.nchunk - 1));
-  if (!early) stage(1, 1, 2);
-  __syncthreads();
-  float v0[16], v1[16];
-  window(v0, 0, 0);
-  int us = 0;                                       // filter stage of chunk ch
-  for (int ch = 0; ch < g.nchunk; ++ch) {
-    const int pb = ch & 1;                          // patch buffer of chunk ch
-    const int u1 = us == 2 ? 0 : us + 1;            // filter stage of chunk ch + 1
-    const int u2 = u1 == 2 ? 0 : u1 + 1;            // and of chunk ch + 2
-    if (early) stage(pb ^ 1, u1, ch + 2);           // chunk ch + 1 in, ch + 2 loaded
-    window(v1, pb, 1);
-    mfma_half(ust + us * WINO_USTAGE, 0, v0);
-    __syncthreads();
-    if (!early) stage(pb, u2, ch + 3);              // chunk ch + 2 in, ch + 3 loaded
-    window(v0, pb ^ 1, 0);                          // past the last chunk: unused
-    mfma_half(ust + us * WINO_USTAGE, 1, v1);
-    us = u1;
-  }
-
-  // ---- output transform in registers and store ---------------------------
-  // Output channel oc0 + 16 blk + r of the lane's tile; one base address a
-  // lane, channels a fixed stride apart. When every tile has all four
-  // pixels (even OH and OW) the pixel pairs are 8-byte aligned and stored
-  // (and the residual read) without conditions.
-  if (p >= P) return;
-  const int OHW = g.OH * g.OW;
-  const int oy = 2 * ty, ox = 2 * tx;
-  const bool yok = oy + 1 < g.OH, xok = ox + 1 < g.OW;
-  const bool full = ((g.OH | g.OW) & 1) == 0;
-  const int oc0 = ocb * 64 + 32 * og + 4 * lk;
-  const size_t ocs = SPLIT ? (size_t)g.N * OHW : (size_t)OHW;   // stride between channels
-  float* yb = g.y + (SPLIT ? ((size_t)slice * g.OC + oc0) * ocs + (size_t)n * OHW
-                           : ((size_t)n * g.OC + oc0) * OHW) + oy * g.OW + ox;
-  const float* rb = Epi::residual ? g.R + ((size_t)n * g.OC + oc0) * OHW + oy * g.OW + ox : nullptr;
-#pragma unroll
-  for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int oc = oc0 + 16 * blk + r;
-      if (oc >= g.OC) continue;
-      float s0[4], s1[4];                           // s = A^T M
-#pragma unroll
+  // Everything from here on depends on the half: it is compiled once per
+  // half (H), so that the transform's formulas and the staging phase are
+  // fixed in each copy instead of selected per instruction.
+  auto run = [&](auto HC) {
+    constexpr int H = decltype(HC)::value;
+    // rows 2h, 2h + 1 of V = B^T d B of the lane's window for channel lk + 4 j
+    // of a chunk (zero past the last channel: its patch is zeros); they need
+    // window rows h .. h + 2
+    auto window = [&](float (&v)[8], int buf, int j) {
+      const float* pj = pbuf + buf * WINO_PBUF + (lk + 4 * j) * WINO_PSTR + wbase + H * WP;
+      float d[12];
+  #pragma unroll
+      for (int a = 0; a < 3; ++a)
+  #pragma unroll
+        for (int b = 0; b < 4; b += 2) {
+          const float2 q = *reinterpret_cast<const float2*>(pj + a * WP + b);
+          d[4 * a + b] = q.x;
+          d[4 * a + b + 1] = q.y;
+        }
+      float t[8];                                     // rows 2h, 2h + 1 of B^T d
+  #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        s0[b] = acc[b][blk][r] + acc[4 + b][blk][r] + acc[8 + b][blk][r];
-        s1[b] = acc[4 + b][blk][r] - acc[8 + b][blk][r] - acc[12 + b][blk][r];
+        if (H == 0) {
+          t[b] = d[b] - d[8 + b];                     // d0 - d2
+          t[4 + b] = d[4 + b] + d[8 + b];             // d1 + d2
+        } else {
+          t[b] = d[4 + b] - d[b];                     // d2 - d1
+          t[4 + b] = d[b] - d[8 + b];                 // d1 - d3
+        }
       }
-      float out[4] = {s0[0] + s0[1] + s0[2], s0[1] - s0[2] - s0[3],
-                      s1[0] + s1[1] + s1[2], s1[1] - s1[2] - s1[3]};
-      float* d = yb + (16 * blk + r) * ocs;
-      if (!SPLIT) {
-        const float b = Epi::bias == 1 ? g.bias[oc] : 0.f;
-        float rv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (Epi::residual) {
-          const float* rr = rb + (16 * blk + r) * OHW;
-          if (full) {
-            const float2 r0 = *reinterpret_cast<const float2*>(rr);
-            const float2 r1 = *reinterpret_cast<const float2*>(rr + g.OW);
-            rv[0] = r0.x; rv[1] = r0.y; rv[2] = r1.x; rv[3] = r1.y;
-          } else {
-            rv[0] = rr[0];
-            if (xok) rv[1] = rr[1];
-            if (yok) rv[2] = rr[g.OW];
-            if (xok && yok) rv[3] = rr[g.OW + 1];
+  #pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        v[4 * a + 0] = t[4 * a] - t[4 * a + 2];
+        v[4 * a + 1] = t[4 * a + 1] + t[4 * a + 2];
+        v[4 * a + 2] = t[4 * a + 2] - t[4 * a + 1];
+        v[4 * a + 3] = t[4 * a + 1] - t[4 * a + 3];
+      }
+    };
+
+    // A operands: the lane's 8 positions of (blk, j) are two 16-byte
+    // quartets of the filter image, quartet q in slot q ^ sw
+    const int sw = ((lane >> 2) ^ (lane >> 3)) & 1;
+    int qoff[2];
+  #pragma unroll
+    for (int q = 0; q < 2; ++q) qoff[q] = H * 8 * 512 + lane * 8 + ((q ^ sw) << 2);
+    floatx4 acc[8][4];
+  #pragma unroll
+    for (int x = 0; x < 8; ++x)
+  #pragma unroll
+      for (int blk = 0; blk < 4; ++blk)
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) acc[x][blk][r] = 0.f;
+    auto mfma_half = [&](const float* st, int j, const float (&v)[8]) {
+  #pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        float4 a[2];
+  #pragma unroll
+        for (int q = 0; q < 2; ++q) a[q] = ld4(st + (blk * 2 + j) * 512 + qoff[q]);
+  #pragma unroll
+        for (int x = 0; x < 8; ++x)
+          acc[x][blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(pick(a[x >> 2], x & 3), v[x],
+                                                              acc[x][blk], 0, 0, 0);
+      }
+    };
+
+    // Waves 0-3 stage in J0, waves 4-7 (their SIMD partners) in J1, so that
+    // on every SIMD one wave's stores and loads overlap the other's MFMAs. A
+    // wave stores its own channel of the patch and its own pieces of the
+    // filter image, so the two groups' stores of one chunk never overlap;
+    // waves 4-7 run one chunk further ahead (they store chunk c+2 in J1 of
+    // chunk c, into the patch buffer and filter stage the barrier before J1
+    // has freed).
+    constexpr bool early = H == 0;
+    auto stage = [&](int buf, int ustage, int next) {
+      __builtin_amdgcn_sched_barrier(0);
+      store_x(buf);
+      store_u(ustage);
+      __builtin_amdgcn_sched_barrier(0);
+      load_x(chunk0 + min(next, g.nchunk - 1));
+      load_u(chunk0 + min(next, g.nchunk - 1));
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    load_x(chunk0);
+    load_u(chunk0);
+    store_x(0);
+    store_u(0);
+    load_x(chunk0 + min(1, g.nchunk - 1));
+    load_u(chunk0 + min(1, g.nchunk - 1));
+    if (!early) stage(1, 1, 2);
+    __syncthreads();
+    float v0[8], v1[8];
+    window(v0, 0, 0);
+    int us = 0;                                       // filter stage of chunk ch
+    for (int ch = 0; ch < g.nchunk; ++ch) {
+      const int pb = ch & 1;                          // patch buffer of chunk ch
+      const int u1 = us == 2 ? 0 : us + 1;            // filter stage of chunk ch + 1
+      const int u2 = u1 == 2 ? 0 : u1 + 1;            // and of chunk ch + 2
+      if (early) stage(pb ^ 1, u1, ch + 2);           // chunk ch + 1 in, ch + 2 loaded
+      window(v1, pb, 1);
+      mfma_half(ust + us * WINO_USTAGE, 0, v0);
+      __syncthreads();
+      if (!early) stage(pb, u2, ch + 3);              // chunk ch + 2 in, ch + 3 loaded
+      window(v0, pb ^ 1, 0);                          // past the last chunk: unused
+      mfma_half(ust + us * WINO_USTAGE, 1, v1);
+      us = u1;
+    }
+
+    // ---- output transform: partial Y of each half, summed through LDS --------
+    // acc[4a' + b][blk][r] holds M at row a = 2h + a', column b, for
+    // oc = 16 blk + 4 lk + r and the lane's tile (the 16x16x4 accumulator
+    // layout). s = A^T M restricted to the half's two rows, Y_h = s A. Half h
+    // finishes channel blocks 2h, 2h + 1: it hands its partials of the other
+    // half's blocks over through LDS (the stages are no longer read).
+    float y[4][4][4];                                 // [blk][r][pixel]
+  #pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+  #pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float s0[4], s1[4];
+  #pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const float m0 = acc[b][blk][r], m1 = acc[4 + b][blk][r];
+          if (H == 0) {                               // rows 0, 1: A^T columns (1, 0), (1, 1)
+            s0[b] = m0 + m1;
+            s1[b] = m1;
+          } else {                                    // rows 2, 3: (1, -1), (0, -1)
+            s0[b] = m0;
+            s1[b] = -m0 - m1;
           }
         }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          out[e] = Epi::apply(out[e], b);
-          if (Epi::residual) out[e] = Epi::post(out[e], rv[e]);
+        y[blk][r][0] = s0[0] + s0[1] + s0[2];
+        y[blk][r][1] = s0[1] - s0[2] - s0[3];
+        y[blk][r][2] = s1[0] + s1[1] + s1[2];
+        y[blk][r][3] = s1[1] - s1[2] - s1[3];
+      }
+    __syncthreads();
+    float* xw = ust + H * 8192;                       // this half's partials for the other half
+  #pragma unroll
+    for (int bb = 0; bb < 2; ++bb)
+  #pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int blk = 2 * (1 - H) + bb;
+        st4(xw + (((tg * 2 + bb) * 4 + r) * 64 + lane) * 4,
+            make_float4(y[blk][r][0], y[blk][r][1], y[blk][r][2], y[blk][r][3]));
+      }
+    __syncthreads();
+    const float* xr = ust + (1 - H) * 8192;
+
+    // Output channel oc0 + 16 bb + r of the lane's tile; one base address a
+    // lane, channels a fixed stride apart. When every tile has all four
+    // pixels (even OH and OW) the pixel pairs are 8-byte aligned and stored
+    // (and the residual read) without conditions.
+    if (p >= P) return;
+    const int OHW = g.OH * g.OW;
+    const int oy = 2 * ty, ox = 2 * tx;
+    const bool yok = oy + 1 < g.OH, xok = ox + 1 < g.OW;
+    const bool full = ((g.OH | g.OW) & 1) == 0;
+    const int oc0 = ocb * 64 + 32 * H + 4 * lk;
+    const size_t ocs = SPLIT ? (size_t)g.N * OHW : (size_t)OHW;   // stride between channels
+    float* yb = g.y + (SPLIT ? ((size_t)slice * g.OC + oc0) * ocs + (size_t)n * OHW
+                             : ((size_t)n * g.OC + oc0) * OHW) + oy * g.OW + ox;
+    const float* rb = Epi::residual ? g.R + ((size_t)n * g.OC + oc0) * OHW + oy * g.OW + ox : nullptr;
+  #pragma unroll
+    for (int bb = 0; bb < 2; ++bb)
+  #pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int oc = oc0 + 16 * bb + r;
+        if (oc >= g.OC) continue;
+        const float4 other = ld4(xr + (((tg * 2 + bb) * 4 + r) * 64 + lane) * 4);
+        const float* mine = y[2 * H + bb][r];
+        float out[4];                                 // Y_0 + Y_1
+        if (H == 0) {
+          out[0] = mine[0] + other.x; out[1] = mine[1] + other.y;
+          out[2] = mine[2] + other.z; out[3] = mine[3] + other.w;
+        } else {
+          out[0] = other.x + mine[0]; out[1] = other.y + mine[1];
+          out[2] = other.z + mine[2]; out[3] = other.w + mine[3];
+        }
+        float* d = yb + (16 * bb + r) * ocs;
+        if (!SPLIT) {
+          const float b = Epi::bias == 1 ? g.bias[oc] : 0.f;
+          float rv[4] = {0.f, 0.f, 0.f, 0.f};
+          if (Epi::residual) {
+            const float* rr = rb + (16 * bb + r) * OHW;
+            if (full) {
+              const float2 r0 = *reinterpret_cast<const float2*>(rr);
+              const float2 r1 = *reinterpret_cast<const float2*>(rr + g.OW);
+              rv[0] = r0.x; rv[1] = r0.y; rv[2] = r1.x; rv[3] = r1.y;
+            } else {
+              rv[0] = rr[0];
+              if (xok) rv[1] = rr[1];
+              if (yok) rv[2] = rr[g.OW];
+              if (xok && yok) rv[3] = rr[g.OW + 1];
+            }
+          }
+  #pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            out[e] = Epi::apply(out[e], b);
+            if (Epi::residual) out[e] = Epi::post(out[e], rv[e]);
+          }
+        }
+        if (full) {
+          *reinterpret_cast<float2*>(d) = make_float2(out[0], out[1]);
+          *reinterpret_cast<float2*>(d + g.OW) = make_float2(out[2], out[3]);
+        } else {
+          d[0] = out[0];
+          if (xok) d[1] = out[1];
+          if (yok) d[g.OW] = out[2];
+          if (xok && yok) d[g.OW + 1] = out[3];
         }
       }
-      if (full) {
-        *reinterpret_cast<float2*>(d) = make_float2(out[0], out[1]);
-        *reinterpret_cast<float2*>(d + g.OW) = make_float2(out[2], out[3]);
-      } else {
-        d[0] = out[0];
-        if (xok) d[1] = out[1];
-        if (yok) d[g.OW] = out[2];
-        if (xok && yok) d[g.OW + 1] = out[3];
-      }
-    }
+  };
+  if (h == 0) {
+    run(WinoHalf<0>());
+  } else {
+    run(WinoHalf<1>());
+  }
 }
 
 }  // namespace mdlc

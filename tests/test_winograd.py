@@ -111,21 +111,21 @@ def test_packed_filters_are_padded_to_whole_blocks_and_slices():
     # 25 chunks over 8 slices: 4 a slice, 7 slices (no empty one), 28 chunks packed
     assert (m["OCP"], m["nchunk"], l.grid[1], m["CP"]) == (192, 4, 7, 224)
     img = c.module.device_constants[l.inputs[0]]
-    assert img.shape == (3, 28, 2, 2, 2, 64, 4, 4)     # [ocb][chunk][og][blk][j][lane][slot][4]
+    assert img.shape == (3, 28, 2, 4, 2, 64, 2, 4)     # [ocb][chunk][h][blk][j][lane][slot][4]
     # undo the per-lane slot swizzle (slot s holds quartet s ^ sw), then back to [16][OCP][CP]
     lanes = np.arange(64)
-    sw = ((lanes >> 1) ^ (lanes >> 3)) & 3
-    img = img[:, :, :, :, :, lanes[:, None], np.arange(4)[None, :] ^ sw[:, None]]
-    # axes: ocb, chunk, og, blk, j, lk, li, q, e -> xi = 4q + e, oc = (ocb, og, blk, li), k = (chunk, j, lk)
-    u = img.reshape(3, 28, 2, 2, 2, 4, 16, 4, 4).transpose(7, 8, 0, 2, 3, 6, 1, 4, 5).reshape(16, 192, 224)
+    sw = ((lanes >> 2) ^ (lanes >> 3)) & 1
+    img = img[:, :, :, :, :, lanes[:, None], np.arange(2)[None, :] ^ sw[:, None]]
+    # axes: ocb, chunk, h, blk, j, lk, li, q, e -> xi = 8h + 4q + e, oc = (ocb, blk, li), k = (chunk, j, lk)
+    u = img.reshape(3, 28, 2, 4, 2, 4, 16, 2, 4).transpose(2, 7, 8, 0, 3, 6, 1, 4, 5).reshape(16, 192, 224)
     assert not u[:, 130:, :].any() and not u[:, :, 200:].any()
     w = wino_filter_transform(c.graph.initializers["w"])
     np.testing.assert_array_equal(u[:, :130, :200], w)
-    # the A operand lane 37 (lk 2, li 5) of the og = 1 wave reads for blk 0, j = 1 in
-    # quartet q = 2: positions 8-11 of oc 32 + 5 = 37, channel 8 * 3 + 2 + 4 = 30 of chunk 3
+    # the A operand lane 37 (lk 2, li 5) of a half-1 wave reads for blk 2, j = 1 in
+    # quartet q = 1: positions 12-15 of oc 32 + 5 = 37, channel 8 * 3 + 2 + 4 = 30 of chunk 3
     raw = c.module.device_constants[l.inputs[0]]
-    q, lane = 2, 37
-    slot = q ^ (((lane >> 1) ^ (lane >> 3)) & 3)
-    np.testing.assert_array_equal(raw[0, 3, 1, 0, 1, lane, slot], w[8:12, 37, 30])
+    q, lane = 1, 37
+    slot = q ^ (((lane >> 2) ^ (lane >> 3)) & 1)
+    np.testing.assert_array_equal(raw[0, 3, 1, 2, 1, lane, slot], w[12:16, 37, 30])
     (r,) = [r for r in c.module.plan if r.kind == "splitk_reduce"]
     assert r.meta["S"] == 7 and c.module.scratch_shapes[r.inputs[0]] == (7 * 130, 60)
