@@ -458,6 +458,16 @@ class HipCodegen(Int8LoweringMixin):
                    win: Optional[tuple] = None) -> None:
         """Append the GEMM launch (and, with split-K, its reduce launch)."""
         M, N, K = meta["M"], meta["N"], meta["K"]
+        # the kernel reads A, dense B and the conv gather's input through
+        # buffer resources of byte offsets below 2^31 - 16
+        nbytes = [4 * M * meta["lda"]]
+        if bmode <= 1:
+            nbytes.append(4 * K * max(meta.get("ldb", 0), N))
+        elif bmode == 3:
+            nbytes.append(4 * N // (meta["OH"] * meta["OW"]) * meta["Cin"] * meta["H"] * meta["W"])
+        if max(nbytes) >= 0x7ffffff0:
+            raise NotImplementedError(f"GEMM operands of {max(nbytes)} bytes exceed the kernel's "
+                                      "2 GiB buffer range")
         slices, chunk = split_slices(K, sched)
         tiles = -(-M // sched.BM) * -(-N // sched.BN)
         block = (sched.threads_per_block(), 1, 1)

@@ -211,16 +211,16 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
     auto window = [&](float (&v)[8], int buf, int j) {
       const float* pj = pbuf + buf * WINO_PBUF + (lk + 4 * j) * WINO_PSTR + wbase + H * WP;
       float d[12];
-  #pragma unroll
+#pragma unroll
       for (int a = 0; a < 3; ++a)
-  #pragma unroll
+#pragma unroll
         for (int b = 0; b < 4; b += 2) {
           const float2 q = *reinterpret_cast<const float2*>(pj + a * WP + b);
           d[4 * a + b] = q.x;
           d[4 * a + b + 1] = q.y;
         }
       float t[8];                                     // rows 2h, 2h + 1 of B^T d
-  #pragma unroll
+#pragma unroll
       for (int b = 0; b < 4; ++b) {
         if (H == 0) {
           t[b] = d[b] - d[8 + b];                     // d0 - d2
@@ -230,7 +230,7 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
           t[4 + b] = d[b] - d[8 + b];                 // d1 - d3
         }
       }
-  #pragma unroll
+#pragma unroll
       for (int a = 0; a < 2; ++a) {
         v[4 * a + 0] = t[4 * a] - t[4 * a + 2];
         v[4 * a + 1] = t[4 * a + 1] + t[4 * a + 2];
@@ -243,22 +243,22 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
     // quartets of the filter image, quartet q in slot q ^ sw
     const int sw = ((lane >> 2) ^ (lane >> 3)) & 1;
     int qoff[2];
-  #pragma unroll
+#pragma unroll
     for (int q = 0; q < 2; ++q) qoff[q] = H * 8 * 512 + lane * 8 + ((q ^ sw) << 2);
     floatx4 acc[8][4];
-  #pragma unroll
+#pragma unroll
     for (int x = 0; x < 8; ++x)
-  #pragma unroll
+#pragma unroll
       for (int blk = 0; blk < 4; ++blk)
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 4; ++r) acc[x][blk][r] = 0.f;
     auto mfma_half = [&](const float* st, int j, const float (&v)[8]) {
-  #pragma unroll
+#pragma unroll
       for (int blk = 0; blk < 4; ++blk) {
         float4 a[2];
-  #pragma unroll
+#pragma unroll
         for (int q = 0; q < 2; ++q) a[q] = ld4(st + (blk * 2 + j) * 512 + qoff[q]);
-  #pragma unroll
+#pragma unroll
         for (int x = 0; x < 8; ++x)
           acc[x][blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(pick(a[x >> 2], x & 3), v[x],
                                                               acc[x][blk], 0, 0, 0);
@@ -314,12 +314,12 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
     // finishes channel blocks 2h, 2h + 1: it hands its partials of the other
     // half's blocks over through LDS (the stages are no longer read).
     float y[4][4][4];                                 // [blk][r][pixel]
-  #pragma unroll
+#pragma unroll
     for (int blk = 0; blk < 4; ++blk)
-  #pragma unroll
+#pragma unroll
       for (int r = 0; r < 4; ++r) {
         float s0[4], s1[4];
-  #pragma unroll
+#pragma unroll
         for (int b = 0; b < 4; ++b) {
           const float m0 = acc[b][blk][r], m1 = acc[4 + b][blk][r];
           if (H == 0) {                               // rows 0, 1: A^T columns (1, 0), (1, 1)
@@ -337,9 +337,9 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
       }
     __syncthreads();
     float* xw = ust + H * 8192;                       // this half's partials for the other half
-  #pragma unroll
+#pragma unroll
     for (int bb = 0; bb < 2; ++bb)
-  #pragma unroll
+#pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int blk = 2 * (1 - H) + bb;
         st4(xw + (((tg * 2 + bb) * 4 + r) * 64 + lane) * 4,
@@ -362,9 +362,9 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
     float* yb = g.y + (SPLIT ? ((size_t)slice * g.OC + oc0) * ocs + (size_t)n * OHW
                              : ((size_t)n * g.OC + oc0) * OHW) + oy * g.OW + ox;
     const float* rb = Epi::residual ? g.R + ((size_t)n * g.OC + oc0) * OHW + oy * g.OW + ox : nullptr;
-  #pragma unroll
+#pragma unroll
     for (int bb = 0; bb < 2; ++bb)
-  #pragma unroll
+#pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int oc = oc0 + 16 * bb + r;
         if (oc >= g.OC) continue;
@@ -395,7 +395,7 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
               if (xok && yok) rv[3] = rr[g.OW + 1];
             }
           }
-  #pragma unroll
+#pragma unroll
           for (int e = 0; e < 4; ++e) {
             out[e] = Epi::apply(out[e], b);
             if (Epi::residual) out[e] = Epi::post(out[e], rv[e]);

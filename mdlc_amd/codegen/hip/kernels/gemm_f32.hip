@@ -121,8 +121,10 @@ __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0,
   // ---- A staging: addresses fixed per thread, advanced by k0 --------------
   constexpr int A_ELEMS = VA ? BM * BK / 4 : BM * BK;
   constexpr int A_PT = (A_ELEMS + NT - 1) / NT;
-  const float* a_ptr[A_PT];
-  int a_k[A_PT], a_lds[A_PT];
+  // A is read through a buffer resource: a masked element's offset is
+  // kOutside, which reads zero, so the loads need no branches
+  const __amdgpu_buffer_rsrc_t rsA = buffer_over(g.A, g.M * g.lda * 4);
+  int a_off[A_PT], a_k[A_PT], a_lds[A_PT];
   bool a_ok[A_PT];
 #pragma unroll
   for (int i = 0; i < A_PT; ++i) {
@@ -131,7 +133,7 @@ __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0,
     const int r = idx / cpr, kc = idx % cpr;
     const int kk = VA ? kc * 4 : kc;
     a_ok[i] = idx < A_ELEMS && m0 + r < g.M;
-    a_ptr[i] = g.A + (size_t)min(m0 + r, g.M - 1) * g.lda + kk;
+    a_off[i] = (min(m0 + r, g.M - 1) * g.lda + kk) * 4;
     a_k[i] = kk;
     a_lds[i] = r * LDA_S + kk;
   }
@@ -142,8 +144,9 @@ __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0,
   // dense: quads (BMODE 0) or scalars (BMODE 1) along n, LDS [k][n]
   constexpr int BD_ELEMS = BMODE == 0 ? BK * BN / 4 : BK * BN;
   constexpr int BD_PT = BT ? 1 : (BD_ELEMS + NT - 1) / NT;
-  const float* b_ptr[BD_PT];
-  int b_k[BD_PT], b_lds[BD_PT];
+  // dense B [K][ldb] through a buffer resource (masked elements read zero)
+  const __amdgpu_buffer_rsrc_t rsD = buffer_over(g.B, BT ? 0 : g.K * g.ldb * 4);
+  int b_off[BD_PT], b_k[BD_PT], b_lds[BD_PT];
   bool b_ok[BD_PT];
   float4 rb[BMODE == 0 ? BD_PT : 1];
   float rbs[BMODE == 1 ? BD_PT : 1];
@@ -155,7 +158,7 @@ __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0,
       const int kr = idx / cpr, nc = idx % cpr;
       const int nn = BMODE == 0 ? nc * 4 : nc;
       b_ok[i] = idx < BD_ELEMS && n0 + nn < g.N;
-      b_ptr[i] = g.B + (size_t)kr * g.ldb + min(n0 + nn, g.N - 1);
+      b_off[i] = (kr * g.ldb + min(n0 + nn, g.N - 1)) * 4;
       b_k[i] = kr;
       b_lds[i] = kr * LDB_S + nn;
     }
@@ -166,6 +169,18 @@ __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0,
   static_assert(!BT || (NT % BN == 0 && BK % (NT / BN) == 0), "conv gather needs NT % BN == 0");
   float rg[RPT];
   int g_base = 0, g_ih = -(1 << 28), g_iw = 0, g_row = 0, g_lds = 0;
+  int g_pix = 0;                                  // BMODE 3: the thread's first row, tap (0, 0)
+  // BMODE 3 reads the input through a buffer resource (out-of-image taps
+  // read zero from offset kOutside, the rows of a thread one channel plane
+  // apart through the scalar offset) and tracks the K tile's filter tap and
+  // first channel in scalars: load_tiles is called once per K tile, in order
+  const __amdgpu_buffer_rsrc_t rsB =
+      buffer_over(g.B, BMODE == 3 ? g.N / (g.OH * g.OW) * g.ximg * 4 : 0);
+  int g_tap = 0, g_c0 = 0;
+  if (BMODE == 3) {
+    g_tap = kbeg / g.Cin;
+    g_c0 = kbeg - g_tap * g.Cin;
+  }
   if (BT) {
     const int col = tid % BN;
     g_row = (tid / BN) * RPT;
@@ -180,44 +195,48 @@ __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0,
       g_base = n * g.ximg;
       g_ih = oh * Win::SH - Win::PT;
       g_iw = ow * Win::SW - Win::PL;
+      g_pix = g_base + g_row * (g.H * g.W) + g_ih * g.W + g_iw;
     }
   }
 
   auto load_tiles = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < A_PT; ++i) {
-      const bool ok = a_ok[i] && k0 + a_k[i] < kend;
+      const int off = a_ok[i] && k0 + a_k[i] < kend ? a_off[i] + k0 * 4 : kOutside;
       if (VA) {
-        ra[i] = ok ? ld4(a_ptr[i] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        ra[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsA, off, 0, 0));
       } else {
-        rs[i] = ok ? a_ptr[i][k0] : 0.f;
+        rs[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsA, off, 0, 0));
       }
     }
     if (BMODE == 0) {
 #pragma unroll
       for (int i = 0; i < BD_PT; ++i) {
-        const bool ok = b_ok[i] && k0 + b_k[i] < kend;
-        rb[i] = ok ? ld4(b_ptr[i] + (size_t)k0 * g.ldb) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int off = b_ok[i] && k0 + b_k[i] < kend ? b_off[i] + k0 * g.ldb * 4 : kOutside;
+        rb[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsD, off, 0, 0));
       }
     } else if (BMODE == 1) {
 #pragma unroll
       for (int i = 0; i < BD_PT; ++i) {
-        const bool ok = b_ok[i] && k0 + b_k[i] < kend;
-        rbs[i] = ok ? b_ptr[i][(size_t)k0 * g.ldb] : 0.f;
+        const int off = b_ok[i] && k0 + b_k[i] < kend ? b_off[i] + k0 * g.ldb * 4 : kOutside;
+        rbs[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsD, off, 0, 0));
       }
     } else if (BMODE == 3) {
       // the whole tile is one tap: k0 = tap * Cin + c0, c0 % BK == 0
       const int HW = g.H * g.W;
-      const int tap = k0 / g.Cin;
-      const int c0 = k0 - tap * g.Cin + g_row;
-      const int kh = tap / Win::KW;
-      const int kw = tap - kh * Win::KW;
-      const int ih = g_ih + kh * Win::DH;
-      const int iw = g_iw + kw * Win::DW;
-      const bool ok = (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W && k0 < kend;
-      const float* src = g.B + g_base + (size_t)c0 * HW + (ok ? ih * g.W + iw : 0);
+      const int kh = g_tap / Win::KW;
+      const int dh = kh * Win::DH, dw = (g_tap - kh * Win::KW) * Win::DW;
+      const bool ok = (unsigned)(g_ih + dh) < (unsigned)g.H && (unsigned)(g_iw + dw) < (unsigned)g.W &&
+                      k0 < kend;
+      const int off = ok ? (g_pix + (g_c0 * HW + dh * g.W + dw)) * 4 : kOutside;
 #pragma unroll
-      for (int i = 0; i < RPT; ++i) rg[i] = ok ? src[(size_t)i * HW] : 0.f;
+      for (int i = 0; i < RPT; ++i)
+        rg[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsB, off, i * HW * 4, 0));
+      g_c0 += BK;
+      if (g_c0 == g.Cin) {
+        g_c0 = 0;
+        ++g_tap;
+      }
     } else {
       // general (c, kh, kw) order: walk the thread's rows incrementally
       constexpr int KHW = Win::KH * Win::KW;
@@ -247,7 +266,7 @@ __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0,
   auto store_tiles = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < A_PT; ++i) {
-      if (tid + i * NT < A_ELEMS) {
+      if (A_ELEMS % NT == 0 || tid + i * NT < A_ELEMS) {   // (the block has NT threads)
         if (VA) st4(&As[buf][a_lds[i]], ra[i]);
         else As[buf][a_lds[i]] = rs[i];
       }
@@ -255,11 +274,11 @@ __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0,
     if (BMODE == 0) {
 #pragma unroll
       for (int i = 0; i < BD_PT; ++i)
-        if (tid + i * NT < BD_ELEMS) st4(&Bs[buf][b_lds[i]], rb[i]);
+        if (BD_ELEMS % NT == 0 || tid + i * NT < BD_ELEMS) st4(&Bs[buf][b_lds[i]], rb[i]);
     } else if (BMODE == 1) {
 #pragma unroll
       for (int i = 0; i < BD_PT; ++i)
-        if (tid + i * NT < BD_ELEMS) Bs[buf][b_lds[i]] = rbs[i];
+        if (BD_ELEMS % NT == 0 || tid + i * NT < BD_ELEMS) Bs[buf][b_lds[i]] = rbs[i];
     } else if (RPT % 4 == 0) {
 #pragma unroll
       for (int i = 0; i < RPT; i += 4)
