@@ -209,8 +209,12 @@ class HipCodegen(Int8LoweringMixin):
             else:
                 self._lower_grouped_conv(g, node, geo, has_bias)
             return
+        # the small-channel kernel reads its input and writes its output through
+        # buffer resources of byte offsets below 2^31 - 16
         if self.conv_mode == "implicit" and self.small_conv and smallc_fits(geo["C"], geo["KH"], geo["KW"], geo["DH"],
-                                                        geo["DW"]):
+                                                        geo["DW"]) \
+                and 4 * geo["N"] * max(geo["C"] * geo["H"] * geo["W"],
+                                       geo["OC"] * geo["OH"] * geo["OW"]) < 0x7ffffff0:
             self._lower_conv_smallc(g, node, geo, has_bias)
             return
         # the Winograd kernel reads its input through a buffer resource of

@@ -754,21 +754,33 @@ __device__ __forceinline__ void conv_smallc_f32(const float* __restrict__ x,
   int t = blockIdx.x;
   if (t >= ntiles) return;
 
+  // The patch elements a thread loads are fixed: element e = tid + 256 q is
+  // channel c, row r, column col of the patch, at (c H + r) W + col from the
+  // block's corner. Loads go through a buffer resource over the block's
+  // image: taps outside it read zero from offset kOutside (no branches).
+  int pe_off[NPT], pe_rc[NPT];
+#pragma unroll
+  for (int q = 0; q < NPT; ++q) {
+    const int e = threadIdx.x + q * 256;
+    const int c = e / (PR * PC);
+    const int rem = e - c * (PR * PC);
+    const int r = rem / PC, col = rem - r * PC;
+    pe_off[q] = (c * H + r) * W + col;
+    pe_rc[q] = e < PSZ ? r << 16 | col : 0x7fff0000;   // past the patch: a row no image has
+  }
   auto load_patch = [&](int tile, float (&pr)[NPT]) {
     const int tw = tile % tiles_w;
     const int th = (tile / tiles_w) % tiles_h;
     const int n = tile / (tiles_w * tiles_h);
     const int ih0 = th * TR * SH - PT, iw0 = tw * TC * SW - PL;
-    const float* xn = x + (size_t)n * C * H * W;
+    const __amdgpu_buffer_rsrc_t rx = buffer_over(x + (size_t)n * C * H * W, (N - n) * C * H * W * 4);
+    const int corner = ih0 * W + iw0;
 #pragma unroll
     for (int q = 0; q < NPT; ++q) {
-      const int e = threadIdx.x + q * 256;
-      const int c = e / (PR * PC);
-      const int rem = e - c * (PR * PC);
-      const int r = rem / PC, col = rem - r * PC;
-      const int ih = ih0 + r, iw = iw0 + col;
-      pr[q] = (e < PSZ && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
-                  ? xn[((size_t)c * H + ih) * W + iw] : 0.f;
+      const int ih = ih0 + (pe_rc[q] >> 16), iw = iw0 + (pe_rc[q] & 0xffff);
+      const bool ok = (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+      pr[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+          rx, ok ? (pe_off[q] + corner) * 4 : kOutside, 0, 0));
     }
   };
   auto store_patch = [&](int buf, const float (&pr)[NPT]) {
@@ -878,10 +890,14 @@ __device__ __forceinline__ void conv_smallc_f32(const float* __restrict__ x,
     };
     const bool full = (ocb + 1) * 32 <= OC && (th + 1) * TR <= OH && (tw + 1) * TC <= OW;
     if (full) {                                  // no per-element branches
+      // one 32-bit offset a block, the channel step in the scalar offset
+      const __amdgpu_buffer_rsrc_t ry = buffer_over(y, N * OC * (int)cs * 4);
 #pragma unroll
       for (int j = 0; j < NB; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) y[o0[j] + ((r / 4) * 8 + (r % 4)) * cs] = outval(j, r);
+        for (int r = 0; r < 16; ++r)
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, outval(j, r)), ry,
+                                                (int)o0[j] * 4, ((r / 4) * 8 + (r % 4)) * (int)cs * 4, 0);
     } else {
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
