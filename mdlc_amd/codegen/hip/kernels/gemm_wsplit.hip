@@ -40,7 +40,7 @@ __device__ __forceinline__ void gemm_f32_wsplit(const float* __restrict__ A,
   const int m0 = (blockIdx.x % tiles_m) * TM;
   const int n0 = (blockIdx.x / tiles_m) * TN;
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar K range
   const int li = lane & 15;
   const int lg = lane >> 4;
 
@@ -49,22 +49,31 @@ __device__ __forceinline__ void gemm_f32_wsplit(const float* __restrict__ A,
   const int s0 = (int)((long long)steps * w / WK);
   const int s1 = (int)((long long)steps * (w + 1) / WK);
 
-  const float* ap[MI];
-  bool aok[MI];
+  // Loads go through buffer resources: a row past M or a column past N has
+  // the out-of-range offset kOutside, k past K falls outside the resource's
+  // range, and a step past this wave's share gets an empty range, so every
+  // masked element reads zero and no load sits behind a branch. (Branches
+  // around loads leave the number of loads in flight unknown to the
+  // compiler, which then waits for all of them at each step.) The step's k0
+  // moves the resource base (scalar work); the per-lane offsets stay fixed.
+  const int a_bytes = M * lda * 4;
+  const int b_bytes = BKN ? N * ldb * 4 : K * ldb * 4;
+  int aoff[MI];
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
     const int row = m0 + mi * 16 + li;
-    aok[mi] = row < M;
-    ap[mi] = A + (size_t)min(row, M - 1) * lda + 4 * lg;
+    aoff[mi] = row < M ? (row * lda + 4 * lg) * 4 : kOutside;
   }
-  const float* bp[NI];
-  bool bok[NI];
+  int boff[NI][BKN ? 1 : 4];
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
     const int col = n0 + ni * 16 + li;
-    bok[ni] = col < N;
-    bp[ni] = BKN ? B + (size_t)min(col, N - 1) * ldb + 4 * lg
-                 : B + (size_t)(4 * lg) * ldb + min(col, N - 1);
+    if (BKN) {
+      boff[ni][0] = col < N ? (col * ldb + 4 * lg) * 4 : kOutside;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) boff[ni][q] = col < N ? ((4 * lg + q) * ldb + col) * 4 : kOutside;
+    }
   }
 
   floatx4 acc[MI][NI];
@@ -82,36 +91,45 @@ __device__ __forceinline__ void gemm_f32_wsplit(const float* __restrict__ A,
     for (int u = 0; u < UN; ++u) {
       const int k0 = (s + u) * 16;
       const bool live = s + u < s1;
+      const __amdgpu_buffer_rsrc_t rA = buffer_over(A + k0, live ? max(a_bytes - k0 * 4, 0) : 0);
+      const __amdgpu_buffer_rsrc_t rB =
+          BKN ? buffer_over(B + k0, live ? max(b_bytes - k0 * 4, 0) : 0)
+              : buffer_over(B + (size_t)k0 * ldb, live ? max(b_bytes - k0 * ldb * 4, 0) : 0);
+      // k past K inside a row (only without VA): its element's offset is
+      // pushed out of range per lane
+      const int kl = k0 + 4 * lg;
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi) {
         if (VA) {
-          const float4 v = (live && aok[mi]) ? ld4(ap[mi] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
-          av[buf][u][mi][0] = v.x;
-          av[buf][u][mi][1] = v.y;
-          av[buf][u][mi][2] = v.z;
-          av[buf][u][mi][3] = v.w;
+          const floatx4 v = __builtin_bit_cast(
+              floatx4, __builtin_amdgcn_raw_buffer_load_b128(rA, aoff[mi], 0, 0));
+#pragma unroll
+          for (int q = 0; q < 4; ++q) av[buf][u][mi][q] = v[q];
         } else {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const bool ok = live && aok[mi] && k0 + 4 * lg + q < K;
-            av[buf][u][mi][q] = ok ? ap[mi][k0 + q] : 0.f;
-          }
+          for (int q = 0; q < 4; ++q)
+            av[buf][u][mi][q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                rA, kl + q < K ? aoff[mi] + 4 * q : kOutside, 0, 0));
         }
       }
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni) {
         if (BKN && VA) {
-          const float4 v = (live && bok[ni]) ? ld4(bp[ni] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
-          bv[buf][u][ni][0] = v.x;
-          bv[buf][u][ni][1] = v.y;
-          bv[buf][u][ni][2] = v.z;
-          bv[buf][u][ni][3] = v.w;
-        } else {
+          const floatx4 v = __builtin_bit_cast(
+              floatx4, __builtin_amdgcn_raw_buffer_load_b128(rB, boff[ni][0], 0, 0));
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const bool ok = live && bok[ni] && k0 + 4 * lg + q < K;
-            bv[buf][u][ni][q] = ok ? (BKN ? bp[ni][k0 + q] : bp[ni][(size_t)(k0 + q) * ldb]) : 0.f;
-          }
+          for (int q = 0; q < 4; ++q) bv[buf][u][ni][q] = v[q];
+        } else if (BKN) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            bv[buf][u][ni][q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                rB, kl + q < K ? boff[ni][0] + 4 * q : kOutside, 0, 0));
+        } else {
+          // rows k >= K lie past the resource's range
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            bv[buf][u][ni][q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                rB, boff[ni][q], 0, 0));
         }
       }
     }

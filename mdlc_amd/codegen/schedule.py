@@ -42,7 +42,7 @@ class MfmaSchedule:
     SK: int = 1
     ST: bool = False        # stream-K remainder (fp32 GEMM/conv, SK == 1): see gemm_f32_mfma
     UN: int = 1             # K-loop unroll of the double-buffered fp32 loop (1 or 2); with
-                            # WK > 1, the 16-deep K steps per register stage (1, 2, 4, 8)
+                            # WK > 1, the 16-deep K steps per register stage (1 .. 16)
     WK: int = 1             # > 1: the wave-split kernel (dense fp32 GEMM): WK waves share the
                             # K range of one BM x BN tile (BM, BN in 16, 32), one launch
     BT: bool = False        # wave-split only: constant B stored K-contiguous per column
@@ -93,12 +93,16 @@ class MfmaSchedule:
     def wsplit_valid(self) -> bool:
         """The wave-split kernel: 16x16x4 MFMAs, a (BM x BN) tile of 16x16
         blocks per wave, WK waves over K, no LDS staging, one launch."""
-        # two register stages of UN steps: 2 * UN * (MI + NI) * 4 operand VGPRs
-        regs = 2 * self.UN * (self.BM // 16 + self.BN // 16) * 4
-        return (self.WK in (2, 4, 8, 16) and self.BM in (16, 32) and self.BN in (16, 32)
+        # two register stages of UN steps: 2 * UN * (MI + NI) * 4 operand VGPRs,
+        # plus MI * NI * 4 accumulators; the partial tiles of all WK waves meet
+        # in LDS (WK * MI * NI * 1 KB)
+        mi, ni = self.BM // 16, self.BN // 16
+        regs = 2 * self.UN * (mi + ni) * 4 + mi * ni * 4
+        return (self.WK in (2, 4, 8, 16) and self.BM in (16, 32, 64) and self.BN in (16, 32, 64)
                 and self.MS == 16 and self.WGM == 1 and self.WGN == 1 and self.BK == 16
-                and not self.DB and self.SK == 1 and not self.ST and self.UN in (1, 2, 4, 8)
-                and regs <= 192)
+                and not self.DB and self.SK == 1 and not self.ST
+                and self.UN in (1, 2, 4, 8, 16) and regs <= 200
+                and self.WK * mi * ni * 1024 <= LDS_LIMIT)
 
     def conv_valid(self) -> bool:
         """Valid for the implicit-GEMM convolution kernels, whose gather gives
@@ -154,10 +158,10 @@ def gemm_search_space(splits=(1,)) -> Iterator[MfmaSchedule]:
 
 
 def wsplit_search_space() -> Iterator[MfmaSchedule]:
-    for bm in (16, 32):
-        for bn in (16, 32):
+    for bm in (16, 32, 64):
+        for bn in (16, 32, 64):
             for wk in (4, 8, 16):
-                for un in (1, 2, 4, 8):
+                for un in (1, 2, 4, 8, 16):
                     for bt in (False, True):
                         s = MfmaSchedule.wsplit(bm, bn, wk, un, bt)
                         if s.is_valid():

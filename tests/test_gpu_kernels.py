@@ -41,6 +41,8 @@ SCHEDULES = [
     MfmaSchedule.wsplit(16, 32, 8, 2),
     MfmaSchedule.wsplit(16, 16, 8, 8),
     MfmaSchedule.wsplit(32, 16, 4, 1, True),                   # weights K-contiguous per column
+    MfmaSchedule.wsplit(64, 16, 4, 2),                         # 64-row tile
+    MfmaSchedule.wsplit(16, 64, 8, 4, True),                   # 64-column tile, deep stages
 ]
 
 
@@ -80,6 +82,19 @@ def test_gemm_transb_and_ragged_shapes(M, N, K, hip_ctx):
     assert_close("C", got["C"], want["C"])
 
 
+@pytest.mark.parametrize("sched", [MfmaSchedule.wsplit(16, 16, 4, 2), MfmaSchedule.wsplit(32, 16, 8, 1, True),
+                                   MfmaSchedule.wsplit(16, 64, 4, 4, True)], ids=lambda s: s.key())
+@pytest.mark.parametrize("M,N,K", [(1, 1000, 512), (7, 13, 5), (33, 1001, 77), (5, 70, 300)])
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_wave_split_ragged_shapes(M, N, K, trans_b, sched, hip_ctx):
+    """The wave-split kernel's out-of-range reads (rows past M, columns past
+    N, k past K inside a row, steps past a wave's share) all read zero."""
+    g, feeds = _gemm_graph(M, N, K, "Relu", True, seed=6, trans_b=trans_b)
+    c, got, want = device_run(g, feeds, ctx=hip_ctx, schedule_fn=lambda n, mnk: sched)
+    assert [l.kind for l in c.module.plan] == ["gemm_ws"]
+    assert_close("C", got["C"], want["C"])
+
+
 @pytest.mark.parametrize("M,N,K", SHAPES, ids=lambda v: str(v))
 def test_micro_gemm_shapes(M, N, K, hip_ctx):
     """The fused GEMM+bias+ReLU micro workload at ResNet-18's batch-1 shapes."""
@@ -92,7 +107,8 @@ def test_micro_gemm_shapes(M, N, K, hip_ctx):
 @pytest.mark.parametrize("sched", [MfmaSchedule.wsplit(16, 16, 8), MfmaSchedule.wsplit(32, 16, 16, 2),
                                    MfmaSchedule.wsplit(16, 32, 4, 2), MfmaSchedule.wsplit(16, 16, 16, 8),
                                    MfmaSchedule.wsplit(32, 16, 4, 4), MfmaSchedule.wsplit(16, 16, 8, 2, True),
-                                   MfmaSchedule.wsplit(32, 32, 4, 1, True)], ids=lambda s: s.key())
+                                   MfmaSchedule.wsplit(32, 32, 4, 1, True), MfmaSchedule.wsplit(16, 64, 8),
+                                   MfmaSchedule.wsplit(64, 32, 4, 2)], ids=lambda s: s.key())
 @pytest.mark.parametrize("M,N,K", SHAPES)
 def test_micro_gemm_wave_split(M, N, K, sched, hip_ctx):
     """The one-launch wave-split kernel on the micro shapes (16-byte A loads,
