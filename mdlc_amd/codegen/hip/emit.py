@@ -61,6 +61,12 @@ STREAM_K_WGS = 256    # stream-K workgroups: one per CU
 SMALLC_WGS = 512      # workgroups stepping through the blocks of the small-channel conv
 
 
+def _check_reduce_size(M: int, N: int) -> None:
+    """The split-K reduce indexes one slice with 32-bit integers."""
+    if M * N >= 2 ** 31:
+        raise NotImplementedError(f"HIP codegen: split-K output of {M * N} elements (2^31 or more)")
+
+
 def dw_rows_per_thread(oh: int) -> int:
     """Outputs per thread down a column in the depthwise kernel: 8 (fewer
     loads per output), 4 for planes of at most 7 rows, where 8 leaves too few
@@ -217,11 +223,12 @@ class HipCodegen(Int8LoweringMixin):
                                        geo["OC"] * geo["OH"] * geo["OW"]) < 0x7ffffff0:
             self._lower_conv_smallc(g, node, geo, has_bias)
             return
-        # the Winograd kernel reads its input through a buffer resource of
-        # byte offsets below 2^31 (offsets at 0x7ffffff0 read as zeros) and
+        # the Winograd kernel reads its input, bias and residual through buffer
+        # resources of byte offsets below 2^31 (offsets at 0x7ffffff0 read as zeros) and
         # divides tile indices below 2^21 in float
         if (self.conv_mode == "implicit" and self.winograd and wino_fits(geo)
                 and geo["N"] * geo["C"] * geo["H"] * geo["W"] * 4 < 0x7ffffff0
+                and geo["N"] * geo["OC"] * geo["OH"] * geo["OW"] * 4 < 0x7ffffff0
                 and geo["N"] * -(-geo["OH"] // 2) * -(-geo["OW"] // 2) < 2 ** 21
                 and (self.winograd is True or wino_pays(
                     geo["OC"], geo["N"] * -(-geo["OH"] // 2) * -(-geo["OW"] // 2), geo["C"]))):
@@ -373,12 +380,13 @@ class HipCodegen(Int8LoweringMixin):
         rtag = "_res" if residual and not split else ""
         ploads = -(-wino_patch(N, H, W, geo["PT"], OH, OW) // 64)
         meta["ploads"] = ploads
-        sig = ("wino", split, ploads, bool(bias) and not split, None if split else epi["act_sig"],
-               None if split else residual)
+        full = OH % 2 == 0 and OW % 2 == 0
+        sig = ("wino", split, ploads, full, bool(bias) and not split,
+               None if split else epi["act_sig"], None if split else residual)
         kname = self._kernel(sig, lambda i: T.wino_kernel(
             f"conv_wino{'_SK' if split else ''}_P{ploads}_{'none' if split else act or 'none'}{rtag}_{i}",
-            split=split, ploads=ploads, with_bias=bool(bias), activation=act, attrs=epi["attrs"],
-            residual=residual))
+            split=split, ploads=ploads, full=full, with_bias=bool(bias), activation=act,
+            attrs=epi["attrs"], residual=residual))
         if not split:
             if res:
                 meta["bytes"] += 4 * OC * P
@@ -394,11 +402,13 @@ class HipCodegen(Int8LoweringMixin):
         self.plan.append(Launch("wino", kname, [udev, x], [ws], grid, (512, 1, 1),
                                 dict(meta, partial=True)))
         vec = REDUCE_VEC if P % 4 == 0 and (OH * OW) % 4 == 0 else 1
-        rsig = ("splitk_reduce", bool(bias), "row", epi["act_sig"], 1.0, 1.0, residual, vec)
+        _check_reduce_size(OC, P)
+        rsig = ("splitk_reduce", bool(bias), "row", epi["act_sig"], 1.0, 1.0, residual, vec, slices,
+                OH * OW)
         rname = self._kernel(rsig, lambda i: T.splitk_reduce_kernel(
             f"splitk_reduce{'4' if vec == 4 else ''}_{act or 'none'}_row{'_res' if residual else ''}_{i}",
             with_bias=bool(bias), bias_mode="row", activation=act, attrs=epi["attrs"],
-            residual=residual, vec=vec))
+            residual=residual, vec=vec, slices=slices, hw=OH * OW))
         self.plan.append(Launch(
             "splitk_reduce", rname, [ws] + bias + extra, [y], (-(-(OC * P) // (256 * vec)), 1, 1),
             (256, 1, 1),
@@ -527,12 +537,14 @@ class HipCodegen(Int8LoweringMixin):
         # four contiguous, 16-byte aligned outputs per thread when the layout allows
         vec = REDUCE_VEC if N % 4 == 0 and (epi["hw"] % 4 == 0 if epi["hw"] else epi["ldc"] % 4 == 0) \
             else 1
+        _check_reduce_size(M, N)
         rsig = ("splitk_reduce", bool(bias), epi["bias_mode"], epi["act_sig"], epi["alpha"], epi["beta"],
-                residual, vec)
+                residual, vec, slices, epi["hw"])
         rname = self._kernel(rsig, lambda i: T.splitk_reduce_kernel(
             f"splitk_reduce{'4' if vec == 4 else ''}_{act or 'none'}_{epi['bias_mode']}{rtag}_{i}",
             with_bias=bool(bias), bias_mode=epi["bias_mode"], activation=act, attrs=epi["attrs"],
-            alpha=epi["alpha"], beta=epi["beta"], residual=residual, vec=vec))
+            alpha=epi["alpha"], beta=epi["beta"], residual=residual, vec=vec, slices=slices,
+            hw=epi["hw"]))
         self.plan.append(Launch(
             "splitk_reduce", rname, [ws] + bias + extra, [out], (-(-(M * N) // (256 * vec)), 1, 1),
             (256, 1, 1),

@@ -61,6 +61,8 @@
 // P = N*OH*OW, for splitk_reduce_f32 to add in slice order and finish.
 namespace mdlc {
 
+typedef unsigned v2u32_t __attribute__((ext_vector_type(2)));
+
 struct WinoArgs {
   const float* __restrict__ U;     // packed filters, [OCP/64][CP/8][16][64][8]
   const float* __restrict__ x;     // [N][C][H][W]
@@ -94,7 +96,8 @@ __device__ __forceinline__ int wino_div(int n, int d, float inv) {
 
 // PL: patch loads per lane (one channel per wave), ceil(largest patch / 64)
 // <= WINO_PMAX / 64.
-template <bool SPLIT, int PL, class Epi>
+// FULL: OH and OW are even, so every tile has its four pixels.
+template <bool SPLIT, int PL, bool FULL, class Epi>
 __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
   static_assert(PL * 64 <= WINO_PMAX, "patch larger than its LDS");
   __shared__ __attribute__((aligned(16))) float ust[3 * WINO_USTAGE];
@@ -335,6 +338,53 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
         y[blk][r][2] = s1[0] + s1[1] + s1[2];
         y[blk][r][3] = s1[1] - s1[2] - s1[3];
       }
+    // Epilogue operands (bias, folded residual) are loaded here, before any
+    // store and ahead of the exchange: a load issued after a store waits for
+    // that store too (one memory counter), which would serialize the stores.
+    // Buffer resources give zeros for channels past OC and pixels past the
+    // image, so the loads need no branches.
+    const int OHW = g.OH * g.OW;
+    const int oy = 2 * ty, ox = 2 * tx;
+    const bool yok = oy + 1 < g.OH, xok = ox + 1 < g.OW;
+    const int oc0 = ocb * 64 + 32 * H + 4 * lk;
+    float bv[2][4] = {};
+    float rv[2][4][4] = {};
+    if (!SPLIT) {
+      if (Epi::bias == 1) {
+        const __amdgpu_buffer_rsrc_t rbias = buffer_over(g.bias, g.OC * 4);
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            bv[bb][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                rbias, (oc0 + 16 * bb + r) * 4, 0, 0));
+      }
+      if (Epi::residual) {
+        const __amdgpu_buffer_rsrc_t rres = buffer_over(g.R, g.N * g.OC * OHW * 4);
+        const int base = ((n * g.OC + oc0) * OHW + oy * g.OW + ox) * 4;
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int o = oc0 + 16 * bb + r < g.OC ? base + (16 * bb + r) * OHW * 4 : kOutside;
+            if (FULL) {
+              const float2 r0 = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rres, o, 0, 0));
+              const float2 r1 = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+                  rres, o == kOutside ? kOutside : o + g.OW * 4, 0, 0));
+              rv[bb][r][0] = r0.x; rv[bb][r][1] = r0.y; rv[bb][r][2] = r1.x; rv[bb][r][3] = r1.y;
+            } else {
+              const bool in = o != kOutside;
+              rv[bb][r][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rres, o, 0, 0));
+              rv[bb][r][1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                  rres, in && xok ? o + 4 : kOutside, 0, 0));
+              rv[bb][r][2] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                  rres, in && yok ? o + g.OW * 4 : kOutside, 0, 0));
+              rv[bb][r][3] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                  rres, in && xok && yok ? o + g.OW * 4 + 4 : kOutside, 0, 0));
+            }
+          }
+      }
+    }
     __syncthreads();
     float* xw = ust + H * 8192;                       // this half's partials for the other half
 #pragma unroll
@@ -348,26 +398,21 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
     __syncthreads();
     const float* xr = ust + (1 - H) * 8192;
 
-    // Output channel oc0 + 16 bb + r of the lane's tile; one base address a
-    // lane, channels a fixed stride apart. When every tile has all four
-    // pixels (even OH and OW) the pixel pairs are 8-byte aligned and stored
-    // (and the residual read) without conditions.
-    if (p >= P) return;
-    const int OHW = g.OH * g.OW;
-    const int oy = 2 * ty, ox = 2 * tx;
-    const bool yok = oy + 1 < g.OH, xok = ox + 1 < g.OW;
-    const bool full = ((g.OH | g.OW) & 1) == 0;
-    const int oc0 = ocb * 64 + 32 * H + 4 * lk;
-    const size_t ocs = SPLIT ? (size_t)g.N * OHW : (size_t)OHW;   // stride between channels
-    float* yb = g.y + (SPLIT ? ((size_t)slice * g.OC + oc0) * ocs + (size_t)n * OHW
-                             : ((size_t)n * g.OC + oc0) * OHW) + oy * g.OW + ox;
-    const float* rb = Epi::residual ? g.R + ((size_t)n * g.OC + oc0) * OHW + oy * g.OW + ox : nullptr;
+    // Output channel oc0 + 16 bb + r of the lane's tile, channels a fixed
+    // stride apart. The stores go through a buffer resource over the output
+    // (or this slice of the workspace): a lane past the last tile, a channel
+    // past OC or a pixel past the image gets the out-of-range offset and its
+    // store is dropped, so the stores need no branches either. With FULL the
+    // pixel pairs are 8-byte aligned.
+    const int ocs = SPLIT ? g.N * OHW : OHW;          // stride between channels
+    const int obase = (SPLIT ? oc0 * ocs + n * OHW : (n * g.OC + oc0) * OHW) + oy * g.OW + ox;
+    const __amdgpu_buffer_rsrc_t rout =
+        buffer_over(g.y + (SPLIT ? (size_t)slice * g.OC * g.N * OHW : 0), g.OC * g.N * OHW * 4);
+    const bool live = p < P;
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int oc = oc0 + 16 * bb + r;
-        if (oc >= g.OC) continue;
         const float4 other = ld4(xr + (((tg * 2 + bb) * 4 + r) * 64 + lane) * 4);
         const float* mine = y[2 * H + bb][r];
         float out[4];                                 // Y_0 + Y_1
@@ -378,37 +423,29 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
           out[0] = other.x + mine[0]; out[1] = other.y + mine[1];
           out[2] = other.z + mine[2]; out[3] = other.w + mine[3];
         }
-        float* d = yb + (16 * bb + r) * ocs;
         if (!SPLIT) {
-          const float b = Epi::bias == 1 ? g.bias[oc] : 0.f;
-          float rv[4] = {0.f, 0.f, 0.f, 0.f};
-          if (Epi::residual) {
-            const float* rr = rb + (16 * bb + r) * OHW;
-            if (full) {
-              const float2 r0 = *reinterpret_cast<const float2*>(rr);
-              const float2 r1 = *reinterpret_cast<const float2*>(rr + g.OW);
-              rv[0] = r0.x; rv[1] = r0.y; rv[2] = r1.x; rv[3] = r1.y;
-            } else {
-              rv[0] = rr[0];
-              if (xok) rv[1] = rr[1];
-              if (yok) rv[2] = rr[g.OW];
-              if (xok && yok) rv[3] = rr[g.OW + 1];
-            }
-          }
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            out[e] = Epi::apply(out[e], b);
-            if (Epi::residual) out[e] = Epi::post(out[e], rv[e]);
+            out[e] = Epi::apply(out[e], bv[bb][r]);
+            if (Epi::residual) out[e] = Epi::post(out[e], rv[bb][r][e]);
           }
         }
-        if (full) {
-          *reinterpret_cast<float2*>(d) = make_float2(out[0], out[1]);
-          *reinterpret_cast<float2*>(d + g.OW) = make_float2(out[2], out[3]);
+        const bool ok = live && oc0 + 16 * bb + r < g.OC;
+        const int o = (obase + (16 * bb + r) * ocs) * 4;
+        if (FULL) {
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, make_float2(out[0], out[1])),
+                                                rout, ok ? o : kOutside, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, make_float2(out[2], out[3])),
+                                                rout, ok ? o + g.OW * 4 : kOutside, 0, 0);
         } else {
-          d[0] = out[0];
-          if (xok) d[1] = out[1];
-          if (yok) d[g.OW] = out[2];
-          if (xok && yok) d[g.OW + 1] = out[3];
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, out[0]), rout,
+                                                ok ? o : kOutside, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, out[1]), rout,
+                                                ok && xok ? o + 4 : kOutside, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, out[2]), rout,
+                                                ok && yok ? o + g.OW * 4 : kOutside, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, out[3]), rout,
+                                                ok && xok && yok ? o + g.OW * 4 + 4 : kOutside, 0, 0);
         }
       }
   };

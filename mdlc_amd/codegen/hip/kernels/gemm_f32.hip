@@ -637,64 +637,65 @@ __device__ __forceinline__ void streamk_fixup_f32(const float* __restrict__ ws,
 
 // Split-K epilogue: out = epi(sum_s ws[s][row][col], bias) with the slices
 // added in slice order (then a folded residual group, if any), written
-// row-major (ldc) or NCHW (hw > 0). One thread per output element (V = 1)
-// or per four consecutive columns (V = 4: N % 4 == 0 and hw % 4 == 0, or
-// ldc % 4 == 0 row-major, so the four outputs are contiguous and 16-byte
-// aligned and every access is 128-bit); consecutive threads on consecutive
-// columns. Both forms do the same float operations per element.
-template <class Epi, int V>
+// row-major (ldc) or NCHW (HW > 0: the plane size, col = n * HW + pixel).
+// One thread per output element (V = 1) or per four consecutive columns
+// (V = 4: N % 4 == 0 and HW % 4 == 0, or ldc % 4 == 0 row-major, so the four
+// outputs are contiguous and 16-byte aligned and every access is 128-bit);
+// consecutive threads on consecutive columns. Both forms do the same float
+// operations per element. The slice count S and the plane size are
+// compile-time constants, so a thread issues all S slice loads before the
+// first addition, and the index arithmetic is 32-bit (M * N < 2^31, checked
+// by the lowering).
+template <class Epi, int V, int S, int HW>
 __device__ __forceinline__ void splitk_reduce_f32(const float* __restrict__ ws,
                                                   const float* __restrict__ bias,
                                                   const float* __restrict__ res,
-                                                  float* __restrict__ C, int S, int M, int N,
-                                                  int ldc, int hw) {
+                                                  float* __restrict__ C, int M, int N, int ldc) {
+  const int q = blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= M * N / V) return;
+  const int i = q * V;
+  const int row = i / N;
+  const int col = i - row * N;
+  const size_t plane = (size_t)M * N;
+  int o;
+  if (HW > 0) {
+    const int n = col / HW;
+    o = (n * M + row) * HW + (col - n * HW);
+  } else {
+    o = row * ldc + col;
+  }
   if (V == 4) {
-    const long long q = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= (long long)M * N / 4) return;
-    const long long i = q * 4;
-    const int row = (int)(i / N);
-    const int col = (int)(i - (long long)row * N);
-    float4 v = ld4(ws + i);
-    for (int s = 1; s < S; ++s) {
-      const float4 w = ld4(ws + (size_t)s * M * N + i);
-      v.x = v.x + w.x; v.y = v.y + w.y; v.z = v.z + w.z; v.w = v.w + w.w;
-    }
+    float4 w[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) w[s] = ld4(ws + s * plane + i);
     float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
     if (Epi::bias == 1) b = make_float4(bias[row], bias[row], bias[row], bias[row]);
     if (Epi::bias == 2) b = ld4(bias + col);
+    float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (Epi::residual) r = ld4(res + o);
+    float4 v = w[0];
+#pragma unroll
+    for (int s = 1; s < S; ++s) {
+      v.x = v.x + w[s].x; v.y = v.y + w[s].y; v.z = v.z + w[s].z; v.w = v.w + w[s].w;
+    }
     v = make_float4(Epi::apply(v.x, b.x), Epi::apply(v.y, b.y), Epi::apply(v.z, b.z),
                     Epi::apply(v.w, b.w));
-    size_t o;
-    if (hw > 0) {
-      const int n = col / hw;
-      o = ((size_t)n * M + row) * hw + (col - n * hw);
-    } else {
-      o = (size_t)row * ldc + col;
-    }
-    if (Epi::residual) {
-      const float4 r = ld4(res + o);
+    if (Epi::residual)
       v = make_float4(Epi::post(v.x, r.x), Epi::post(v.y, r.y), Epi::post(v.z, r.z),
                       Epi::post(v.w, r.w));
-    }
     st4(C + o, v);
     return;
   }
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (long long)M * N) return;
-  const int row = (int)(i / N);
-  const int col = (int)(i - (long long)row * N);
-  float v = ws[i];
-  for (int s = 1; s < S; ++s) v = v + ws[(size_t)s * M * N + i];
+  float w[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) w[s] = ws[s * plane + i];
   const float b = Epi::bias == 1 ? bias[row] : (Epi::bias == 2 ? bias[col] : 0.f);
+  const float r = Epi::residual ? res[o] : 0.f;
+  float v = w[0];
+#pragma unroll
+  for (int s = 1; s < S; ++s) v = v + w[s];
   v = Epi::apply(v, b);
-  size_t o;
-  if (hw > 0) {
-    const int n = col / hw;
-    o = ((size_t)n * M + row) * hw + (col - n * hw);
-  } else {
-    o = (size_t)row * ldc + col;
-  }
-  if (Epi::residual) v = Epi::post(v, res[o]);
+  if (Epi::residual) v = Epi::post(v, r);
   C[o] = v;
 }
 

@@ -223,9 +223,12 @@ def gemm_wsplit_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_
 
 def splitk_reduce_kernel(name: str, *, with_bias: bool, bias_mode: str,
                          activation: Optional[str], attrs: dict, alpha: float = 1.0,
-                         beta: float = 1.0, residual: Optional[str] = None, vec: int = 1) -> tuple:
-    """Split-K epilogue, ``vec`` (1 or 4) outputs per thread.
-    ABI: (ws, [bias], [res], C, int S, int M, int N, int ldc, int hw)."""
+                         beta: float = 1.0, residual: Optional[str] = None, vec: int = 1,
+                         slices: int, hw: int) -> tuple:
+    """Split-K epilogue, ``vec`` (1 or 4) outputs per thread, for ``slices``
+    slices and NCHW planes of ``hw`` pixels (0: row-major), both compiled in.
+    ABI: (ws, [bias], [res], C, int S, int M, int N, int ldc, int hw); the S
+    and hw arguments repeat the compiled values."""
     epi = f"{name}_epi"
     src = epilogue_struct(epi, bias_mode=bias_mode if with_bias else None, activation=activation,
                           attrs=attrs, alpha=alpha, beta=beta, residual=residual)
@@ -235,8 +238,8 @@ def splitk_reduce_kernel(name: str, *, with_bias: bool, bias_mode: str,
         f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
         f"    const float* __restrict__ ws, {bias_arg}{res_arg}float* __restrict__ C, int S, int M,\n"
         "    int N, int ldc, int hw) {\n"
-        f"  mdlc::splitk_reduce_f32<{epi}, {int(vec)}>(ws, {'bias' if with_bias else 'nullptr'}, "
-        f"{'res' if residual else 'nullptr'}, C, S, M, N, ldc, hw);\n}}\n")
+        f"  mdlc::splitk_reduce_f32<{epi}, {int(vec)}, {int(slices)}, {int(hw)}>(ws, "
+        f"{'bias' if with_bias else 'nullptr'}, {'res' if residual else 'nullptr'}, C, M, N, ldc);\n}}\n")
 
 
 def streamk_fixup_kernel(name: str, sched: MfmaSchedule, skw: int, *, with_bias: bool,
@@ -284,7 +287,7 @@ def conv_smallc_kernel(name: str, win: tuple, tile: tuple, *, with_bias: bool,
         f"{'res' if residual else 'nullptr'}, y, N, H, W, OC, OH, OW);\n}}\n")
 
 
-def wino_kernel(name: str, *, split: bool, ploads: int, with_bias: bool,
+def wino_kernel(name: str, *, split: bool, ploads: int, full: bool, with_bias: bool,
                 activation: Optional[str], attrs: dict, residual: Optional[str] = None) -> tuple:
     """3x3 stride-1 convolution by Winograd F(2x2, 3x3) on the matrix cores.
     ABI: (U, x, [bias], [res], y, int N, int C, int H, int W, int OC, int OH,
@@ -293,7 +296,8 @@ def wino_kernel(name: str, *, split: bool, ploads: int, with_bias: bool,
     channel blocks of 64 x tile blocks of 64 (tiles fastest), grid y = the
     channel slices. ``split``: y is the split-K workspace and the kernel
     takes no bias or residual (``splitk_reduce_kernel`` finishes).
-    ``ploads``: input patch loads per lane and channel (``wino_patch``)."""
+    ``ploads``: input patch loads per lane and channel (``wino_patch``).
+    ``full``: OH and OW are even (every 2x2 tile lies inside the output)."""
     if split:
         with_bias, residual, activation = False, None, None
     epi = f"{name}_epi"
@@ -309,7 +313,8 @@ def wino_kernel(name: str, *, split: bool, ploads: int, with_bias: bool,
         f"  mdlc::WinoArgs g{{U, x, {'bias' if with_bias else 'nullptr'}, "
         f"{'res' if residual else 'nullptr'}, y, N, C, H, W, OC, OH, OW, TH, TW, CP, OCP, PT, PL, "
         "nchunk};\n"
-        f"  mdlc::conv_wino_f32<{'true' if split else 'false'}, {int(ploads)}, {epi}>(g);\n}}\n")
+        f"  mdlc::conv_wino_f32<{'true' if split else 'false'}, {int(ploads)}, "
+        f"{'true' if full else 'false'}, {epi}>(g);\n}}\n")
 
 
 def im2col_kernel(name: str = "im2col") -> tuple:
