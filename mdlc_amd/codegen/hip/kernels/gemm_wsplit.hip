@@ -36,9 +36,13 @@ __device__ __forceinline__ void gemm_f32_wsplit(const float* __restrict__ A,
   constexpr int TM = 16 * MI, TN = 16 * NI;
   __shared__ __attribute__((aligned(16))) floatx4 red[WK][MI][NI][64];
 
+  // Logical tile t (m fastest) from an XCD-aware remap: each XCD runs a
+  // contiguous range of tiles, so its L2 holds a few column blocks of B and
+  // a range of A's rows instead of fetching all of both.
   const int tiles_m = (M + TM - 1) / TM;
-  const int m0 = (blockIdx.x % tiles_m) * TM;
-  const int n0 = (blockIdx.x / tiles_m) * TN;
+  const int t = xcd_remap(blockIdx.x, tiles_m * ((N + TN - 1) / TN));
+  const int m0 = (t % tiles_m) * TM;
+  const int n0 = (t / tiles_m) * TN;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar K range
   const int li = lane & 15;
