@@ -499,14 +499,29 @@ class HipCodegen(Int8LoweringMixin):
                 raise ValueError(f"schedule {sched.key()} is for dense GEMMs only")
             b_kn = bool(meta.get("b_kn"))
             va = vec_a and K % 16 == 0 and meta["lda"] % 4 == 0 and (not b_kn or meta["ldb"] % 4 == 0)
-            wsig = ("gemm_ws", sched, bool(bias), epi["bias_mode"], epi["act_sig"], epi["alpha"],
-                    epi["beta"], va, b_kn)
+            if slices == 1:
+                wsig = ("gemm_ws", sched, bool(bias), epi["bias_mode"], epi["act_sig"], epi["alpha"],
+                        epi["beta"], va, b_kn)
+                kname = self._kernel(wsig, lambda i: T.gemm_wsplit_kernel(
+                    f"gemm_{sched.key()}_{act or 'none'}_{epi['bias_mode']}_{i}", sched,
+                    with_bias=bool(bias), bias_mode=epi["bias_mode"], activation=act,
+                    attrs=epi["attrs"], alpha=epi["alpha"], beta=epi["beta"], vec_a=va, b_kn=b_kn))
+                self.plan.append(Launch("gemm_ws", kname, operands + bias, [out], (tiles, 1, 1),
+                                        block, meta))
+                return
+            # K also split over workgroups: raw slices to the workspace (ldc = N), then the reduce
+            ws = out + "__splitk"
+            self.scratch[ws] = (slices * M, N)
+            self.scratch_class[ws] = "splitk"
+            wsig = ("gemm_ws", sched, va, b_kn, "partial")
             kname = self._kernel(wsig, lambda i: T.gemm_wsplit_kernel(
-                f"gemm_{sched.key()}_{act or 'none'}_{epi['bias_mode']}_{i}", sched,
-                with_bias=bool(bias), bias_mode=epi["bias_mode"], activation=act,
-                attrs=epi["attrs"], alpha=epi["alpha"], beta=epi["beta"], vec_a=va, b_kn=b_kn))
-            self.plan.append(Launch("gemm_ws", kname, operands + bias, [out], (tiles, 1, 1), block,
-                                    meta))
+                f"gemm_{sched.key()}_SK{slices}_{i}", sched, with_bias=False,
+                bias_mode=epi["bias_mode"], activation=None, attrs={}, vec_a=va, b_kn=b_kn))
+            extra_bytes = 4 * (M * N + (M if epi["bias_mode"] == "row" else N) * len(bias))
+            self.plan.append(Launch("gemm_ws", kname, list(operands), [ws], (tiles, slices, 1), block,
+                                    dict(meta, partial=True, ldc=N,
+                                         bytes=meta["bytes"] - extra_bytes + 4 * slices * M * N)))
+            self._emit_reduce(ws, bias, [], out, M, N, slices, epi, meta, act, "", None)
             return
         if sched.ST and tiles % STREAM_K_WGS:
             self._emit_stream_k(kind, sched, operands, bias, out, meta, epi, bmode=bmode,
@@ -534,6 +549,11 @@ class HipCodegen(Int8LoweringMixin):
         self.plan.append(Launch(kind, kname, list(operands), [ws], (tiles * slices, 1, 1), block,
                                 dict(meta, partial=True,
                                      bytes=meta["bytes"] - extra_bytes + 4 * slices * M * N)))
+        self._emit_reduce(ws, bias, extra, out, M, N, slices, epi, meta, act, rtag, residual)
+
+    def _emit_reduce(self, ws, bias, extra, out, M, N, slices, epi, meta, act, rtag, residual) -> None:
+        """The split-K reduce launch: adds the ``slices`` partial sums in ws in
+        slice order and applies bias, activation and residual."""
         # four contiguous, 16-byte aligned outputs per thread when the layout allows
         vec = REDUCE_VEC if N % 4 == 0 and (epi["hw"] % 4 == 0 if epi["hw"] else epi["ldc"] % 4 == 0) \
             else 1

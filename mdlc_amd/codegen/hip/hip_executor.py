@@ -146,7 +146,8 @@ class HipExecutor:
                      I(m["hw"]), I(m["ksplit"]), I(m["kchunk"])]
         elif k == "gemm_ws":
             args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
-            args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["ldb"]), I(m["ldc"])]
+            args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["ldb"]), I(m["ldc"]),
+                     I(m["kchunk"])]
         elif k == "conv":
             args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
             args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["Cin"]), I(m["H"]),

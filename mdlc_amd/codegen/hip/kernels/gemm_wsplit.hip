@@ -27,12 +27,16 @@
 // whatever its width, so the 16-byte forms matter more than the bytes.
 namespace mdlc {
 
-template <int MI, int NI, int WK, int UN, bool VA, bool BKN, class Epi>
+// SPLIT: the K range is also cut over gridDim.y workgroups (kchunk values
+// of K each, a multiple of 16); workgroup y writes its raw partial tile to
+// slice y of the split-K workspace, C[(y * M + row) * ldc + col], for
+// splitk_reduce_f32 to add in slice order and finish.
+template <int MI, int NI, int WK, int UN, bool VA, bool BKN, class Epi, bool SPLIT = false>
 __device__ __forceinline__ void gemm_f32_wsplit(const float* __restrict__ A,
                                                 const float* __restrict__ B,
                                                 const float* __restrict__ bias,
                                                 float* __restrict__ C, int M, int N, int K,
-                                                int lda, int ldb, int ldc) {
+                                                int lda, int ldb, int ldc, int kchunk) {
   constexpr int TM = 16 * MI, TN = 16 * NI;
   __shared__ __attribute__((aligned(16))) floatx4 red[WK][MI][NI][64];
 
@@ -48,10 +52,12 @@ __device__ __forceinline__ void gemm_f32_wsplit(const float* __restrict__ A,
   const int li = lane & 15;
   const int lg = lane >> 4;
 
-  // this wave's contiguous share of the 16-deep K steps
+  // this wave's contiguous share of the workgroup's 16-deep K steps
   const int steps = (K + 15) / 16;
-  const int s0 = (int)((long long)steps * w / WK);
-  const int s1 = (int)((long long)steps * (w + 1) / WK);
+  const int sb = SPLIT ? (int)blockIdx.y * (kchunk / 16) : 0;
+  const int sn = SPLIT ? min(steps, sb + kchunk / 16) - sb : steps;
+  const int s0 = sb + (int)((long long)sn * w / WK);
+  const int s1 = sb + (int)((long long)sn * (w + 1) / WK);
 
   // Loads go through buffer resources: a row past M or a column past N has
   // the out-of-range offset kOutside, k past K falls outside the resource's
@@ -188,8 +194,12 @@ __device__ __forceinline__ void gemm_f32_wsplit(const float* __restrict__ A,
     for (int k = 0; k < WK; ++k) v += redf[k * MI * NI * 256 + slot];
     const int gr = m0 + row, gc = n0 + col;
     if (gr < M && gc < N) {
-      const float b = Epi::bias == 2 ? bias[gc] : (Epi::bias == 1 ? bias[gr] : 0.f);
-      C[(size_t)gr * ldc + gc] = Epi::apply(v, b);
+      if (SPLIT) {
+        C[((size_t)blockIdx.y * M + gr) * ldc + gc] = v;
+      } else {
+        const float b = Epi::bias == 2 ? bias[gc] : (Epi::bias == 1 ? bias[gr] : 0.f);
+        C[(size_t)gr * ldc + gc] = Epi::apply(v, b);
+      }
     }
   }
 }

@@ -204,9 +204,15 @@ def gemm_wsplit_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_
                        beta: float = 1.0, vec_a: bool, b_kn: bool) -> tuple:
     """The wave-split GEMM (``sched.WK`` waves share the K range of one
     tile). ABI: (A, B, [bias], C, int M, int N, int K, int lda, int ldb,
-    int ldc); one workgroup of 64 * WK threads per BM x BN tile, m fastest.
-    ``b_kn``: B is stored [N][ldb] (K contiguous per output column)."""
+    int ldc, int kchunk); one workgroup of 64 * WK threads per BM x BN tile,
+    m fastest. ``b_kn``: B is stored [N][ldb] (K contiguous per output
+    column). With ``sched.SK > 1`` grid y is the K slice (``kchunk`` values
+    of K each) and C the split-K workspace: raw partial sums, no bias or
+    epilogue (``splitk_reduce_kernel`` finishes)."""
     s = sched
+    split = s.SK > 1
+    if split:
+        with_bias, activation, alpha = False, None, 1.0
     epi = f"{name}_epi"
     src = epilogue_struct(epi, bias_mode=bias_mode if with_bias else None, activation=activation,
                           attrs=attrs, alpha=alpha, beta=beta)
@@ -214,11 +220,12 @@ def gemm_wsplit_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_
     return name, src + (
         f'extern "C" __global__ __launch_bounds__({s.threads_per_block()}) void {name}(\n'
         f"    const float* __restrict__ A, const float* __restrict__ B, {bias_arg}"
-        "float* __restrict__ C, int M, int N,\n    int K, int lda, int ldb, int ldc) {\n"
+        "float* __restrict__ C, int M, int N,\n    int K, int lda, int ldb, int ldc, int kchunk) {\n"
         f"  mdlc::gemm_f32_wsplit<{s.BM // 16}, {s.BN // 16}, {s.WK}, {s.UN}, "
-        f"{'true' if vec_a else 'false'}, {'true' if b_kn else 'false'}, {epi}>(A, B, "
+        f"{'true' if vec_a else 'false'}, {'true' if b_kn else 'false'}, {epi}, "
+        f"{'true' if split else 'false'}>(A, B, "
         f"{'bias' if with_bias else 'nullptr'}, C, "
-        "M, N, K, lda, ldb, ldc);\n}\n")
+        "M, N, K, lda, ldb, ldc, kchunk);\n}\n")
 
 
 def splitk_reduce_kernel(name: str, *, with_bias: bool, bias_mode: str,

@@ -100,7 +100,7 @@ class MfmaSchedule:
         regs = 2 * self.UN * (mi + ni) * 4 + mi * ni * 4
         return (self.WK in (2, 4, 8, 16) and self.BM in (16, 32, 64) and self.BN in (16, 32, 64)
                 and self.MS == 16 and self.WGM == 1 and self.WGN == 1 and self.BK == 16
-                and not self.DB and self.SK == 1 and not self.ST
+                and not self.DB and self.SK >= 1 and not self.ST
                 and self.UN in (1, 2, 4, 8, 16) and regs <= 200
                 and self.WK * mi * ni * 1024 <= LDS_LIMIT)
 
@@ -125,8 +125,8 @@ class MfmaSchedule:
         return self.key() + (f"_SK{self.SK}" if self.SK > 1 else "") + ("_ST" if self.ST else "")
 
     @staticmethod
-    def wsplit(bm: int, bn: int, wk: int, un: int = 1, bt: bool = False) -> "MfmaSchedule":
-        return MfmaSchedule(bm, bn, 16, 1, 1, 16, False, 1, False, un, wk, bt)
+    def wsplit(bm: int, bn: int, wk: int, un: int = 1, bt: bool = False, sk: int = 1) -> "MfmaSchedule":
+        return MfmaSchedule(bm, bn, 16, 1, 1, 16, False, sk, False, un, wk, bt)
 
     def with_split(self, sk: int) -> "MfmaSchedule":
         return MfmaSchedule(self.BM, self.BN, self.BK, self.WGM, self.WGN, self.MS, self.DB, sk,
@@ -164,6 +164,15 @@ def wsplit_search_space() -> Iterator[MfmaSchedule]:
                 for un in (1, 2, 4, 8, 16):
                     for bt in (False, True):
                         s = MfmaSchedule.wsplit(bm, bn, wk, un, bt)
+                        if s.is_valid():
+                            yield s
+    # K also split over workgroups (a split-K workspace and the reduce launch)
+    for bm in (16, 32, 64):
+        for bn in (16, 32, 64):
+            for wk in (4, 8):
+                for un in (1, 2, 4):
+                    for sk in (2, 4, 8, 16):
+                        s = MfmaSchedule.wsplit(bm, bn, wk, un, True, sk)
                         if s.is_valid():
                             yield s
 

@@ -43,6 +43,8 @@ SCHEDULES = [
     MfmaSchedule.wsplit(32, 16, 4, 1, True),                   # weights K-contiguous per column
     MfmaSchedule.wsplit(64, 16, 4, 2),                         # 64-row tile
     MfmaSchedule.wsplit(16, 64, 8, 4, True),                   # 64-column tile, deep stages
+    MfmaSchedule.wsplit(16, 16, 4, 2, True, 3),                # ... and K over 3 workgroups
+    MfmaSchedule.wsplit(32, 32, 8, 1, False, 2),
 ]
 
 
@@ -65,7 +67,7 @@ def _gemm_graph(M, N, K, act, bias, seed=0, trans_b=False):
     return b.graph(), {"A": A}
 
 
-@pytest.mark.parametrize("sched", SCHEDULES, ids=lambda s: s.key())
+@pytest.mark.parametrize("sched", SCHEDULES, ids=lambda s: s.key_full())
 @pytest.mark.parametrize("act,bias", [("Relu", True), (None, False), ("Sigmoid", True)])
 def test_gemm_kernel_matches_oracle(sched, act, bias, hip_ctx):
     assert sched.is_valid()
@@ -83,7 +85,8 @@ def test_gemm_transb_and_ragged_shapes(M, N, K, hip_ctx):
 
 
 @pytest.mark.parametrize("sched", [MfmaSchedule.wsplit(16, 16, 4, 2), MfmaSchedule.wsplit(32, 16, 8, 1, True),
-                                   MfmaSchedule.wsplit(16, 64, 4, 4, True)], ids=lambda s: s.key())
+                                   MfmaSchedule.wsplit(16, 64, 4, 4, True),
+                                   MfmaSchedule.wsplit(16, 32, 4, 1, True, 4)], ids=lambda s: s.key_full())
 @pytest.mark.parametrize("M,N,K", [(1, 1000, 512), (7, 13, 5), (33, 1001, 77), (5, 70, 300)])
 @pytest.mark.parametrize("trans_b", [False, True])
 def test_wave_split_ragged_shapes(M, N, K, trans_b, sched, hip_ctx):
@@ -91,7 +94,7 @@ def test_wave_split_ragged_shapes(M, N, K, trans_b, sched, hip_ctx):
     N, k past K inside a row, steps past a wave's share) all read zero."""
     g, feeds = _gemm_graph(M, N, K, "Relu", True, seed=6, trans_b=trans_b)
     c, got, want = device_run(g, feeds, ctx=hip_ctx, schedule_fn=lambda n, mnk: sched)
-    assert [l.kind for l in c.module.plan] == ["gemm_ws"]
+    assert [l.kind for l in c.module.plan][0] == "gemm_ws"
     assert_close("C", got["C"], want["C"])
 
 
@@ -108,14 +111,17 @@ def test_micro_gemm_shapes(M, N, K, hip_ctx):
                                    MfmaSchedule.wsplit(16, 32, 4, 2), MfmaSchedule.wsplit(16, 16, 16, 8),
                                    MfmaSchedule.wsplit(32, 16, 4, 4), MfmaSchedule.wsplit(16, 16, 8, 2, True),
                                    MfmaSchedule.wsplit(32, 32, 4, 1, True), MfmaSchedule.wsplit(16, 64, 8),
-                                   MfmaSchedule.wsplit(64, 32, 4, 2)], ids=lambda s: s.key())
+                                   MfmaSchedule.wsplit(64, 32, 4, 2), MfmaSchedule.wsplit(16, 16, 8, 2, True, 8),
+                                   MfmaSchedule.wsplit(64, 16, 4, 4, True, 12)], ids=lambda s: s.key_full())
 @pytest.mark.parametrize("M,N,K", SHAPES)
 def test_micro_gemm_wave_split(M, N, K, sched, hip_ctx):
-    """The one-launch wave-split kernel on the micro shapes (16-byte A loads,
-    K % 16 == 0) against the oracle."""
+    """The wave-split kernel on the micro shapes (16-byte A loads, K % 16 ==
+    0) against the oracle: one launch, or with K also split over workgroups
+    the partial launch and the ordered reduce."""
     g, feeds = build_micro_gemm(M, N, K)
     c, got, want = device_run(g, feeds, ctx=hip_ctx, schedule_fn=lambda n, mnk: sched)
-    assert [l.kind for l in c.module.plan] == ["gemm_ws"]
+    kinds = [l.kind for l in c.module.plan]
+    assert kinds == (["gemm_ws", "splitk_reduce"] if sched.SK > 1 else ["gemm_ws"])
     assert_close("C", got["C"], want["C"])
 
 
