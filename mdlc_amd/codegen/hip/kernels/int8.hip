@@ -9,10 +9,25 @@ namespace mdlc {
 
 typedef signed char i8;
 
+// The clamp comes first (its bounds are integers, so clamping before or
+// after the rounding gives the same code); adding 1.5 * 2^23 then rounds to
+// the nearest integer with ties to even (the float addition's own rounding)
+// and leaves that integer in the low mantissa bits: bits = 0x4B400000 + q,
+// whose low byte is q in two's complement. Four instructions a code instead
+// of a round, a convert and the byte packing of 32-bit integers.
+__device__ __forceinline__ int requant_word(int acc, float m, float lo) {
+  const float v = fminf(fmaxf((float)acc * m, lo), 127.0f);
+  return __builtin_bit_cast(int, v + 12582912.0f);
+}
 __device__ __forceinline__ i8 requant(int acc, float m, float lo) {
-  float r = rintf((float)acc * m);
-  r = fminf(fmaxf(r, lo), 127.0f);
-  return (i8)(int)r;
+  return (i8)requant_word(acc, m, lo);
+}
+// The low bytes of four words as one word (byte j from x_j): three byte
+// permutes instead of masks, shifts and ors.
+__device__ __forceinline__ int pack4(int x0, int x1, int x2, int x3) {
+  const unsigned lo = __builtin_amdgcn_perm((unsigned)x1, (unsigned)x0, 0x0c0c0400u);
+  const unsigned hi = __builtin_amdgcn_perm((unsigned)x3, (unsigned)x2, 0x0c0c0400u);
+  return (int)__builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
 template <int MS> struct MfmaI8;
@@ -160,9 +175,16 @@ __device__ __forceinline__ void qgemm_epilogue(const QGemmArgs& g, Acc& acc, int
                 if (col + j < g.N) r.b[j] = g.aux[off + j];
             }
           }
+          if (EPI == 0) {
+            int wq[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            o.b[j] = finish(requant(acc[mi][ni][4 * q + j] + bv[j], mv[j], (float)LO), r.b[j]);
+            for (int j = 0; j < 4; ++j) wq[j] = requant_word(acc[mi][ni][4 * q + j] + bv[j], mv[j], (float)LO);
+            o.w = pack4(wq[0], wq[1], wq[2], wq[3]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              o.b[j] = finish(requant(acc[mi][ni][4 * q + j] + bv[j], mv[j], (float)LO), r.b[j]);
+          }
           if (full) {
             *reinterpret_cast<int*>(cp) = o.w;
           } else {
