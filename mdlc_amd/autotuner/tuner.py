@@ -25,6 +25,7 @@ from typing import Optional
 from mdlc_amd.codegen.schedule import (
     CUS, DEFAULT_GEMM, MfmaSchedule, default_qdw_schedule, default_qschedule, default_schedule,
     gemm_search_space, qdw_search_space, qdw_valid, qgemm_search_space, qsched_valid, split_slices,
+    wsplit_conv_search_space,
     wsplit_search_space,
 )
 
@@ -248,7 +249,10 @@ def problem_candidates(problem: dict, *, budget: int = 24, seed: int = 0) -> lis
         return list(qdw_search_space())
     if is_int8(problem):
         return qcandidates(M, N, K, budget=budget, seed=seed)
-    return candidates(M, N, K, budget=budget, seed=seed, conv=is_implicit_conv(problem))
+    cands = candidates(M, N, K, budget=budget, seed=seed, conv=is_implicit_conv(problem))
+    if is_implicit_conv(problem) and problem.get("C", 1) % 16 == 0 and problem.get("group", 1) == 1:
+        cands += list(wsplit_conv_search_space())      # tap-major gathers on the wave-split kernel
+    return cands
 
 
 def _problem_graph(problem: dict, sched_seed: int = 0):

@@ -242,7 +242,9 @@ class HipCodegen(Int8LoweringMixin):
                    **{k: geo[k] for k in ("C", "H", "W", "KH", "KW", "SH", "SW", "DH", "DW",
                                           "PT", "PB", "PL", "PR", "OH", "OW")}}
         sched = self._schedule(node, (OC, P, K), problem)
-        if self.conv_mode == "implicit" and not sched.conv_valid():
+        if self.conv_mode == "implicit" and sched.WK > 1 and (geo["C"] % 16 or not sched.is_valid()):
+            raise ValueError(f"wave-split schedule {sched.key_full()} needs Cin % 16 == 0")
+        if self.conv_mode == "implicit" and sched.WK == 1 and not sched.conv_valid():
             raise ValueError(f"schedule {sched.key_full()} does not fit the convolution gather "
                              f"(threads per block must be a multiple of BN and BK of NT/BN)")
         tap_major = self.conv_mode == "implicit" and geo["C"] % sched.BK == 0
@@ -267,6 +269,9 @@ class HipCodegen(Int8LoweringMixin):
             win = (geo["KH"], geo["KW"], geo["SH"], geo["SW"], geo["DH"], geo["DW"], geo["PT"], geo["PL"])
             meta.update({"Cin": geo["C"], "H": geo["H"], "W": geo["W"], "OH": OH, "OW": OW,
                          "k_order": "tap" if tap_major else "channel"})
+            if sched.WK > 1:
+                self._emit_conv_ws(sched, wdev, x, bias, y, meta, epi, win)
+                return
             self._emit_gemm("conv", sched, [wdev, x], bias, y, meta, epi, bmode=3 if tap_major else 2,
                             vec_a=lda % 4 == 0, win=win, out_nchw=True)
             return
@@ -550,6 +555,44 @@ class HipCodegen(Int8LoweringMixin):
                                 dict(meta, partial=True,
                                      bytes=meta["bytes"] - extra_bytes + 4 * slices * M * N)))
         self._emit_reduce(ws, bias, extra, out, M, N, slices, epi, meta, act, rtag, residual)
+
+    def _emit_conv_ws(self, sched, wdev, x, bias, y, meta, epi, win) -> None:
+        """A tap-major implicit-GEMM convolution on the wave-split kernel: one
+        launch with the epilogue, or (``sched.SK > 1``) K also split over
+        workgroups into the split-K workspace plus the ordered reduce."""
+        M, N, K = meta["M"], meta["N"], meta["K"]
+        batch = meta["out_4d"][0]
+        if max(4 * batch * meta["Cin"] * meta["H"] * meta["W"], 4 * M * K, 4 * M * N) >= 0x7ffffff0:
+            raise NotImplementedError("HIP codegen: conv operands exceed the wave-split kernel's "
+                                      "2 GiB buffer range")
+        slices, chunk = split_slices(K, sched)
+        tiles = -(-M // sched.BM) * -(-N // sched.BN)
+        block = (sched.threads_per_block(), 1, 1)
+        act = epi["act"]
+        residual, res = epi.get("residual"), epi.get("res_input")
+        extra = [res] if res else []
+        meta = dict(meta, ksplit=slices, kchunk=chunk, ldc=0, hw=epi["hw"])
+        if slices == 1:
+            sig = ("conv_ws", sched, win, bool(bias), epi["act_sig"], residual)
+            kname = self._kernel(sig, lambda i: T.conv_wsplit_kernel(
+                f"conv_{sched.key()}_{act or 'none'}{'_res' if residual else ''}_{i}", sched, win,
+                with_bias=bool(bias), activation=act, attrs=epi["attrs"], residual=residual))
+            self.plan.append(Launch("conv_ws", kname, [wdev, x] + bias + extra, [y], (tiles, 1, 1),
+                                    block, meta))
+            return
+        ws = y + "__splitk"
+        self.scratch[ws] = (slices * M, N)
+        self.scratch_class[ws] = "splitk"
+        sig = ("conv_ws", sched, win, "partial")
+        kname = self._kernel(sig, lambda i: T.conv_wsplit_kernel(
+            f"conv_{sched.key()}_SK{slices}_{i}", sched, win, with_bias=False, activation=None,
+            attrs={}))
+        extra_bytes = 4 * (M * N * (1 + len(extra)) + M * len(bias))
+        self.plan.append(Launch("conv_ws", kname, [wdev, x], [ws], (tiles, slices, 1), block,
+                                dict(meta, partial=True, ldc=N,
+                                     bytes=meta["bytes"] - extra_bytes + 4 * slices * M * N)))
+        self._emit_reduce(ws, bias, extra, y, M, N, slices, epi, meta, act,
+                          "_res" if residual else "", residual)
 
     def _emit_reduce(self, ws, bias, extra, out, M, N, slices, epi, meta, act, rtag, residual) -> None:
         """The split-K reduce launch: adds the ``slices`` partial sums in ws in

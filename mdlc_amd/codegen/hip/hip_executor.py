@@ -148,6 +148,10 @@ class HipExecutor:
             args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
             args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["ldb"]), I(m["ldc"]),
                      I(m["kchunk"])]
+        elif k == "conv_ws":
+            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+            args += [I(m[f]) for f in ("M", "N", "K", "lda", "Cin", "H", "W", "OH", "OW", "ldc",
+                                       "kchunk")]
         elif k == "conv":
             args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
             args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["Cin"]), I(m["H"]),

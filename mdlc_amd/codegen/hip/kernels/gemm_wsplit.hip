@@ -31,12 +31,24 @@ namespace mdlc {
 // of K each, a multiple of 16); workgroup y writes its raw partial tile to
 // slice y of the split-K workspace, C[(y * M + row) * ldc + col], for
 // splitk_reduce_f32 to add in slice order and finish.
-template <int MI, int NI, int WK, int UN, bool VA, bool BKN, class Epi, bool SPLIT = false>
+//
+// CONV: B is the implicit-GEMM view of an NCHW convolution input (Win the
+// window), K ordered (kh, kw, c) with Cin % 16 == 0, so the 16 k of a step
+// share one tap and a lane's four are consecutive channels: per step and
+// column block one bounds check and one base offset (the tap's pixel), the
+// channels one plane (H*W floats) apart. A holds the weights as [OC][K] in
+// that order; column p = (image, pixel) and the output goes to NCHW, with
+// the folded residual (Epi::residual, read at the output's own position).
+template <int MI, int NI, int WK, int UN, bool VA, bool BKN, class Epi, bool SPLIT = false,
+          class Win = NoWin, bool CONV = false>
 __device__ __forceinline__ void gemm_f32_wsplit(const float* __restrict__ A,
                                                 const float* __restrict__ B,
                                                 const float* __restrict__ bias,
                                                 float* __restrict__ C, int M, int N, int K,
-                                                int lda, int ldb, int ldc, int kchunk) {
+                                                int lda, int ldb, int ldc, int kchunk,
+                                                const float* __restrict__ res = nullptr,
+                                                int Cin = 0, int H = 0, int W = 0, int OH = 0,
+                                                int OW = 0) {
   constexpr int TM = 16 * MI, TN = 16 * NI;
   __shared__ __attribute__((aligned(16))) floatx4 red[WK][MI][NI][64];
 
@@ -67,7 +79,24 @@ __device__ __forceinline__ void gemm_f32_wsplit(const float* __restrict__ A,
   // compiler, which then waits for all of them at each step.) The step's k0
   // moves the resource base (scalar work); the per-lane offsets stay fixed.
   const int a_bytes = M * lda * 4;
-  const int b_bytes = BKN ? N * ldb * 4 : K * ldb * 4;
+  const int b_bytes = CONV ? (N / (OH * OW)) * Cin * H * W * 4 : (BKN ? N * ldb * 4 : K * ldb * 4);
+  const int HW = H * W;
+  // CONV: per column block the lane's image offset and window corner; a
+  // column past N gets a corner no tap reaches
+  int cimg[CONV ? NI : 1], cih[CONV ? NI : 1], ciw[CONV ? NI : 1];
+  if (CONV) {
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) {
+      const int p = n0 + ni * 16 + li;
+      const int ohw = OH * OW;
+      const int img = p / ohw;
+      const int pix = p - img * ohw;
+      const int oh = pix / OW;
+      cimg[ni] = (img * Cin + 4 * lg) * HW;
+      cih[ni] = p < N ? oh * Win::SH - Win::PT : -(1 << 28);
+      ciw[ni] = (pix - oh * OW) * Win::SW - Win::PL;
+    }
+  }
   int aoff[MI];
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
@@ -103,8 +132,9 @@ __device__ __forceinline__ void gemm_f32_wsplit(const float* __restrict__ A,
       const bool live = s + u < s1;
       const __amdgpu_buffer_rsrc_t rA = buffer_over(A + k0, live ? max(a_bytes - k0 * 4, 0) : 0);
       const __amdgpu_buffer_rsrc_t rB =
-          BKN ? buffer_over(B + k0, live ? max(b_bytes - k0 * 4, 0) : 0)
-              : buffer_over(B + (size_t)k0 * ldb, live ? max(b_bytes - k0 * ldb * 4, 0) : 0);
+          CONV ? buffer_over(B, live ? b_bytes : 0)
+               : BKN ? buffer_over(B + k0, live ? max(b_bytes - k0 * 4, 0) : 0)
+                     : buffer_over(B + (size_t)k0 * ldb, live ? max(b_bytes - k0 * ldb * 4, 0) : 0);
       // k past K inside a row (only without VA): its element's offset is
       // pushed out of range per lane
       const int kl = k0 + 4 * lg;
@@ -122,9 +152,21 @@ __device__ __forceinline__ void gemm_f32_wsplit(const float* __restrict__ A,
                 rA, kl + q < K ? aoff[mi] + 4 * q : kOutside, 0, 0));
         }
       }
+      // CONV: the step's tap and first channel (wave-uniform, scalar)
+      const int tap = CONV ? k0 / Cin : 0;
+      const int kh = tap / Win::KW, kw = tap - (tap / Win::KW) * Win::KW;
+      const int cofs = (k0 - tap * Cin) * HW;
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni) {
-        if (BKN && VA) {
+        if (CONV) {
+          const int ih = cih[ni] + kh * Win::DH, iw = ciw[ni] + kw * Win::DW;
+          const bool ok = (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+          const int base = (cimg[ni] + cofs + ih * W + iw) * 4;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            bv[buf][u][ni][q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                rB, ok ? base + q * HW * 4 : kOutside, 0, 0));
+        } else if (BKN && VA) {
           const floatx4 v = __builtin_bit_cast(
               floatx4, __builtin_amdgcn_raw_buffer_load_b128(rB, boff[ni][0], 0, 0));
 #pragma unroll
@@ -196,6 +238,14 @@ __device__ __forceinline__ void gemm_f32_wsplit(const float* __restrict__ A,
     if (gr < M && gc < N) {
       if (SPLIT) {
         C[((size_t)blockIdx.y * M + gr) * ldc + gc] = v;
+      } else if (CONV) {
+        const int ohw = OH * OW;
+        const int img = gc / ohw;
+        const size_t o = ((size_t)img * M + gr) * ohw + (gc - img * ohw);
+        const float b = Epi::bias == 1 ? bias[gr] : 0.f;
+        float r = Epi::apply(v, b);
+        if (Epi::residual) r = Epi::post(r, res[o]);
+        C[o] = r;
       } else {
         const float b = Epi::bias == 2 ? bias[gc] : (Epi::bias == 1 ? bias[gr] : 0.f);
         C[(size_t)gr * ldc + gc] = Epi::apply(v, b);

@@ -228,6 +228,38 @@ def gemm_wsplit_kernel(name: str, sched: MfmaSchedule, *, with_bias: bool, bias_
         "M, N, K, lda, ldb, ldc, kchunk);\n}\n")
 
 
+def conv_wsplit_kernel(name: str, sched: MfmaSchedule, win: tuple, *, with_bias: bool,
+                       activation: Optional[str], attrs: dict,
+                       residual: Optional[str] = None) -> tuple:
+    """The wave-split kernel on an implicit-GEMM convolution (K ordered
+    (kh, kw, c), Cin % 16 == 0): ABI (W, x, [bias], [res], y, int M, int N,
+    int K, int lda, int Cin, int H, int W, int OH, int OW, int ldc,
+    int kchunk); grid x the BM x BN tiles (M = output channels, N = batch x
+    output pixels), y the K slices. Without a split the epilogue (bias,
+    activation, folded residual) writes NCHW output; with ``sched.SK > 1`` y
+    is the split-K workspace (row-major, ``ldc`` = N) and
+    ``splitk_reduce_kernel`` finishes."""
+    s = sched
+    split = s.SK > 1
+    if split:
+        with_bias, activation, residual = False, None, None
+    epi = f"{name}_epi"
+    src = epilogue_struct(epi, bias_mode="row" if with_bias else None, activation=activation,
+                          attrs=attrs, residual=residual)
+    winty = "mdlc::ConvWin<%d, %d, %d, %d, %d, %d, %d, %d>" % tuple(win)
+    bias_arg = ("const float* __restrict__ bias, " if with_bias else "") + \
+        ("const float* __restrict__ res, " if residual else "")
+    return name, src + (
+        f'extern "C" __global__ __launch_bounds__({s.threads_per_block()}) void {name}(\n'
+        f"    const float* __restrict__ A, const float* __restrict__ B, {bias_arg}"
+        "float* __restrict__ C, int M, int N,\n    int K, int lda, int Cin, int H, int W, int OH, "
+        "int OW, int ldc, int kchunk) {\n"
+        f"  mdlc::gemm_f32_wsplit<{s.BM // 16}, {s.BN // 16}, {s.WK}, {s.UN}, true, false, {epi}, "
+        f"{'true' if split else 'false'}, {winty}, true>(A, B, "
+        f"{'bias' if with_bias else 'nullptr'}, C, M, N, K, lda, 0, ldc, kchunk, "
+        f"{'res' if residual else 'nullptr'}, Cin, H, W, OH, OW);\n}}\n")
+
+
 def splitk_reduce_kernel(name: str, *, with_bias: bool, bias_mode: str,
                          activation: Optional[str], attrs: dict, alpha: float = 1.0,
                          beta: float = 1.0, residual: Optional[str] = None, vec: int = 1,

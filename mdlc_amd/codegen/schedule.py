@@ -177,6 +177,19 @@ def wsplit_search_space() -> Iterator[MfmaSchedule]:
                             yield s
 
 
+def wsplit_conv_search_space() -> Iterator[MfmaSchedule]:
+    """Wave-split forms for tap-major implicit-GEMM convolutions (Cin % 16 ==
+    0): the weights are dense K-contiguous rows, so no ``BT`` variants."""
+    for bm in (16, 32, 64):
+        for bn in (16, 32, 64):
+            for wk in (4, 8, 16):
+                for un in (1, 2):
+                    for sk in (1, 2, 4, 8):
+                        s = MfmaSchedule.wsplit(bm, bn, wk, un, False, sk)
+                        if s.is_valid():
+                            yield s
+
+
 def split_slices(K: int, sched: MfmaSchedule) -> tuple:
     """(slices, chunk): K cut into chunks that are multiples of BK, with no
     empty slice."""

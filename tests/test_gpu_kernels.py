@@ -177,6 +177,60 @@ def test_conv_matches_oracle(case, mode, hip_ctx):
     assert_close("y", got["y"], want["y"])
 
 
+WS_CONV_CASES = [
+    # n, c, h, w, oc, k, s, p: Cin % 16 == 0 (taps whole per 16-deep K step)
+    (1, 16, 9, 9, 24, 3, 1, 1),
+    (2, 32, 7, 7, 48, 3, 1, 1),          # tiles cross images (49 pixels an image)
+    (3, 16, 14, 14, 40, 3, 2, 1),
+    (2, 64, 14, 14, 72, 1, 2, 0),
+    (1, 128, 5, 5, 96, 3, 1, 1),
+]
+
+
+@pytest.mark.parametrize("sched", [MfmaSchedule.wsplit(16, 16, 4, 1), MfmaSchedule.wsplit(32, 16, 8, 2),
+                                   MfmaSchedule.wsplit(16, 64, 4, 2, False, 3),
+                                   MfmaSchedule.wsplit(64, 32, 8, 1, False, 2)],
+                         ids=lambda s: s.key_full())
+@pytest.mark.parametrize("case", WS_CONV_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_conv_wave_split(case, sched, hip_ctx):
+    """The wave-split kernel on tap-major implicit-GEMM convolutions (padding
+    taps, stride 2, 1x1, columns of one tile in several images), with the
+    bias/ReLU epilogue, or K also split over workgroups and the reduce."""
+    g, feeds = _conv_graph(*case)
+    c, got, want = device_run(g, feeds, ctx=hip_ctx, winograd=False, small_conv=False,
+                              schedule_fn=lambda n, mnk: sched)
+    kinds = [l.kind for l in c.module.plan]
+    assert kinds == (["conv_ws", "splitk_reduce"] if sched.SK > 1 else ["conv_ws"])
+    assert_close("y", got["y"], want["y"])
+
+
+def test_resnet18_b1_wave_split_convs(hip_ctx):
+    """ResNet-18 batch 1 with every conv of 16 or more input channels on the
+    wave-split kernel (residual adds folded into its epilogue or the split-K
+    reduce), each fused group in isolation on the oracle's inputs."""
+    from mdlc_amd.codegen.hip.hip_executor import HipExecutor
+    from mdlc_amd.compiler import compile_graph
+    from mdlc_amd.tools.build_resnet18 import build_resnet18, make_input
+    from oracle.reference import run_reference
+
+    def fn(node, mnk):
+        M, N, K = mnk
+        return MfmaSchedule.wsplit(16, 32, 8, 1, False, 4 if K >= 2304 else 1)
+
+    x = make_input(1)
+    c = compile_graph(build_resnet18(batch=1), feeds={"input": x}, schedule_fn=fn, winograd=False)
+    assert sum(l.kind == "conv_ws" for l in c.module.plan) == 19
+    want = run_reference(c.graph, {"input": x}, return_all=True)
+    ex = HipExecutor(c.module, hip_ctx)
+    try:
+        ex._upload_feeds({"input": x})
+        got = ex.run_isolated(want)
+    finally:
+        ex.close()
+    for t, v in got.items():
+        assert_close(t, v, want[t])
+
+
 SMALLC_CASES = [
     # n, c, h, w, oc, k, s, p, act, bias: every tile rule, ragged edges, OC not a multiple of 32
     (2, 3, 30, 30, 64, 7, 2, 3, "Relu", True),
