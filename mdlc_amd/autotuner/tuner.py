@@ -180,6 +180,15 @@ class AutotuneCache:
             json.dump(self.entries, f, indent=1, sort_keys=True)
 
 
+def conv_schedule_ok(sched: MfmaSchedule, problem: dict) -> bool:
+    """A schedule the implicit-GEMM conv lowering accepts for this problem:
+    the tiled gather kernels', or a wave-split form when the K steps hold
+    whole taps (Cin % 16 == 0, one group)."""
+    if sched.WK > 1:
+        return sched.is_valid() and problem.get("C", 1) % 16 == 0 and problem.get("group", 1) == 1
+    return sched.conv_valid()
+
+
 def is_implicit_conv(problem: dict) -> bool:
     """True for convolutions lowered to the implicit-GEMM gather kernels,
     whose schedules must also satisfy ``MfmaSchedule.conv_valid``."""
@@ -445,7 +454,8 @@ class Tuner:
                 return hit
             if not self.tune_misses:
                 return default_qschedule(problem["M"], problem["N"], problem["K"])
-        elif hit is not None and (hit.conv_valid() if is_implicit_conv(problem) else hit.is_valid()):
+        elif hit is not None and (conv_schedule_ok(hit, problem) if is_implicit_conv(problem)
+                                  else hit.is_valid()):
             return hit
         if not self.tune_misses:
             return default_schedule(problem["M"], problem["N"], problem["K"])
