@@ -127,7 +127,7 @@ def test_measured_tuning_picks_a_correct_schedule(hip_ctx):
     res = tune_problem(problem, budget=4, ctx=hip_ctx)
     assert res.measured and res.n_evaluated >= 4 and res.rejected == []
     assert all(ms > 0 for _, ms in res.ranking)
-    assert res.best.conv_valid()
+    assert conv_schedule_ok(res.best, problem)
     g, feeds = _problem_graph(problem)
     _, got, want = device_run(g, feeds, ctx=hip_ctx, schedule_fn=lambda n, mnk: res.best,
                               small_conv=False)
