@@ -25,7 +25,7 @@ from typing import Optional
 from mdlc_amd.codegen.schedule import (
     CUS, DEFAULT_GEMM, MfmaSchedule, default_qdw_schedule, default_qschedule, default_schedule,
     gemm_search_space, qdw_search_space, qdw_valid, qgemm_search_space, qsched_valid, split_slices,
-    wsplit_conv_search_space,
+    unsplit_if_one_slice, wsplit_conv_search_space,
     wsplit_search_space,
 )
 
@@ -230,7 +230,7 @@ def candidates(M: int, N: int, K: int, *, budget: int = 24, seed: int = 0, extra
     pick += [s.with_unroll(2) for s in [s for s in pick if s.DB and s.UN == 1][:unroll]]
     if not conv:                      # dense GEMMs: every wave-split form is measured too
         pick += list(wsplit_search_space())
-    return pick
+    return unique_forms(pick, K)
 
 
 def _tiles(s: MfmaSchedule, M: int, N: int) -> int:
@@ -261,7 +261,19 @@ def problem_candidates(problem: dict, *, budget: int = 24, seed: int = 0) -> lis
     cands = candidates(M, N, K, budget=budget, seed=seed, conv=is_implicit_conv(problem))
     if is_implicit_conv(problem) and problem.get("C", 1) % 16 == 0 and problem.get("group", 1) == 1:
         cands += list(wsplit_conv_search_space())      # tap-major gathers on the wave-split kernel
-    return cands
+    return unique_forms(cands, K)
+
+
+def unique_forms(cands: list, K: int) -> list:
+    """The candidates as the lowering will build them (a split that leaves
+    one slice of K is no split), each form once, in first-seen order."""
+    seen, out = set(), []
+    for s in cands:
+        s = unsplit_if_one_slice(s, K)
+        if s not in seen:
+            seen.add(s)
+            out.append(s)
+    return out
 
 
 def _problem_graph(problem: dict, sched_seed: int = 0):

@@ -47,7 +47,8 @@ from mdlc_amd.codegen.hip import templates as T
 from mdlc_amd.codegen.hip.emit_int8 import Int8LoweringMixin
 from mdlc_amd.codegen.hip.plan import LIBRARY_PARTS, QUANT_OPS, HipModule, Launch, round4, round16  # noqa: F401
 from mdlc_amd.codegen.schedule import (WINO_BK, WINO_BM, WINO_BN, MfmaSchedule, default_schedule,
-                                      smallc_fits, smallc_pairs, smallc_tile, split_slices, wino_fits,
+                                      smallc_fits, smallc_pairs, smallc_tile, split_slices,
+                                      unsplit_if_one_slice, wino_fits,
                                       wino_patch, wino_pays, wino_slices)
 from mdlc_amd.ir import DType, Graph, Node
 from mdlc_amd.passes.fuse_elementwise import ELEMENTWISE
@@ -124,7 +125,7 @@ class HipCodegen(Int8LoweringMixin):
         sched = fn(problem) if fn is not None else self.schedule_fn(node, mnk)
         if not sched.is_valid():
             raise ValueError(f"invalid schedule {sched} for {mnk}")
-        return sched
+        return unsplit_if_one_slice(sched, mnk[2])
 
     def _kernel(self, sig: tuple, make) -> str:
         """Return the kernel for ``sig``, generating it once."""

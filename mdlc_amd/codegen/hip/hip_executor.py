@@ -21,15 +21,93 @@ drift accumulated along the chain.
 
 from __future__ import annotations
 
+from dataclasses import dataclass, field
 from typing import Optional
 
 import numpy as np
 
+from mdlc_amd.codegen.hip.abi import check_launch, declared_kinds
 from mdlc_amd.codegen.hip.emit import HipModule, Launch
 from mdlc_amd.codegen.hip.hiprtc_runtime import (STATIC_SCRATCH_BYTES, Arg, HipContext, HipError, Plan,
                                                  compile_code_object)
 from mdlc_amd.ir import DType
 from mdlc_amd.runtime.memory_planner import align_up, plan_memory
+
+
+@dataclass
+class ArenaLayout:
+    """Byte offsets of every tensor in the executor's one allocation:
+    constants (sorted by name), runtime inputs, the planner's pooled buffers,
+    then one scratch region per class (or, with ``static_scratch``, offsets
+    into the separate workspace in ``ws_offsets``)."""
+    mem_plan: object
+    offsets: dict = field(default_factory=dict)
+    shapes: dict = field(default_factory=dict)
+    dtypes: dict = field(default_factory=dict)
+    ws_offsets: dict = field(default_factory=dict)
+    ws_bytes: int = 0
+    arena_bytes: int = 0
+    constants: dict = field(default_factory=dict)
+
+    def nbytes(self, name: str) -> int:
+        return int(np.prod(self.shapes[name], dtype=np.int64)) * np.dtype(self.dtypes[name]).itemsize
+
+
+def arena_layout(module: HipModule, *, static_scratch: bool = False) -> ArenaLayout:
+    """The arena layout ``HipExecutor`` allocates for ``module`` (no device
+    needed)."""
+    g = module.graph
+    lay = ArenaLayout(plan_memory(g))
+    cur = 0
+    const_vals: dict = {}
+    for l in module.plan:
+        for e in l.inputs:
+            if e in module.device_constants:
+                const_vals[e] = module.device_constants[e]
+            elif g.is_constant(e):
+                const_vals[e] = np.asarray(g.initializers[e])
+    for name in sorted(const_vals):
+        arr = np.ascontiguousarray(const_vals[name])
+        lay.constants[name] = arr
+        lay.offsets[name] = cur
+        lay.shapes[name], lay.dtypes[name] = arr.shape, arr.dtype
+        cur += align_up(arr.nbytes)
+    for name in g.runtime_inputs:
+        info = g.info(name)
+        lay.offsets[name] = cur
+        lay.shapes[name] = tuple(info.shape)
+        lay.dtypes[name] = DType.to_numpy(info.dtype)
+        cur += align_up(info.nbytes())
+    act_base = cur
+    for t, bid in lay.mem_plan.assignment.items():
+        info = g.info(t)
+        lay.offsets[t] = act_base + lay.mem_plan.offsets[bid]
+        lay.shapes[t] = tuple(info.shape)
+        lay.dtypes[t] = DType.to_numpy(info.dtype)
+    cur = act_base + lay.mem_plan.arena_bytes
+    regions: dict = {}
+    for name, (r, ld) in module.scratch_shapes.items():
+        cls = module.scratch_class.get(name, "cols")
+        regions[cls] = max(regions.get(cls, 0), r * ld * 4)
+    region_at: dict = {}
+    ws = 0                                  # static mode: offsets within the workspace
+    for cls in sorted(regions):
+        if static_scratch:
+            region_at[cls] = ws
+            ws += align_up(regions[cls])
+        else:
+            region_at[cls] = cur
+            cur += align_up(regions[cls])
+    for name, (r, ld) in module.scratch_shapes.items():
+        at = region_at[module.scratch_class.get(name, "cols")]
+        if static_scratch:
+            lay.ws_offsets[name] = at
+        else:
+            lay.offsets[name] = at
+        lay.shapes[name], lay.dtypes[name] = (r, ld), np.dtype(np.float32)
+    lay.ws_bytes = ws
+    lay.arena_bytes = cur
+    return lay
 
 
 class HipExecutor:
@@ -42,8 +120,13 @@ class HipExecutor:
         scratch, so ``run`` allocates no device memory for them."""
         self.module = module
         self.static_scratch = static_scratch
+        # every launch's arguments against its kernel's declaration, before
+        # any device call
+        self._declared = declared_kinds("\n".join(module.kernels.values()))
+        for l in module.plan:
+            check_launch(l.kernel_name, self._declared,
+                         [a.kind for a in launch_args(l, lambda e: Arg.ptr(0))])
         self.ctx = ctx or HipContext()
-        g = module.graph
         self.code = self.ctx.load_code(compile_code_object(module.sources(), arch=self.ctx.arch,
                                                            use_cache=use_cache))
         self.funcs = {name: self.code.func(name) for name in module.kernels}
@@ -52,63 +135,15 @@ class HipExecutor:
                 self.funcs[l.kernel_name] = self.code.func(l.kernel_name)
 
         # ---- arena layout ------------------------------------------------
-        self.mem_plan = plan_memory(g)
-        self.offsets: dict = {}
-        self.shapes: dict = {}
-        self.dtypes: dict = {}
-        cur = 0
-        const_vals: dict = {}
-        for l in module.plan:
-            for e in l.inputs:
-                if e in module.device_constants:
-                    const_vals[e] = module.device_constants[e]
-                elif g.is_constant(e):
-                    const_vals[e] = np.asarray(g.initializers[e])
-        for name in sorted(const_vals):
-            arr = np.ascontiguousarray(const_vals[name])
-            const_vals[name] = arr
-            self.offsets[name] = cur
-            self.shapes[name], self.dtypes[name] = arr.shape, arr.dtype
-            cur += align_up(arr.nbytes)
-        for name in g.runtime_inputs:
-            info = g.info(name)
-            self.offsets[name] = cur
-            self.shapes[name] = tuple(info.shape)
-            self.dtypes[name] = DType.to_numpy(info.dtype)
-            cur += align_up(info.nbytes())
-        act_base = cur
-        for t, bid in self.mem_plan.assignment.items():
-            info = g.info(t)
-            self.offsets[t] = act_base + self.mem_plan.offsets[bid]
-            self.shapes[t] = tuple(info.shape)
-            self.dtypes[t] = DType.to_numpy(info.dtype)
-        cur = act_base + self.mem_plan.arena_bytes
-        regions: dict = {}
-        for name, (r, ld) in module.scratch_shapes.items():
-            cls = module.scratch_class.get(name, "cols")
-            regions[cls] = max(regions.get(cls, 0), r * ld * 4)
-        region_at: dict = {}
-        ws = 0                                  # static mode: offsets within the workspace
-        for cls in sorted(regions):
-            if static_scratch:
-                region_at[cls] = ws
-                ws += align_up(regions[cls])
-            else:
-                region_at[cls] = cur
-                cur += align_up(regions[cls])
-        self.ws_offsets: dict = {}
-        for name, (r, ld) in module.scratch_shapes.items():
-            at = region_at[module.scratch_class.get(name, "cols")]
-            if static_scratch:
-                self.ws_offsets[name] = at
-            else:
-                self.offsets[name] = at
-            self.shapes[name], self.dtypes[name] = (r, ld), np.dtype(np.float32)
-        self.ws_bytes = ws
-        if static_scratch and ws > STATIC_SCRATCH_BYTES:
-            raise HipError(f"the plan's workspace of {ws} bytes exceeds the static scratch of "
-                           f"{STATIC_SCRATCH_BYTES} bytes; run it with the arena's workspace")
-        self.arena_bytes = cur
+        lay = arena_layout(module, static_scratch=static_scratch)
+        self.mem_plan = lay.mem_plan
+        self.offsets, self.shapes, self.dtypes = lay.offsets, lay.shapes, lay.dtypes
+        self.ws_offsets, self.ws_bytes = lay.ws_offsets, lay.ws_bytes
+        if static_scratch and self.ws_bytes > STATIC_SCRATCH_BYTES:
+            raise HipError(f"the plan's workspace of {self.ws_bytes} bytes exceeds the static scratch "
+                           f"of {STATIC_SCRATCH_BYTES} bytes; run it with the arena's workspace")
+        self.arena_bytes = cur = lay.arena_bytes
+        const_vals = lay.constants
         self.arena = self.ctx.malloc(max(cur, 256))
         self.base = int(self.arena.value)
         for name, arr in const_vals.items():
@@ -136,107 +171,8 @@ class HipExecutor:
         return Arg.ptr(self.ptr(e))
 
     def _record(self, l: Launch) -> tuple:
-        m = l.meta
-        P = self._arg_ptr
-        I = Arg.i32  # noqa: E741
-        k = l.kind
-        if k == "gemm":
-            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
-            args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["ldb"]), I(m["ldc"]),
-                     I(m["hw"]), I(m["ksplit"]), I(m["kchunk"])]
-        elif k == "gemm_ws":
-            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
-            args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["ldb"]), I(m["ldc"]),
-                     I(m["kchunk"])]
-        elif k == "conv_ws":
-            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
-            args += [I(m[f]) for f in ("M", "N", "K", "lda", "Cin", "H", "W", "OH", "OW", "ldc",
-                                       "kchunk")]
-        elif k == "conv":
-            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
-            args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["Cin"]), I(m["H"]),
-                     I(m["W"]), I(m["OH"]), I(m["OW"]), I(m["ksplit"]), I(m["kchunk"])]
-        elif k == "gconv":
-            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
-            args += [I(m[f]) for f in ("M", "N", "K", "lda", "Cin", "H", "W", "OH", "OW", "ksplit",
-                                       "kchunk", "ximg", "cimg")]
-        elif k == "wino":
-            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
-            args += [I(m[f]) for f in ("N", "C", "H", "W", "OC", "OH", "OW", "TH", "TW", "CP", "OCP",
-                                       "PT", "PL", "nchunk")]
-        elif k == "conv_smallc":
-            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
-            args += [I(m[f]) for f in ("batch", "H", "W", "OC", "OH", "OW")]
-        elif k == "streamk_fixup":
-            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
-            args += [I(m[f]) for f in ("M", "N", "K", "full", "ldc", "hw")]
-        elif k == "splitk_reduce":
-            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
-            args += [I(m["S"]), I(m["M"]), I(m["N"]), I(m["ldc"]), I(m["hw"])]
-        elif k == "im2col":
-            args = [P(l.inputs[0]), P(l.outputs[0])]
-            args += [I(m[f]) for f in ("C", "H", "W", "KH", "KW", "OH", "OW", "SH", "SW",
-                                       "PH", "PW", "DH", "DW", "batch", "ldc")]
-        elif k == "dwconv":
-            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
-            args += [I(m[f]) for f in ("N", "C", "H", "W", "OC", "OH", "OW", "PT", "PL")]
-        elif k == "elementwise":
-            args = [P(e) for e in l.inputs] + [P(o) for o in l.outputs] + [I(m["N"])]
-        elif k in ("maxpool", "avgpool"):
-            args = [P(l.inputs[0]), P(l.outputs[0])]
-            args += [I(m[f]) for f in ("planes", "H", "W", "OH", "OW", "KH", "KW", "SH", "SW",
-                                       "PT", "PL", "DH", "DW")]
-        elif k == "gap":
-            args = [P(l.inputs[0]), P(l.outputs[0]), I(m["planes"]), I(m["HW"])]
-        elif k == "softmax":
-            args = [P(l.inputs[0]), P(l.outputs[0])]
-            args += ([Arg.i64(m["outer"]), I(m["L"])] if m["rows"] else
-                     [Arg.i64(m["outer"]), I(m["L"]), I(m["inner"])])
-        elif k == "transpose":
-            args = [P(l.inputs[0]), P(l.outputs[0]), Arg.i64(m["total"]), Arg.dims6(m["out_dims"]),
-                    Arg.dims6(m["src_strides"])]
-        elif k == "pad":
-            args = [P(l.inputs[0]), P(l.outputs[0]), Arg.i64(m["total"]), Arg.dims6(m["out_dims"]),
-                    Arg.dims6(m["in_dims"]), Arg.dims6(m["before"], fill=0), Arg.f32(m["value"])]
-        elif k == "concat":
-            args = [P(l.inputs[0]), P(l.outputs[0])] + [Arg.i64(m[f]) for f in
-                                                         ("rows", "run", "dst_stride", "dst_off")]
-        elif k == "copy":
-            args = [P(l.inputs[0]), P(l.outputs[0]), Arg.i64(m["nbytes"])]
-        elif k == "quantize":
-            args = [P(l.inputs[0]), P(l.outputs[0]), I(m["N"]), I(m["C"]), I(m["HW"]),
-                    Arg.f32(m["inv_s"])]
-        elif k == "qgemm":
-            args = [P(e) for e in l.inputs[:4]] + [P(l.outputs[0])]
-            args += [P(l.inputs[4]) if len(l.inputs) > 4 else Arg.ptr(0)]
-            args += [I(m[f]) for f in ("M", "N", "K", "lda", "ldb", "ldc", "Cin", "H", "W", "OH", "OW")]
-            args += [Arg.f32(m.get("res_mult", 0.0)), Arg.f32(m.get("acc_mult", 0.0))]
-        elif k == "qconv_first":
-            args = [P(l.inputs[0]), Arg.f32(m["inv_s"])] + [P(e) for e in l.inputs[1:4]]
-            args += [P(l.inputs[4]) if len(l.inputs) > 4 else Arg.ptr(0), P(l.outputs[0])]
-            args += [I(m[f]) for f in ("N", "H", "W", "OH", "OW")]
-        elif k == "qmlp":
-            args = [P(e) for e in l.inputs]
-            if not m["mixer"]:                     # no token mixer: null Wd, bd, md
-                args[1:1] = [Arg.ptr(0)] * 3
-            args += [P(l.outputs[0]), I(m["M"]), I(m["H"]), I(m["W"]), Arg.f32(m["res_mult"]),
-                     Arg.f32(m["acc_mult"])]
-        elif k == "qdwconv":
-            args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
-            args += [I(m[f]) for f in ("N", "C", "H", "W", "OH", "OW", "PT", "PL")]
-        elif k == "qadd":
-            args = [P(l.inputs[0]), P(l.inputs[1]), P(l.outputs[0]), Arg.i64(m["n"]),
-                    Arg.f32(m["ma"]), Arg.f32(m["mb"])]
-        elif k == "qlut":
-            args = [P(l.inputs[0]), P(l.inputs[1]), P(l.outputs[0]), Arg.i64(m["n"])]
-        elif k == "qgap":
-            args = [P(l.inputs[0]), P(l.outputs[0]), I(m["N"]), I(m["C"]), I(m["HW"]),
-                    Arg.f32(m["m"])]
-        elif k == "dequantize":
-            args = [P(l.inputs[0]), P(l.outputs[0]), Arg.i64(m["n"]), I(m["C"]), I(m["HW"]),
-                    Arg.f32(m["s"])]
-        else:
-            raise HipError(f"launch kind {k!r} has no device implementation")
+        args = launch_args(l, self._arg_ptr)
+        check_launch(l.kernel_name, self._declared, [a.kind for a in args])
         return (self.funcs[l.kernel_name].value, l.grid, l.block, 0, args)
 
     # ---- execution ----------------------------------------------------------
@@ -351,3 +287,111 @@ def run_on_gpu(module: HipModule, feeds: dict, *, timing: bool = False) -> dict:
         return ex.run(feeds, timing=timing)
     finally:
         ex.close()
+
+
+def launch_args(l: Launch, arg_ptr) -> list:
+    """The packed argument list of one launch, in its kernel's ABI order.
+    ``arg_ptr(tensor)`` gives the ``Arg`` for a tensor's device address (a
+    pointer, or an offset into the plan's workspace)."""
+    m = l.meta
+    P = arg_ptr
+    I = Arg.i32  # noqa: E741
+    k = l.kind
+    if k == "gemm":
+        args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+        args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["ldb"]), I(m["ldc"]),
+                 I(m["hw"]), I(m["ksplit"]), I(m["kchunk"])]
+    elif k == "gemm_ws":
+        args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+        args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["ldb"]), I(m["ldc"]),
+                 I(m["kchunk"])]
+    elif k == "conv_ws":
+        args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+        args += [I(m[f]) for f in ("M", "N", "K", "lda", "Cin", "H", "W", "OH", "OW", "ldc",
+                                   "kchunk")]
+    elif k == "conv":
+        args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+        args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["Cin"]), I(m["H"]),
+                 I(m["W"]), I(m["OH"]), I(m["OW"]), I(m["ksplit"]), I(m["kchunk"])]
+    elif k == "gconv":
+        args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+        args += [I(m[f]) for f in ("M", "N", "K", "lda", "Cin", "H", "W", "OH", "OW", "ksplit",
+                                   "kchunk", "ximg", "cimg")]
+    elif k == "wino":
+        args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+        args += [I(m[f]) for f in ("N", "C", "H", "W", "OC", "OH", "OW", "TH", "TW", "CP", "OCP",
+                                   "PT", "PL", "nchunk")]
+    elif k == "conv_smallc":
+        args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+        args += [I(m[f]) for f in ("batch", "H", "W", "OC", "OH", "OW")]
+    elif k == "streamk_fixup":
+        args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+        args += [I(m[f]) for f in ("M", "N", "K", "full", "ldc", "hw")]
+    elif k == "splitk_reduce":
+        args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+        args += [I(m["S"]), I(m["M"]), I(m["N"]), I(m["ldc"]), I(m["hw"])]
+    elif k == "im2col":
+        args = [P(l.inputs[0]), P(l.outputs[0])]
+        args += [I(m[f]) for f in ("C", "H", "W", "KH", "KW", "OH", "OW", "SH", "SW",
+                                   "PH", "PW", "DH", "DW", "batch", "ldc")]
+    elif k == "dwconv":
+        args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+        args += [I(m[f]) for f in ("N", "C", "H", "W", "OC", "OH", "OW", "PT", "PL")]
+    elif k == "elementwise":
+        args = [P(e) for e in l.inputs] + [P(o) for o in l.outputs] + [I(m["N"])]
+    elif k in ("maxpool", "avgpool"):
+        args = [P(l.inputs[0]), P(l.outputs[0])]
+        args += [I(m[f]) for f in ("planes", "H", "W", "OH", "OW", "KH", "KW", "SH", "SW",
+                                   "PT", "PL", "DH", "DW")]
+    elif k == "gap":
+        args = [P(l.inputs[0]), P(l.outputs[0]), I(m["planes"]), I(m["HW"])]
+    elif k == "softmax":
+        args = [P(l.inputs[0]), P(l.outputs[0])]
+        args += ([Arg.i64(m["outer"]), I(m["L"])] if m["rows"] else
+                 [Arg.i64(m["outer"]), I(m["L"]), I(m["inner"])])
+    elif k == "transpose":
+        args = [P(l.inputs[0]), P(l.outputs[0]), Arg.i64(m["total"]), Arg.dims6(m["out_dims"]),
+                Arg.dims6(m["src_strides"])]
+    elif k == "pad":
+        args = [P(l.inputs[0]), P(l.outputs[0]), Arg.i64(m["total"]), Arg.dims6(m["out_dims"]),
+                Arg.dims6(m["in_dims"]), Arg.dims6(m["before"], fill=0), Arg.f32(m["value"])]
+    elif k == "concat":
+        args = [P(l.inputs[0]), P(l.outputs[0])] + [Arg.i64(m[f]) for f in
+                                                     ("rows", "run", "dst_stride", "dst_off")]
+    elif k == "copy":
+        args = [P(l.inputs[0]), P(l.outputs[0]), Arg.i64(m["nbytes"])]
+    elif k == "quantize":
+        args = [P(l.inputs[0]), P(l.outputs[0]), I(m["N"]), I(m["C"]), I(m["HW"]),
+                Arg.f32(m["inv_s"])]
+    elif k == "qgemm":
+        args = [P(e) for e in l.inputs[:4]] + [P(l.outputs[0])]
+        args += [P(l.inputs[4]) if len(l.inputs) > 4 else Arg.ptr(0)]
+        args += [I(m[f]) for f in ("M", "N", "K", "lda", "ldb", "ldc", "Cin", "H", "W", "OH", "OW")]
+        args += [Arg.f32(m.get("res_mult", 0.0)), Arg.f32(m.get("acc_mult", 0.0))]
+    elif k == "qconv_first":
+        args = [P(l.inputs[0]), Arg.f32(m["inv_s"])] + [P(e) for e in l.inputs[1:4]]
+        args += [P(l.inputs[4]) if len(l.inputs) > 4 else Arg.ptr(0), P(l.outputs[0])]
+        args += [I(m[f]) for f in ("N", "H", "W", "OH", "OW")]
+    elif k == "qmlp":
+        args = [P(e) for e in l.inputs]
+        if not m["mixer"]:                     # no token mixer: null Wd, bd, md
+            args[1:1] = [Arg.ptr(0)] * 3
+        args += [P(l.outputs[0]), I(m["M"]), I(m["H"]), I(m["W"]), Arg.f32(m["res_mult"]),
+                 Arg.f32(m["acc_mult"])]
+    elif k == "qdwconv":
+        args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+        args += [I(m[f]) for f in ("N", "C", "H", "W", "OH", "OW", "PT", "PL")]
+    elif k == "qadd":
+        args = [P(l.inputs[0]), P(l.inputs[1]), P(l.outputs[0]), Arg.i64(m["n"]),
+                Arg.f32(m["ma"]), Arg.f32(m["mb"])]
+    elif k == "qlut":
+        args = [P(l.inputs[0]), P(l.inputs[1]), P(l.outputs[0]), Arg.i64(m["n"])]
+    elif k == "qgap":
+        args = [P(l.inputs[0]), P(l.outputs[0]), I(m["N"]), I(m["C"]), I(m["HW"]),
+                Arg.f32(m["m"])]
+    elif k == "dequantize":
+        args = [P(l.inputs[0]), P(l.outputs[0]), Arg.i64(m["n"]), I(m["C"]), I(m["HW"]),
+                Arg.f32(m["s"])]
+    else:
+        raise HipError(f"launch kind {k!r} has no device implementation")
+    return args

@@ -292,13 +292,17 @@ class HipContext:
 # ----- packed launch plans ------------------------------------------------------
 
 class Arg:
-    """A kernel argument for a packed plan: a raw value of a fixed width."""
+    """A kernel argument for a packed plan: a raw value of a fixed width and
+    its kind, which ``abi.check_launch`` matches against the kernel's
+    declared parameter: ``p`` pointer, ``i`` 32-bit int, ``q`` 64-bit int,
+    ``f`` float, ``d`` an ``mdlc::Dims6`` record."""
 
-    __slots__ = ("data", "workspace")
+    __slots__ = ("data", "workspace", "kind")
 
-    def __init__(self, data: bytes, workspace: bool = False) -> None:
+    def __init__(self, data: bytes, workspace: bool = False, kind: str = "p") -> None:
         self.data = data
         self.workspace = workspace
+        self.kind = kind
 
     @staticmethod
     def ws(offset: int) -> "Arg":
@@ -311,15 +315,15 @@ class Arg:
 
     @staticmethod
     def i32(v: int) -> "Arg":
-        return Arg(struct.pack("<i", int(v)))
+        return Arg(struct.pack("<i", int(v)), kind="i")
 
     @staticmethod
     def i64(v: int) -> "Arg":
-        return Arg(struct.pack("<q", int(v)))
+        return Arg(struct.pack("<q", int(v)), kind="q")
 
     @staticmethod
     def f32(v: float) -> "Arg":
-        return Arg(struct.pack("<f", float(v)))
+        return Arg(struct.pack("<f", float(v)), kind="f")
 
     @staticmethod
     def dims6(vals, fill: int = 1) -> "Arg":
@@ -328,7 +332,7 @@ class Arg:
         vals = [int(v) for v in vals]
         if len(vals) > 6:
             raise HipError(f"more than six dimensions: {vals}")
-        return Arg(struct.pack("<6i", *([fill] * (6 - len(vals)) + vals)))
+        return Arg(struct.pack("<6i", *([fill] * (6 - len(vals)) + vals)), kind="d")
 
 
 def pack_plan(launches: list, workspace: Optional[tuple] = None) -> bytes:

@@ -82,7 +82,9 @@ __device__ __forceinline__ void gemm_f32_wsplit(const float* __restrict__ A,
   const int b_bytes = CONV ? (N / (OH * OW)) * Cin * H * W * 4 : (BKN ? N * ldb * 4 : K * ldb * 4);
   const int HW = H * W;
   // CONV: per column block the lane's image offset and window corner; a
-  // column past N gets a corner no tap reaches
+  // column past N gets image 0 and a corner row one above the highest any
+  // tap reaches (ih <= -DH - 1 for every kh), so every tap fails the bounds
+  // check and the address arithmetic stays small
   int cimg[CONV ? NI : 1], cih[CONV ? NI : 1], ciw[CONV ? NI : 1];
   if (CONV) {
 #pragma unroll
@@ -92,8 +94,8 @@ __device__ __forceinline__ void gemm_f32_wsplit(const float* __restrict__ A,
       const int img = p / ohw;
       const int pix = p - img * ohw;
       const int oh = pix / OW;
-      cimg[ni] = (img * Cin + 4 * lg) * HW;
-      cih[ni] = p < N ? oh * Win::SH - Win::PT : -(1 << 28);
+      cimg[ni] = p < N ? (img * Cin + 4 * lg) * HW : 0;
+      cih[ni] = p < N ? oh * Win::SH - Win::PT : -(Win::KH * Win::DH) - 1;
       ciw[ni] = (pix - oh * OW) * Win::SW - Win::PL;
     }
   }

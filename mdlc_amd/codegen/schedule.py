@@ -22,7 +22,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from dataclasses import asdict, dataclass
+from dataclasses import asdict, dataclass, replace
 from typing import Iterator, Optional
 
 LDS_LIMIT = 160 * 1024         # bytes one workgroup may allocate (gfx950: 160 KB per CU)
@@ -198,6 +198,17 @@ def split_slices(K: int, sched: MfmaSchedule) -> tuple:
     chunk = -(-K // sched.SK)
     chunk = -(-chunk // sched.BK) * sched.BK
     return -(-K // chunk), chunk
+
+
+def unsplit_if_one_slice(sched: MfmaSchedule, K: int) -> MfmaSchedule:
+    """``sched`` with SK = 1 when its split leaves one slice of K. The
+    kernels pick their split-K form (raw partial sums into the workspace, no
+    bias or residual parameters) from the schedule, and the lowering picks
+    the launch form from the slice count: they must agree, or the launch's
+    arguments no longer match the kernel's parameters."""
+    if sched.SK > 1 and split_slices(K, sched)[0] == 1:
+        return replace(sched, SK=1)
+    return sched
 
 
 DEFAULT_GEMM = MfmaSchedule()
