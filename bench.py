@@ -39,7 +39,6 @@ TRAFFIC_JSON = os.path.join(ROOT, "profiles", "resnet18_b32_traffic.json")
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_INT8_MFMA_TOPS = 5000.0
 PEAK_HBM_GBS = 8000.0
-CALIBRATION = "each Conv/Gemm LSUV-rescaled to unit output std as the reference exporters do"
 FINISHERS = ("splitk_reduce", "streamk_fixup")
 
 
@@ -87,38 +86,87 @@ def _threads_used(info: dict) -> int:
     return max([1] + [p["threads"] or 1 for p in info["blas_pools"]])
 
 
-def cpu_baseline_network(name: str, seconds: float = 8.0) -> dict:
+def cpu_network(name: str, batch: int, *, seconds: float = 0.0, sample: int = 0) -> dict:
     """The NumPy oracle (a restatement of the reference executor) on the
-    host: single images repeated for ``seconds``, then one forward of the
-    benchmark's batch of 32."""
+    host for one network workload: at batch 1, single-image forwards
+    repeated for ``seconds``; at a larger batch, one forward over ``sample``
+    of the batch's images (the whole batch when ``sample`` equals it)."""
     from mdlc_amd.compiler import compile_graph
     from oracle.reference import ReferenceExecutor
 
     build, make_input = builders(name)
     info = host_info()
-    x1 = make_input(1, seed=7)
-    ex1 = ReferenceExecutor(compile_graph(build(batch=1), feeds={"input": x1}).graph)
-    ex1.run({"input": x1})
-    n, t0 = 0, time.perf_counter()
-    while True:
-        ex1.run({"input": x1})
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and n >= 2:
-            break
-    b1 = n / el
-    x32 = make_input(32)
-    ex32 = ReferenceExecutor(compile_graph(build(batch=32), feeds={"input": x32}).graph)
-    t0 = time.perf_counter()
-    ex32.run({"input": x32})
-    t32 = time.perf_counter() - t0
     threads = _threads_used(info)
-    return {"value": 32 / t32, "unit": "images/s", "cores": threads, "kind": "port",
-            "sample": f"one batch-32 {name} forward ({t32:.1f} s) and {n} single-image forwards "
-                      f"({el:.1f} s, {b1:.2f} images/s) through the NumPy oracle (the reference "
-                      f"executor's algorithm: einsum convolutions, single-threaded; BLAS matrix "
-                      f"products on up to {threads} threads), host of the GPU box",
-            "batch1_images_per_s": b1, "host": info}
+    how = ("einsum convolutions, single-threaded; BLAS matrix products on up to "
+           f"{threads} threads" if name != "repvit_int8" else
+           "exact int64 NumPy products with the requantization, single-threaded")
+    if batch == 1:
+        x = make_input(1, seed=7)
+        ex = ReferenceExecutor(compile_graph(build(batch=1), feeds={"input": x}).graph)
+        ex.run({"input": x})
+        n, t0 = 0, time.perf_counter()
+        while True:
+            ex.run({"input": x})
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds and n >= 2:
+                break
+        value, what = n / el, f"{n} single-image forwards ({el:.1f} s)"
+    else:
+        k = min(sample or batch, batch)
+        x = make_input(batch)[:k]
+        ex = ReferenceExecutor(compile_graph(build(batch=k), feeds={"input": x}).graph)
+        t0 = time.perf_counter()
+        ex.run({"input": x})
+        el = time.perf_counter() - t0
+        value = k / el
+        what = (f"one batch-{batch} forward ({el:.1f} s)" if k == batch else
+                f"one forward over {k} of the batch's {batch} images ({el:.1f} s; per-image "
+                f"work is independent of the batch)")
+    log(f"cpu {name} b={batch}: {value:.2f} images/s")
+    return {"value": value, "unit": "images/s", "cores": threads, "kind": "port",
+            "sample": f"{what} of {name} through the NumPy oracle (the reference executor's "
+                      f"algorithm: {how}), host of the GPU box",
+            "host": info}
+
+
+def cpu_micro(compiled) -> dict:
+    """Each micro GEMM through the oracle (A @ B + bias, relu; BLAS) for
+    at least a second."""
+    from oracle.reference import run_reference
+
+    rates = {}
+    for (M, N, K), c, feeds in compiled:
+        run_reference(c.graph, feeds)
+        t0, n = time.perf_counter(), 0
+        while time.perf_counter() - t0 < 1.0 or n < 2:
+            run_reference(c.graph, feeds)
+            n += 1
+        rates[f"{M}x{N}x{K}"] = 2.0 * M * N * K * n / (time.perf_counter() - t0) / 1e9
+    info = host_info()
+    log("cpu micro GEMMs: " + ", ".join(f"{k} {v:.1f} GFLOP/s" for k, v in rates.items()))
+    return {"value": sum(rates.values()) / len(rates), "unit": "GFLOP/s (mean over shapes)",
+            "cores": _threads_used(info), "kind": "port", "host": info,
+            "sample": "each shape through the NumPy oracle (A @ B + bias, relu; BLAS) for >= 1 s: "
+                      + ", ".join(f"{k}: {v:.1f}" for k, v in rates.items())}
+
+
+def cpu_int8(feeds, w, size: int) -> dict:
+    """32 rows of the int8 GEMM through the oracle's exact int64 product and
+    requantization."""
+    import numpy as np
+
+    from oracle.quant import gemm_acc, requant
+
+    rows = 32
+    t0 = time.perf_counter()
+    requant(gemm_acc(feeds["xq"][:rows], w, None), np.ones(size, np.float32) * 1e-5)
+    el = time.perf_counter() - t0
+    log(f"cpu int8 GEMM: {2.0 * rows * size * size / el / 1e9:.1f} GOP/s")
+    return {"value": 2.0 * rows * size * size / el / 1e12, "unit": "TOP/s", "cores": 1, "kind": "port",
+            "host": host_info(),
+            "sample": f"{rows} of the {size} rows through the oracle's exact int64 matmul + requant "
+                      f"({el:.2f} s; NumPy integer matmul, one thread)"}
 
 
 # ----- device timing ------------------------------------------------------------------
@@ -274,6 +322,7 @@ def compile_network(args, name: str, batch: int):
 
 def network(args, name: str, batch: int, *, steps: int, headline: bool) -> dict:
     c, feeds = compile_network(args, name, batch)
+    cold = cold_compile_seconds(c) if headline else None
     ms, host_s, prof, arena = time_module(c, feeds, steps, args.warmup, args.profile_iters,
                                           args.graph, host_loop=headline)
     value = batch * 1000.0 / ms
@@ -281,40 +330,46 @@ def network(args, name: str, batch: int, *, steps: int, headline: bool) -> dict:
     traffic = TRAFFIC_JSON if (name == "resnet18" and batch == 32 and not args.no_fold) else ""
     roof, _ = roofline(prof, traffic_json=traffic, verbose=headline)
     int8 = name == "repvit_int8"
-    work = sum(l.meta.get("ops" if int8 else "flops", 0) for l in c.module.plan)
+    key = "ops" if int8 else "flops"
+    # executed: the multiply-adds the kernels perform (a Winograd conv performs
+    # fewer than the convolution it computes); algorithmic: 2*M*N*K of every
+    # conv/GEMM as the reference's im2col formulation counts it
+    executed = sum(l.meta.get(key, 0) for l in c.module.plan)
+    algorithmic = sum(l.meta.get("direct_flops", l.meta.get(key, 0)) for l in c.module.plan)
     metric = METRIC if (name == "resnet18" and batch == 32) else \
         f"{name} b={batch} {'int8' if int8 else 'fp32'} images/sec"
+    g, r = ("gop", "tops") if int8 else ("gflop", "tflops")
     line = {"metric": metric, "value": value, "unit": "images/s", "ms_per_step": ms,
-            "steps": steps, "dtype": "i8" if int8 else "f32",
-            "workload": f"{name}_{'int8' if int8 else 'fp32'}_b{batch}",
-            "launches": len(c.module.plan), "gop_per_step": work / 1e9,
-            ("network_tops" if int8 else "network_tflops"): work / (ms * 1e-3) / 1e12,
+            "steps": steps, "dtype": "i8" if int8 else "f32", "workload": workload_key(name, batch),
+            "launches": len(c.module.plan),
+            f"algorithmic_{g}_per_step": algorithmic / 1e9,
+            f"network_{r}": algorithmic / (ms * 1e-3) / 1e12,
+            f"executed_{g}_per_step": executed / 1e9,
+            f"executed_{r}": executed / (ms * 1e-3) / 1e12,
             "roofline": roof}
     if host_s:
         line["host_buffer_images_per_s"] = batch / host_s
+    if cold is not None:
+        line["cold_compile_s"] = cold
+        log(f"{name} b={batch}: cold hipRTC compile {cold:.1f} s")
     return line
 
 
-def micro_gemm(args, *, steps: int, cpu: bool) -> dict:
+def micro_compiled(args) -> list:
     from mdlc_amd.compiler import compile_graph
     from mdlc_amd.tools.micro_gemm import SHAPES, build_micro_gemm
 
-    shapes, total_flops, total_ms, cpu_rates = {}, 0.0, 0.0, {}
-    compiled = []
+    out = []
     for M, N, K in SHAPES:
         g, feeds = build_micro_gemm(M, N, K)
-        compiled.append(((M, N, K), compile_graph(g, feeds=feeds, schedule_fn=schedule_source(args)),
-                         feeds))
-    if cpu:                                   # host leg first, before any device call
-        from oracle.reference import run_reference
+        out.append(((M, N, K), compile_graph(g, feeds=feeds, schedule_fn=schedule_source(args)), feeds))
+    return out
 
-        for (M, N, K), c, feeds in compiled:
-            run_reference(c.graph, feeds)
-            t0, n = time.perf_counter(), 0
-            while time.perf_counter() - t0 < 1.0 or n < 2:
-                run_reference(c.graph, feeds)
-                n += 1
-            cpu_rates[f"{M}x{N}x{K}"] = 2.0 * M * N * K * n / (time.perf_counter() - t0) / 1e9
+
+def micro_gemm(args, *, steps: int, cpu: bool) -> dict:
+    shapes, total_flops, total_ms = {}, 0.0, 0.0
+    compiled = micro_compiled(args)
+    cpu_line = cpu_micro(compiled) if cpu else None      # host leg first, before any device call
     for (M, N, K), c, feeds in compiled:
         ms, _, prof, _ = time_module(c, feeds, steps, args.warmup, args.profile_iters,
                                      host_loop=False)
@@ -334,47 +389,36 @@ def micro_gemm(args, *, steps: int, cpu: bool) -> dict:
             "value": total_flops / (total_ms * 1e-3) / 1e12, "unit": "TFLOP/s",
             "ms_per_step": total_ms, "steps": steps, "dtype": "f32",
             "workload": "micro_gemm_bias_relu", "shapes": shapes}
-    if cpu_rates:
-        info = host_info()
-        line["cpu_baseline"] = {
-            "value": sum(cpu_rates.values()) / len(cpu_rates), "unit": "GFLOP/s (mean over shapes)",
-            "cores": _threads_used(info), "kind": "port", "host": info,
-            "sample": "each shape through the NumPy oracle (A @ B + bias, relu; BLAS) for >= 1 s: "
-                      + ", ".join(f"{k}: {v:.1f}" for k, v in cpu_rates.items())}
+    if cpu_line:
+        line["cpu_baseline"] = cpu_line
     return line
 
 
-def int8_gemm(args, *, steps: int, cpu: bool) -> dict:
+def int8_problem(size: int):
+    """(feeds, weights, graph) of the requantized int8 GEMM at M = N = K = size."""
     import numpy as np
 
-    from mdlc_amd.compiler import compile_graph
     from mdlc_amd.tools.graph_builder import GraphBuilder
 
-    M = N = K = args.size
     rng = np.random.default_rng(0)
     b = GraphBuilder("i8gemm")
-    b.input("xq", (M, K), dtype="int8")
-    w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    b.input("xq", (size, size), dtype="int8")
+    w = rng.integers(-127, 128, (size, size)).astype(np.int8)
     b.const("w", w)
-    b.const("b", rng.integers(-1000, 1000, N).astype(np.int32))
-    b.const("m", rng.uniform(2e-6, 1e-5, N).astype(np.float32))
+    b.const("b", rng.integers(-1000, 1000, size).astype(np.int32))
+    b.const("m", rng.uniform(2e-6, 1e-5, size).astype(np.float32))
     b.node("QGemm", ["xq", "w", "b", "m"], "y", transB=1)
     b.output("y")
-    feeds = {"xq": rng.integers(-127, 128, (M, K)).astype(np.int8)}
-    c = compile_graph(b.graph(), feeds=feeds, schedule_fn=schedule_source(args))
-    cpu_line = None
-    if cpu:                                   # host leg first: 32 rows through the oracle
-        from oracle.quant import gemm_acc, requant
+    return {"xq": rng.integers(-127, 128, (size, size)).astype(np.int8)}, w, b.graph()
 
-        rows = 32
-        t0 = time.perf_counter()
-        requant(gemm_acc(feeds["xq"][:rows], w, None), np.ones(N, np.float32) * 1e-5)
-        el = time.perf_counter() - t0
-        info = host_info()
-        cpu_line = {"value": 2.0 * rows * N * K / el / 1e12, "unit": "TOP/s", "cores": 1,
-                    "kind": "port", "host": info,
-                    "sample": f"{rows} of the {M} rows through the oracle's exact int64 "
-                              f"matmul + requant ({el:.2f} s; NumPy integer matmul, one thread)"}
+
+def int8_gemm(args, *, steps: int, cpu: bool) -> dict:
+    from mdlc_amd.compiler import compile_graph
+
+    M = N = K = args.size
+    feeds, w, g = int8_problem(M)
+    c = compile_graph(g, feeds=feeds, schedule_fn=schedule_source(args))
+    cpu_line = cpu_int8(feeds, w, M) if cpu else None   # host leg first
     ms, _, prof, _ = time_module(c, feeds, steps, args.warmup, args.profile_iters, host_loop=False)
     tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     roof, _ = roofline(prof, verbose=False)
@@ -390,8 +434,8 @@ def int8_gemm(args, *, steps: int, cpu: bool) -> dict:
 def full_line(args, part: dict, *, scaling: str, data: str, config: dict) -> dict:
     """The driver's JSON contract around one measured part."""
     keep = {k: v for k, v in part.items()
-            if k in ("launches", "gop_per_step", "network_tflops", "network_tops",
-                     "host_buffer_images_per_s", "shapes", "M", "N", "K")}
+            if k in ("launches", "host_buffer_images_per_s", "cold_compile_s", "shapes", "M", "N", "K")
+            or k.startswith(("algorithmic_", "executed_", "network_"))}
     out = {"metric": part["metric"], "value": part["value"], "unit": part["unit"], "n_gpus": 1,
            "steps": part["steps"], "warmup": args.warmup, "ms_per_step": part["ms_per_step"],
            "higher_is_better": True, "scaling": scaling, "vs_baseline": None,
@@ -411,23 +455,67 @@ def data_text(name: str) -> str:
     if name in ("micro_gemm", "int8_gemm"):
         return ("synthetic A, B, bias ~ N(0,1)/sqrt(K), fixed seed per shape" if name == "micro_gemm"
                 else "synthetic int8 codes")
-    return ("synthetic N(0,1) images, random-init weights (Kaiming-normal conv/FC, BN gamma "
-            "U(0.5,1.5) beta N(0,0.1) mean N(0,0.1) var U(0.5,1.5); " + CALIBRATION + ")")
+    init = ("synthetic N(0,1) images, random-init weights (Kaiming-normal conv/FC, BN gamma "
+            "U(0.5,1.5) beta N(0,0.1) mean N(0,0.1) var U(0.5,1.5)")
+    if name == "resnet18":
+        return init + ", used as drawn like the reference's ResNet-18 exporter)"
+    return init + "; each Conv/Gemm LSUV-rescaled to unit output std, as the reference's " \
+        "MobileNetV2 exporter does)"
 
 
-def secondary(args) -> dict:
-    """The other benchmark configs, each with its own roofline block."""
+SECONDARY = (("resnet18", 1, 50), ("mobilenetv2", 1, 50), ("mobilenetv2", 32, 20),
+             ("repvit_int8", 32, 20))
+
+
+def workload_key(name: str, batch: int) -> str:
+    return f"{name}_{'int8' if name == 'repvit_int8' else 'fp32'}_b{batch}"
+
+
+def cpu_legs(args, headline: str, batch: int, with_secondary: bool) -> dict:
+    """Every CPU baseline of the run, timed before the first device call:
+    the headline workload's, then each secondary config's on a bounded
+    sample (about 45 s in all)."""
+    out = {workload_key(headline, batch): cpu_network(headline, batch, seconds=6.0, sample=batch)}
+    if with_secondary:
+        for name, b, _ in SECONDARY:
+            key = workload_key(name, b)
+            if key not in out:
+                out[key] = (cpu_network(name, 1, seconds=4.0) if b == 1 else
+                            cpu_network(name, b, sample=8 if name == "mobilenetv2" else 4))
+        out["micro_gemm_bias_relu"] = cpu_micro(micro_compiled(args))
+        feeds, w, _ = int8_problem(4096)
+        out["int8_gemm_4096"] = cpu_int8(feeds, w, 4096)
+    return out
+
+
+def secondary(args, cpu: dict) -> dict:
+    """The other benchmark configs, each with its own roofline block and the
+    CPU baseline measured for it before the first device call."""
     out = {}
-    for name, batch, steps in (("resnet18", 1, 50), ("mobilenetv2", 1, 50), ("mobilenetv2", 32, 20),
-                               ("repvit_int8", 32, 20)):
+    for name, batch, steps in SECONDARY:
         part = network(args, name, batch, steps=steps, headline=False)
+        if part["workload"] in cpu:
+            part["cpu_baseline"] = cpu[part["workload"]]
         out[part["workload"]] = {k: v for k, v in part.items() if k not in ("workload", "dtype")}
     out["micro_gemm_bias_relu"] = micro_gemm(args, steps=200, cpu=False)
+    if "micro_gemm_bias_relu" in cpu:
+        out["micro_gemm_bias_relu"]["cpu_baseline"] = cpu["micro_gemm_bias_relu"]
     size = args.size
     args.size = 4096
     out["int8_gemm_4096"] = int8_gemm(args, steps=20, cpu=False)
+    if "int8_gemm_4096" in cpu:
+        out["int8_gemm_4096"]["cpu_baseline"] = cpu["int8_gemm_4096"]
     args.size = size
     return out
+
+
+def cold_compile_seconds(c) -> float:
+    """hipRTC compile time of the module with no code-object cache."""
+    from mdlc_amd.codegen.hip.hiprtc_runtime import compile_code_object
+
+    t0 = time.perf_counter()
+    compile_code_object(c.module.sources(), use_cache=False)
+    return time.perf_counter() - t0
 
 
 def main(argv=None) -> int:
@@ -451,7 +539,8 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="measure only the selected workload")
-    ap.add_argument("--profile-iters", type=int, default=3)
+    ap.add_argument("--profile-iters", type=int, default=25,
+                    help="runs of the plan whose per-launch median the roofline uses")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -467,16 +556,17 @@ def main(argv=None) -> int:
         part = int8_gemm(args, steps=args.steps, cpu=cpu)
         line = full_line(args, part, scaling="strong", data=data_text(w), config={})
     else:
-        base = cpu_baseline_network(w) if cpu else None      # host leg before any device call
+        with_sec = w == "resnet18" and args.batch == 32 and not args.no_secondary
+        cpu_lines = cpu_legs(args, w, args.batch, with_sec) if cpu else {}
         part = network(args, w, args.batch, steps=args.steps, headline=True)
-        if base:
-            part["cpu_baseline"] = base
+        if part["workload"] in cpu_lines:
+            part["cpu_baseline"] = cpu_lines[part["workload"]]
         line = full_line(args, part, scaling="weak", data=data_text(w),
                          config={"batch": args.batch, "image": [3, 224, 224],
                                  "conv_mode": args.conv_mode, "winograd": args.winograd,
                                  "backend_folds": not args.no_fold})
-        if w == "resnet18" and args.batch == 32 and not args.no_secondary:
-            line["config"]["secondary"] = secondary(args)
+        if with_sec:
+            line["config"]["secondary"] = secondary(args, cpu_lines)
     print(json.dumps(line), flush=True)
     return 0
 

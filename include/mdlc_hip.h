@@ -96,8 +96,10 @@ int mdlc_event_elapsed_ms(void* start, void* stop, float* ms);
  *
  * mdlc_plan_run enqueues every launch `iters` times without waiting.
  * mdlc_plan_time_ms brackets `iters` runs (after `warmup` runs) with events.
- * mdlc_plan_profile times each launch separately with its own event pair,
- * averaged over `iters` runs, into per_launch_ms[0..n_launches).
+ * mdlc_plan_profile times each launch's kernel execution with a start and
+ * stop event attached to its own dispatch (hipExtModuleLaunchKernel), over
+ * `iters` runs of the plan, and writes each launch's median into
+ * per_launch_ms[0..n_launches).
  * mdlc_plan_use_graph(plan, 1) captures the plan once into a hipGraph and
  * replays that graph from then on (0 returns to direct launches). */
 int mdlc_plan_create(const void* packed, size_t nbytes, void** plan);

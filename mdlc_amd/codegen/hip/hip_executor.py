@@ -267,8 +267,10 @@ class HipExecutor:
                     got[o] = self.read(o)
         return got
 
-    def profile(self, iters: int = 3) -> list:
-        """[(launch, ms)] — each launch timed with its own event pair."""
+    def profile(self, iters: int = 25) -> list:
+        """[(launch, ms)]: each launch's kernel time from start and stop
+        events attached to its own dispatch, the median over ``iters`` runs
+        of the plan."""
         return list(zip(self.module.plan, self.plan.profile(iters)))
 
     def close(self) -> None:

@@ -37,6 +37,28 @@ class Compiled:
     passes: PassManager
     feeds: dict
     checks: list = field(default_factory=list)
+    golden: Optional[dict] = None          # outputs of the original graph on ``feeds``
+    evaluate: Optional[Callable] = None     # the host evaluator they came from
+
+    def verify(self, evaluate: Optional[Callable] = None, *, rtol: Optional[float] = None,
+               atol: Optional[float] = None) -> list:
+        """The optimized graph's outputs on ``feeds`` against the original
+        graph's (mdlc/compiler.py:43-46), both computed by ``evaluate(graph,
+        feeds)`` — the evaluator given to ``compile_onnx(verify_passes=...)``
+        unless another is passed here. Returns one ``CheckResult`` per
+        output and keeps them in ``checks`` for the report."""
+        from mdlc_amd.testing import FP32_NETWORK, graph_checks
+
+        evaluate = evaluate or self.evaluate
+        if evaluate is None:
+            raise ValueError("Compiled.verify needs a host evaluator of IR graphs, "
+                             "evaluate(graph, feeds) -> outputs (this package has no CPU executor)")
+        golden = self.golden if self.golden is not None and evaluate is self.evaluate \
+            else evaluate(self.original, self.feeds)
+        self.checks = graph_checks(evaluate, self.graph, self.feeds, golden,
+                                   rtol=FP32_NETWORK.rtol if rtol is None else rtol,
+                                   atol=FP32_NETWORK.atol if atol is None else atol)
+        return self.checks
 
     def report(self) -> str:
         n_fused = sum(1 for n in self.graph.nodes if n.is_fused)
@@ -99,16 +121,23 @@ def compile_graph(graph: Graph, *, batch: int = 1, feeds: Optional[dict] = None,
     return Compiled(original, graph, module, mem_plan, pm, feeds)
 
 
-def compile_onnx(source, *, verify_passes: bool = True, **kw) -> Compiled:
+def compile_onnx(source, *, verify_passes=False, **kw) -> Compiled:
     """Compile an ONNX model (mdlc/compiler.py:64-95): a path to an ``.onnx``
     file, its bytes, a decoded ``ModelProto`` of ``mdlc_amd.frontend``, or an
     IR ``Graph``. The model is imported by this package's own protobuf reader
     (the ``onnx`` package is not needed) and then compiled by
     ``compile_graph``, which takes the remaining keywords (``batch``,
     ``feeds``, ``schedule_fn``, backend options). Structural verification runs
-    after every pass; ``verify_passes`` is accepted for the reference's
-    signature (its numerical check against onnxruntime needs the test oracle
-    here, which the product does not import)."""
+    after every pass.
+
+    ``verify_passes`` adds the reference's numerical check: given a host
+    evaluator of IR graphs, ``evaluate(graph, feeds) -> {output: array}``
+    (for instance the NumPy oracle's ``run_reference``), the original graph's
+    outputs on the feeds become the golden values, every pass that changes
+    the graph is re-evaluated against them at the network tolerance
+    (raising ``AssertionError`` naming the pass), and ``Compiled.verify()``
+    checks the optimized graph. This package ships no CPU executor, so
+    ``True`` raises instead of checking nothing."""
     from mdlc_amd.frontend import import_onnx, import_onnx_model
     from mdlc_amd.frontend.onnx_proto import ModelProto
 
@@ -121,4 +150,19 @@ def compile_onnx(source, *, verify_passes: bool = True, **kw) -> Compiled:
     else:
         raise TypeError(f"compile_onnx takes a path, model bytes, a ModelProto or a Graph, "
                         f"not {type(source).__name__}")
-    return compile_graph(graph, **kw)
+    if verify_passes is True:
+        raise TypeError("verify_passes=True needs the host evaluator that computes the golden "
+                        "outputs: pass verify_passes=evaluate, a function (graph, feeds) -> "
+                        "{output: array} such as the NumPy oracle's run_reference")
+    if not verify_passes:
+        return compile_graph(graph, **kw)
+    from mdlc_amd.testing import pass_checker
+
+    evaluate = verify_passes
+    feeds = kw.pop("feeds", None)
+    if feeds is None:
+        feeds = make_dummy_feeds(graph, batch=kw.get("batch", 1))
+    golden = evaluate(graph.clone(), feeds)
+    c = compile_graph(graph, feeds=feeds, verify=pass_checker(evaluate, feeds, golden), **kw)
+    c.golden, c.evaluate = golden, evaluate
+    return c

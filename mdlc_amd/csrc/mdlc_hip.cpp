@@ -2,8 +2,10 @@
 // The C ABI is declared (with the reference interface each entry replaces)
 // in include/mdlc_hip.h.
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <hip/hiprtc.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -450,22 +452,37 @@ int mdlc_plan_profile(void* plan, int iters, float* per_launch_ms) {
   if (!per_launch_ms || iters <= 0) return fail(kBadArg, "mdlc_plan_profile", "bad arguments");
   if ((rc = need_workspace(p, "mdlc_plan_profile"))) return rc;
   size_t n = p->launches.size();
-  std::vector<hipEvent_t> ev(2 * n, nullptr);
+  // the events ride on each kernel's own dispatch (hipExtModuleLaunchKernel),
+  // so they time the kernel's execution, not the queue's work around it;
+  // the `iters` runs of the plan are enqueued back to back (one wait at the
+  // end: a wait per run would start each run's first kernel on an idle
+  // device), and a launch's figure is the median of its `iters` times
+  const size_t runs = static_cast<size_t>(iters);
+  std::vector<hipEvent_t> ev(2 * n * runs, nullptr);
   for (auto& e : ev)
     if ((rc = check(hipEventCreate(&e), "hipEventCreate"))) break;
-  for (size_t i = 0; i < n; ++i) per_launch_ms[i] = 0.f;
-  for (int it = 0; it < iters && !rc; ++it) {
+  std::vector<float> samples(n * runs, 0.f);
+  for (size_t it = 0; it < runs && !rc; ++it) {
     for (size_t i = 0; i < n && !rc; ++i) {
-      rc = check(hipEventRecord(ev[2 * i], g_stream), "hipEventRecord");
-      if (!rc) rc = enqueue(p->launches[i]);
-      if (!rc) rc = check(hipEventRecord(ev[2 * i + 1], g_stream), "hipEventRecord");
+      Launch& l = p->launches[i];
+      hipEvent_t* e = &ev[2 * (it * n + i)];
+      rc = check(hipExtModuleLaunchKernel(l.fn, l.grid[0] * l.block[0], l.grid[1] * l.block[1],
+                                          l.grid[2] * l.block[2], l.block[0], l.block[1],
+                                          l.block[2], l.lds, g_stream, l.argv.data(), nullptr,
+                                          e[0], e[1], 0),
+                 "hipExtModuleLaunchKernel");
     }
-    if (!rc) rc = check(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
-    for (size_t i = 0; i < n && !rc; ++i) {
-      float t = 0.f;
-      rc = check(hipEventElapsedTime(&t, ev[2 * i], ev[2 * i + 1]), "hipEventElapsedTime");
-      per_launch_ms[i] += t / static_cast<float>(iters);
-    }
+  }
+  if (!rc) rc = check(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
+  for (size_t it = 0; it < runs && !rc; ++it)
+    for (size_t i = 0; i < n && !rc; ++i)
+      rc = check(hipEventElapsedTime(&samples[i * runs + it], ev[2 * (it * n + i)],
+                                     ev[2 * (it * n + i) + 1]),
+                 "hipEventElapsedTime");
+  for (size_t i = 0; i < n && !rc; ++i) {
+    float* s = &samples[i * iters];
+    std::sort(s, s + iters);
+    per_launch_ms[i] = iters % 2 ? s[iters / 2] : 0.5f * (s[iters / 2 - 1] + s[iters / 2]);
   }
   for (auto& e : ev)
     if (e) hipEventDestroy(e);

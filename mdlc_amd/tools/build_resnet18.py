@@ -11,10 +11,14 @@ reference's 141 ops and constant folding has the same work to do.
 
 Weights: conv and FC Kaiming-normal (fan-in), FC bias U(-1/sqrt(512),
 1/sqrt(512)), BatchNorm gamma U(0.5,1.5), beta N(0,0.1), running_mean
-N(0,0.1), running_var U(0.5,1.5); all from one seeded generator. Then, as the
-reference's exporters do for their random-init models (mdlc/tools/
-export_utils.py:16-50), each Conv/Gemm is rescaled so its output has unit
-std on a fixed calibration input (``calibrate=False`` skips this).
+N(0,0.1), running_var U(0.5,1.5); all from one seeded generator, and used
+as drawn, like the reference's ResNet-18 exporter (mdlc/tools/
+build_resnet18.py:14-30 applies no calibration). With these BatchNorm
+statistics the residual stream grows to |x| of a few hundred by stage 4.
+``calibrate=True`` instead rescales each Conv/Gemm to unit output std on a
+fixed calibration input (the LSUV step mdlc/tools/export_utils.py:16-50
+applies to the reference's MobileNetV2 and RepViT exports), which gives a
+well-conditioned variant of the same network.
 """
 
 from __future__ import annotations
@@ -28,7 +32,7 @@ STAGES = [(64, 1), (128, 2), (256, 2), (512, 2)]
 
 
 def build_resnet18(*, batch: int = 1, seed: int = 0, num_classes: int = 1000,
-                   identities: bool = True, calibrate: bool = True) -> Graph:
+                   identities: bool = True, calibrate: bool = False) -> Graph:
     b = GraphBuilder("resnet18", seed)
     rng = b.rng
     b.input("input", (batch, 3, 224, 224))

@@ -36,6 +36,21 @@ def kernel_stats(path: str) -> list:
     return rows
 
 
+def kernel_medians(path: str) -> dict:
+    """Median dispatch duration per kernel name."""
+    con = sqlite3.connect(path)
+    by: dict = {}
+    for name, d in con.execute("select name, duration from kernels"):
+        by.setdefault(name, []).append(d)
+    con.close()
+    out = {}
+    for name, v in by.items():
+        v.sort()
+        k = len(v)
+        out[name] = v[k // 2] if k % 2 else 0.5 * (v[k // 2 - 1] + v[k // 2])
+    return out
+
+
 def counter_stats(path: str, counter: str) -> list:
     con = sqlite3.connect(path)
     rows = con.execute(
@@ -134,12 +149,13 @@ def main(argv=None) -> int:
             print(f"{name[:64]:64s} {n:10d} {avg:18.1f}")
         return 0
     rows = kernel_stats(args.db)
+    med = kernel_medians(args.db)
     total = sum(r[2] for r in rows) or 1
-    print(f"{'kernel':64s} {'calls':>6s} {'total_us':>10s} {'avg_us':>9s} {'min_us':>9s} "
-          f"{'max_us':>9s} {'pct':>6s}")
+    print(f"{'kernel':64s} {'calls':>6s} {'total_us':>10s} {'avg_us':>9s} {'med_us':>9s} "
+          f"{'min_us':>9s} {'max_us':>9s} {'pct':>6s}")
     for name, n, tot, avg, mn, mx in rows:
-        print(f"{name[:64]:64s} {n:6d} {tot / 1e3:10.1f} {avg / 1e3:9.2f} {mn / 1e3:9.2f} "
-              f"{mx / 1e3:9.2f} {100.0 * tot / total:6.2f}")
+        print(f"{name[:64]:64s} {n:6d} {tot / 1e3:10.1f} {avg / 1e3:9.2f} {med[name] / 1e3:9.2f} "
+              f"{mn / 1e3:9.2f} {mx / 1e3:9.2f} {100.0 * tot / total:6.2f}")
     return 0
 
 

@@ -240,3 +240,24 @@ class ReferenceExecutor:
 
 def run_reference(graph, feeds, **kw):
     return ReferenceExecutor(graph).run(feeds, **kw)
+
+
+def run_groups_float64(graph, env32):
+    """Every node of ``graph`` re-run in float64 on the float32 values of its
+    inputs in ``env32`` (the float32 oracle's ``return_all`` environment,
+    constants included; float32 inputs and constants are widened exactly).
+    The result is each group's exact answer to the rounding of float64 for
+    the same inputs the device's isolated run receives, so the float32
+    oracle's own rounding error can be measured beside the device's. The ops
+    of runtime/ops.py keep their inputs' dtype (NumPy promotes nothing to
+    float32), so the same restatement runs in float64."""
+    ex = ReferenceExecutor(graph)
+    env64 = {k: (np.asarray(v, np.float64) if np.asarray(v).dtype == np.float32 else v)
+             for k, v in env32.items()}
+    out = {}
+    for node in graph.nodes:
+        for name, val in zip(node.outputs, ex.exec_node(node, env64)):
+            if name:
+                out[name] = val
+    return out
+

@@ -218,7 +218,8 @@ def test_resnet18_b1_wave_split_convs(hip_ctx):
         return MfmaSchedule.wsplit(16, 32, 8, 1, False, 4 if K >= 2304 else 1)
 
     x = make_input(1)
-    c = compile_graph(build_resnet18(batch=1), feeds={"input": x}, schedule_fn=fn, winograd=False)
+    c = compile_graph(build_resnet18(batch=1, calibrate=True), feeds={"input": x}, schedule_fn=fn,
+                      winograd=False)
     assert sum(l.kind == "conv_ws" for l in c.module.plan) == 19
     want = run_reference(c.graph, {"input": x}, return_all=True)
     ex = HipExecutor(c.module, hip_ctx)

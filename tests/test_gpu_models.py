@@ -62,8 +62,12 @@ def _isolated(c, feeds, ctx):
 def test_resnet18_every_group(batch, mode, fold, hip_ctx):
     """Every fused group run in isolation on the oracle's inputs: the
     reference's 32 groups, or 23 once the 8 residual Add+Relu groups are
-    folded into their convs and the pool writes the flattened logits input."""
-    g = build_resnet18(batch=batch)
+    folded into their convs and the pool writes the flattened logits input.
+    The LSUV-rescaled variant of the weights (activations of order one),
+    where the float32 oracle meets the per-tensor tier against float64 in
+    every group; the stated weights are covered by
+    ``test_resnet18_stated_weights_every_group``."""
+    g = build_resnet18(batch=batch, calibrate=True)
     feeds = {"input": make_input(batch)}
     c = compile_graph(g, feeds=feeds, conv_mode=mode.split("-")[0], fuse_residual=fold,
                       winograd=mode == "implicit")
@@ -87,8 +91,8 @@ def oracle_b32():
 
     def get(name):
         if name not in cache:
-            build, x = ((build_resnet18, make_input(32)) if name == "resnet18" else
-                        (build_mobilenetv2, mb_input(32, seed=5)))
+            build, x = ((lambda batch: build_resnet18(batch=batch, calibrate=True), make_input(32))
+                        if name == "resnet18" else (build_mobilenetv2, mb_input(32, seed=5)))
             c = compile_graph(build(batch=32), feeds={"input": x}, fuse_residual=False)
             cache[name] = ({"input": x}, run_reference(c.graph, {"input": x}, return_all=True))
         return cache[name]
@@ -119,7 +123,8 @@ def test_resnet18_b32_every_group(fold, oracle_b32, hip_ctx):
     never build: split-K slices with their ordered reduce, stream-K convs
     with their fix-up, and the stem on 512 workgroups."""
     feeds, want = oracle_b32("resnet18")
-    c = compile_graph(build_resnet18(batch=32), feeds=feeds, fuse_residual=fold, winograd=False)
+    c = compile_graph(build_resnet18(batch=32, calibrate=True), feeds=feeds, fuse_residual=fold,
+                      winograd=False)
     kinds = {l.kind for l in c.module.plan}
     assert {"splitk_reduce", "streamk_fixup", "conv_smallc"} <= kinds, kinds
     assert any("_SK_" in l.kernel_name and l.kind == "conv" for l in c.module.plan)
@@ -148,16 +153,73 @@ def test_resnet18_b32_winograd_every_group(fold, oracle_b32, hip_ctx):
     kernel (13 of the 20 convs, stages 2-4 with channel slices and their
     reduce): every group in isolation within rtol 1e-4 / atol 1e-5."""
     feeds, want = oracle_b32("resnet18")
-    c = compile_graph(build_resnet18(batch=32), feeds=feeds, fuse_residual=fold, winograd=True)
+    c = compile_graph(build_resnet18(batch=32, calibrate=True), feeds=feeds, fuse_residual=fold,
+                      winograd=True)
     wino = [l for l in c.module.plan if l.kind == "wino"]
     assert len(wino) == 13 and any(l.grid[1] > 1 for l in wino)
     got = _every_group_b32(c, feeds, want, hip_ctx)
     assert len(got) == (23 if fold else 32)
 
 
+@pytest.fixture(scope="module")
+def stated_oracle():
+    """ResNet-18 with the weights as BASELINE.json states them (no
+    calibration, like the reference's exporter): the float32 oracle's every
+    tensor of the folded graph and every group re-run in float64 on those
+    inputs, once per batch."""
+    from oracle.reference import run_groups_float64
+
+    cache = {}
+
+    def get(batch):
+        if batch not in cache:
+            x = make_input(batch)
+            c = compile_graph(build_resnet18(batch=batch), feeds={"input": x})
+            want32 = run_reference(c.graph, {"input": x}, return_all=True)
+            cache[batch] = ({"input": x}, want32, run_groups_float64(c.graph, want32))
+        return cache[batch]
+    return get
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("path", ["winograd", "direct"])
+@pytest.mark.parametrize("batch", [1, 32])
+def test_resnet18_stated_weights_every_group(batch, path, stated_oracle, hip_ctx):
+    """The stated config (configs 0 and 2: the BASELINE.json weight
+    distributions used as drawn). Its residual stream reaches |x| of a few
+    hundred, and from stage 2 on the float32 oracle itself misses rtol 1e-4
+    / atol 1e-5 against float64 (up to ~6x). Every group runs in isolation on
+    the oracle's inputs and is measured against the float64 re-run of the
+    same group: held to the tier where the float32 oracle meets it there,
+    elsewhere to within 2x of the float32 oracle's own error. The chained
+    logits are held to the network tier against the float32 oracle. The
+    table printed per group (device and float32-oracle ratios to float64)
+    shows the Winograd path against the direct one."""
+    from mdlc_amd.testing import check_against_float64
+
+    feeds, want32, want64 = stated_oracle(batch)
+    c = compile_graph(build_resnet18(batch=batch), feeds=feeds, winograd=path == "winograd")
+    assert sum(l.kind == "wino" for l in c.module.plan) == (13 if path == "winograd" else 0)
+    ex = HipExecutor(c.module, hip_ctx)
+    try:
+        ex._upload_feeds(feeds)
+        got = ex.run_isolated(want32)
+        chained = ex.run(feeds)["outputs"]
+    finally:
+        ex.close()
+    assert len(got) == 23
+    checks = [check_against_float64(t, v, want32[t], want64[t], rtol=DEVICE_TENSOR.rtol,
+                                    atol=DEVICE_TENSOR.atol) for t, v in got.items()]
+    print(f"\nstated weights, batch {batch}, {path}:")
+    for r in checks:
+        print(" ", r)
+    assert all(r.ok for r in checks), [str(r) for r in checks if not r.ok]
+    assert_close("logits", chained["logits"], want32["logits"], FP32_NETWORK)
+
+
 @pytest.mark.parametrize("batch", [1, 3])
 def test_resnet18_winograd_every_group(batch, hip_ctx):
-    g = build_resnet18(batch=batch)
+    g = build_resnet18(batch=batch, calibrate=True)
     feeds = {"input": make_input(batch)}
     c = compile_graph(g, feeds=feeds, winograd=True)
     assert sum(l.kind == "wino" for l in c.module.plan) == 13

@@ -169,3 +169,45 @@ def test_typed_tensor_fields():
         back = P.parse_model(P.serialize_model(P.ModelProto(graph=P.GraphProto(initializer=[
             P.array_to_tensor("t", got)]))))
         assert np.array_equal(P.tensor_to_array(back.graph.initializer[0]), want)
+
+
+@pytest.mark.parametrize("name", ["residual_block", "resnet18_w4"])
+def test_compile_onnx_verifies_every_pass_numerically(name):
+    """``verify_passes`` with the oracle as the host evaluator: the original
+    model's outputs are the golden values, every pass is re-checked against
+    them, and ``Compiled.verify()`` passes on the optimized graph (the
+    reference's compile_onnx(verify_passes=True), mdlc/compiler.py:64-95)."""
+    feeds, _ = fixture_cases(name)[0]
+    c = compile_onnx(fixture_path(name), verify_passes=run_reference, feeds=feeds)
+    assert c.golden is not None and set(c.golden) == set(c.graph.outputs)
+    checks = c.verify()
+    assert checks and all(r.ok for r in checks), [str(r) for r in checks]
+    assert "correctness vs golden: PASS" in c.report()
+
+
+def test_compile_onnx_verify_passes_true_is_refused():
+    with pytest.raises(TypeError, match="evaluator"):
+        compile_onnx(fixture_path("mlp"), verify_passes=True)
+    c = compile_onnx(fixture_path("mlp"))
+    with pytest.raises(ValueError, match="evaluator"):
+        c.verify()
+
+
+def test_a_pass_that_breaks_numerics_is_named(monkeypatch):
+    """A planted slip in the Conv+BN fold (the folded bias loses its beta
+    term) is caught by the per-pass check, which names the pass."""
+    from mdlc_amd.passes.fuse_conv_bn import FuseConvBN
+
+    real = FuseConvBN.run
+
+    def broken(self, graph):
+        changed = real(self, graph)
+        for k in list(graph.initializers):
+            if k.endswith("_bias_bnfold"):
+                graph.initializers[k] = graph.initializers[k] * 0.5 + 0.25
+        return changed
+
+    monkeypatch.setattr(FuseConvBN, "run", broken)
+    feeds, _ = fixture_cases("conv_bn_relu")[0]
+    with pytest.raises(AssertionError, match="changed the outputs"):
+        compile_onnx(fixture_path("conv_bn_relu"), verify_passes=run_reference, feeds=feeds)

@@ -423,3 +423,78 @@ def test_view_and_matmul_planted_slips_are_caught(monkeypatch):
                         real_pad(x, np.roll(np.asarray(pads), len(pads) // 2), value, mode))
     with pytest.raises(AssertionError):
         test_pad_brute_force("constant", -2.5)
+
+
+def test_float64_group_rerun_matches_torch_float64():
+    """``run_groups_float64`` on the stated-weights ResNet-18 (a 56x56 input
+    keeps it small): every folded conv group equals torch's float64 conv2d +
+    bias + ReLU (+ the residual add) on the widened float32 inputs to float64
+    rounding, and differs from the float32 oracle by float32 rounding. A
+    planted slip that re-runs the groups without widening their inputs (so
+    every sum rounds to float32) is caught by the same comparison."""
+    from mdlc_amd.compiler import compile_graph
+    from mdlc_amd.tools.build_resnet18 import build_resnet18
+    from oracle import reference
+    from oracle.reference import run_groups_float64, run_reference
+
+    g = build_resnet18(batch=1)
+    x = np.random.default_rng(3).standard_normal((1, 3, 224, 224)).astype(np.float32)
+    c = compile_graph(g, feeds={"input": x})
+    env32 = run_reference(c.graph, {"input": x}, return_all=True)
+    want64 = run_groups_float64(c.graph, env32)
+
+    def torch_group(n, env):
+        t = lambda e: torch.from_numpy(np.asarray(env[e], np.float64))  # noqa: E731
+        a = n.attrs
+        p = a["pads"]
+        y = F.conv2d(F.pad(t(n.inputs[0]), (p[1], p[3], p[0], p[2])), t(n.inputs[1]),
+                     t(n.inputs[2]) if len(n.inputs) > 2 and n.inputs[2] else None,
+                     stride=a["strides"], dilation=a.get("dilations", [1, 1]))
+        if a.get("residual_subgraph"):
+            if a.get("activation") == "Relu":
+                y = torch.relu(y)
+            y = torch.relu(y + t(n.inputs[3]))
+        elif a.get("activation") == "Relu":
+            y = torch.relu(y)
+        return y.numpy()
+
+    convs = [n for n in c.graph.nodes if n.op_type in ("FusedConvAct", "Conv") and len(n.inputs) >= 2]
+    assert len(convs) >= 15
+    for n in convs:
+        ref = torch_group(n, env32)
+        o = n.outputs[0]
+        assert want64[o].dtype == np.float64
+        np.testing.assert_allclose(want64[o], ref, rtol=1e-12, atol=1e-12)
+        assert 0 < np.abs(env32[o] - want64[o]).max() < 1e-4 * max(1.0, np.abs(ref).max())
+
+    # planted: the re-run forgets to widen, so it is the float32 oracle again
+    def slipped(graph, env):
+        ex = reference.ReferenceExecutor(graph)
+        return {n.outputs[0]: ex.exec_node(n, env)[0] for n in graph.nodes}
+
+    bad = slipped(c.graph, env32)
+    n = convs[-1]
+    assert not np.allclose(bad[n.outputs[0]], torch_group(n, env32), rtol=1e-12, atol=1e-12)
+
+
+def test_check_against_float64_rule():
+    """The float64-relative bar: a float32 result as accurate as the float32
+    reference passes at either magnitude; one with a dropped term fails."""
+    from mdlc_amd.testing import DEVICE_TENSOR, check_against_float64
+
+    rng = np.random.default_rng(0)
+    for scale in (1.0, 300.0):
+        a = rng.standard_normal((64, 2304)) * scale
+        b = rng.standard_normal((2304, 49))
+        want64 = a @ b
+        ref32 = (a.astype(np.float32) @ b.astype(np.float32)).astype(np.float32)
+        # the same sums in another float32 order (blocked, like a tiled kernel)
+        dev = sum((a[:, k:k + 64].astype(np.float32) @ b[k:k + 64].astype(np.float32))
+                  for k in range(0, 2304, 64)).astype(np.float32)
+        r = check_against_float64("x", dev, ref32, want64, rtol=DEVICE_TENSOR.rtol,
+                                  atol=DEVICE_TENSOR.atol)
+        assert r.ok, r
+        dropped = dev - (a[:, :1].astype(np.float32) @ b[:1].astype(np.float32))
+        r = check_against_float64("x", dropped, ref32, want64, rtol=DEVICE_TENSOR.rtol,
+                                  atol=DEVICE_TENSOR.atol)
+        assert not r.ok and r.device > 10 * r.bound, r
