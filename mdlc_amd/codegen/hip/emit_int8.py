@@ -16,7 +16,7 @@ import numpy as np
 from mdlc_amd.codegen.hip import templates as T
 from mdlc_amd.codegen.hip.plan import Launch, round16
 from mdlc_amd.codegen.schedule import (
-    default_qdw_schedule, default_qschedule, qdw_valid, qmlp_layout, qsched_valid,
+    default_qdw_schedule, default_qschedule, qdw_valid, qmlp_latency_form, qmlp_layout, qsched_valid,
 )
 from mdlc_amd.passes.shape_inference import conv_geometry
 
@@ -307,9 +307,11 @@ class Int8LoweringMixin:
                         self._padded_vector(g, bd, C, np.int32), self._padded_vector(g, md, C, np.float32)]
             ops += 2 * M * C * kh * kw
             wbytes = C * (kh * kw + 8)
-        kname = self._kernel(("qmlp", C, E, lay, lo1, lo2, mix), lambda i: T.qmlp_kernel(
-            f"qmlp_c{C}_e{E}_{lay.key()}{'_dw%dx%d' % mix[:2] if mix else ''}_{i}", C, E, lay,
-            lo1=lo1, lo2=lo2, mixer=mix))
+        mixb, ew2 = qmlp_latency_form(C, E, M, lay, mix)
+        kname = self._kernel(("qmlp", C, E, lay, lo1, lo2, mix, mixb, ew2), lambda i: T.qmlp_kernel(
+            f"qmlp_c{C}_e{E}_{lay.key()}{'_dw%dx%d' % mix[:2] if mix else ''}"
+            f"{'_b%d' % mixb if mixb != 3 else ''}{'_w2' if ew2 else ''}_{i}", C, E, lay,
+            lo1=lo1, lo2=lo2, mixer=mix, mix_batch=mixb, early_w2=ew2))
         self.plan.append(Launch(
             "qmlp", kname, ins, [y], (-(-M // lay.BM), 1, 1), (256, 1, 1),
             {"M": M, "C": C, "E": E, "H": H, "W": W, "layout": lay, "node": node, "mixer": bool(mix),

@@ -765,46 +765,72 @@ struct QMlpArgs {
 // Wd[n][tap*16 + n%16] = w[n][tap] and zeros elsewhere (KD = KH*KW*16
 // rounded up to 64). The int32 sums are exact, so this equals the unfused
 // depthwise conv bit for bit.
-template <int C, int BM, int XS, int KH, int KW, int PT, int PL, int LOD>
+// A wave's tiles are handled in batches of MIXB (at most 3, or all of them):
+// the loads of every tile of a batch (its Z fragments and block-diagonal
+// weights, KD / 64 steps each) are issued before the first MFMA, so a batch
+// costs one memory round trip instead of one per tile.
+template <int C, int BM, int XS, int KH, int KW, int PT, int PL, int LOD, int MIXB_MAX>
 __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ Xs, int m0) {
   constexpr int TAPS = KH * KW;
   constexpr int KD = (TAPS * 16 + 63) / 64 * 64;
+  constexpr int NS = KD / 64;
   constexpr int CB = C / 16, TILES = (BM / 16) * CB;
+  constexpr int TPW = (TILES + 3) / 4;                // tiles per wave
+  constexpr int MIXB = TPW < MIXB_MAX ? TPW : MIXB_MAX;  // tiles per batch
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int li = lane & 15, lk = lane >> 4;
   const int hw = g.H * g.W;
   const __amdgpu_buffer_rsrc_t rZ = buffer_over(g.X, g.M * C);
-  for (int t = wave; t < TILES; t += 4) {
-    const int rb = t / CB, cb = t - (t / CB) * CB;
-    const int row = rb * 16 + li;
-    const int m = m0 + row;
-    int n = 0, oh = -(1 << 20), ow = 0;
-    if (m < g.M) {
-      n = m / hw;
-      const int s = m - n * hw;
-      oh = s / g.W;
-      ow = s - oh * g.W;
-    }
-    intx4 acc = intx4{0, 0, 0, 0};
+  const __amdgpu_buffer_rsrc_t rW = buffer_over(g.Wd, C * KD);
 #pragma unroll
-    for (int s = 0; s < KD / 64; ++s) {
-      const int tap = s * 4 + lk;
-      const int ih = oh - PT + tap / KW, iw = ow - PL + tap % KW;
-      const bool ok = tap < TAPS && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
-      const int off = ok ? ((n * g.H + ih) * g.W + iw) * C + cb * 16 : kOutside;
-      const intx4 a = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rZ, off, 0, 0));
-      const intx4 w = *reinterpret_cast<const intx4*>(g.Wd + (cb * 16 + li) * KD + s * 64 + lk * 16);
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, a, acc, 0, 0, 0);
-    }
-    // acc[j]: row `row`, channel cb*16 + lk*4 + j
-    const int c = cb * 16 + lk * 4;
-    const intx4 bv = *reinterpret_cast<const intx4*>(g.bd + c);
-    const floatx4 mv = *reinterpret_cast<const floatx4*>(g.md + c);
-    union { int w; i8 b[4]; } o;
+  for (int b0 = 0; b0 < TPW; b0 += MIXB) {
+    intx4 a[MIXB][NS], w[MIXB][NS];
+    int row[MIXB], cbv[MIXB];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o.b[j] = requant(acc[j] + bv[j], mv[j], (float)LOD);
-    *reinterpret_cast<int*>(&Xs[row * XS + c]) = o.w;
+    for (int u = 0; u < MIXB; ++u) {
+      // tile t of this wave; past the last tile (TILES % 4 != 0) a tile with
+      // every load out of range, whose result is never stored
+      const int t = wave + 4 * (b0 + u);
+      const bool tile_ok = b0 + u < TPW && t < TILES;
+      const int rb = t / CB, cb = t - (t / CB) * CB;
+      row[u] = rb * 16 + li;
+      cbv[u] = cb;
+      const int m = m0 + row[u];
+      int n = 0, oh = -(1 << 20), ow = 0;
+      if (tile_ok && m < g.M) {
+        n = m / hw;
+        const int sp = m - n * hw;
+        oh = sp / g.W;
+        ow = sp - oh * g.W;
+      }
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int tap = s * 4 + lk;
+        const int ih = oh - PT + tap / KW, iw = ow - PL + tap % KW;
+        const bool ok = tap < TAPS && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
+        const int off = ok ? ((n * g.H + ih) * g.W + iw) * C + cb * 16 : kOutside;
+        a[u][s] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rZ, off, 0, 0));
+        w[u][s] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(
+            rW, tile_ok ? ((cb * 16 + li) * KD + s * 64 + lk * 16) : kOutside, 0, 0));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < MIXB; ++u) {
+      const int t = wave + 4 * (b0 + u);
+      if (b0 + u >= TPW || t >= TILES) continue;
+      intx4 acc = intx4{0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < NS; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[u][s], a[u][s], acc, 0, 0, 0);
+      // acc[j]: row `row`, channel cb*16 + lk*4 + j
+      const int c = cbv[u] * 16 + lk * 4;
+      const intx4 bv = *reinterpret_cast<const intx4*>(g.bd + c);
+      const floatx4 mv = *reinterpret_cast<const floatx4*>(g.md + c);
+      union { int w; i8 b[4]; } o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o.b[j] = requant(acc[j] + bv[j], mv[j], (float)LOD);
+      *reinterpret_cast<int*>(&Xs[row[u] * XS + c]) = o.w;
+    }
   }
 }
 
@@ -866,8 +892,12 @@ __device__ __forceinline__ void qmlp_gemm(const i8* __restrict__ As, const i8* _
   }
 }
 
+// MIXB_MAX: the token mixer's tiles per load batch. EW2: fetch the second
+// GEMM's weight fragments at the start with the first's (registers for both
+// sets; chosen where the launch has at most one workgroup per CU, so the
+// registers cost no occupancy) instead of under the first GEMM's epilogue.
 template <int C, int E, int BM, int WGM1, int WGN1, int NI1, int WGM2, int WGN2, int NI2, int LO1,
-          int LO2, int MIX, int KH, int KW, int PT, int PL, int LOD>
+          int LO2, int MIX, int KH, int KW, int PT, int PL, int LOD, int MIXB_MAX = 3, bool EW2 = false>
 __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   constexpr int CP = (C + 63) / 64 * 64, EP = (E + 63) / 64 * 64;
   constexpr int XS = CP + 16, HS = EP + 16;    // LDS row strides (bytes)
@@ -888,8 +918,10 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   // the first weight chunk is fetched while the X tile comes in
   QMlpFrags<CP, CP, NI1> w1f;
   w1f.load(g.W1, qmlp_col0<WGN1, NI1>(0));
+  QMlpFrags<EP, EP, NI2> w2f;
+  if constexpr (EW2) w2f.load(g.W2, qmlp_col0<WGN2, NI2>(0));
   if constexpr (MIX) {
-    qmlp_mixer<C, BM, XS, KH, KW, PT, PL, LOD>(g, Xs, m0);
+    qmlp_mixer<C, BM, XS, KH, KW, PT, PL, LOD, MIXB_MAX>(g, Xs, m0);
   } else {
     const __amdgpu_buffer_rsrc_t rX = buffer_over(g.X, g.M * C);
     constexpr int CPR = CP / 16;
@@ -912,7 +944,6 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   }
   __syncthreads();
 
-  QMlpFrags<EP, EP, NI2> w2f;
   qmlp_gemm<CP, XS, CP, E, BM, WGM1, WGN1, NI1>(Xs, g.W1, w1f, [&](int r, int n, const intx4& acc,
                                                                     int, int) {
     const intx4 bv = *reinterpret_cast<const intx4*>(&b1s[n]);
@@ -921,7 +952,9 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) o.b[j] = tab[(int)requant(acc[j] + bv[j], mv[j], (float)LO1) + 128];
     *reinterpret_cast<int*>(&Hs[r * HS + n]) = o.w;
-  }, [&]() { w2f.load(g.W2, qmlp_col0<WGN2, NI2>(0)); });
+  }, [&]() {
+    if constexpr (!EW2) w2f.load(g.W2, qmlp_col0<WGN2, NI2>(0));
+  });
   __syncthreads();
 
   qmlp_gemm<EP, HS, EP, C, BM, WGM2, WGN2, NI2>(Hs, g.W2, w2f, [&](int r, int n, const intx4& acc,

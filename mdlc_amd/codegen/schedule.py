@@ -381,6 +381,25 @@ def qmlp_layout(C: int, E: int, M: int, bm: Optional[int] = None) -> Optional[QM
     return None
 
 
+def qmlp_latency_form(C: int, E: int, M: int, layout: QMlpLayout, mixer) -> tuple:
+    """(token-mixer tiles per load batch, fetch both weight sets at the
+    start) for the fused MLP. A launch with at most one workgroup per CU has
+    one wave per SIMD, so registers cost no occupancy: every mixer tile of a
+    wave is loaded in one batch (while its fragments fit in 160 registers)
+    and the second GEMM's weights come with the first's, leaving one memory
+    round trip for each. Larger grids keep batches of three and the second
+    weights under the first GEMM's epilogue."""
+    if -(-M // layout.BM) > CUS:
+        return 3, False
+    tiles_per_wave = -(-(layout.BM // 16) * (C // 16) // 4)
+    if mixer:
+        steps = -(-mixer[0] * mixer[1] * 16 // 64)
+        batch = tiles_per_wave if tiles_per_wave * steps * 8 <= 160 else 3
+    else:
+        batch = 3
+    return max(1, min(batch, max(tiles_per_wave, 1))), True
+
+
 # ----- direct convolution for few input channels ---------------------------
 
 SMALLC_MAX_C = 4          # input channels up to which a conv takes the direct kernel

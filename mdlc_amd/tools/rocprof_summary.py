@@ -36,6 +36,25 @@ def kernel_stats(path: str) -> list:
     return rows
 
 
+def kernel_stats_by_grid(path: str) -> list:
+    """Per (kernel name, grid): calls, total, average, median, min, max
+    duration — kernels of one name built by separate plans for different
+    shapes (the micro GEMMs) are told apart by their grids."""
+    con = sqlite3.connect(path)
+    by: dict = {}
+    for name, gx, gy, gz, d in con.execute(
+            "select name, grid_x, grid_y, grid_z, duration from kernels order by dispatch_id"):
+        by.setdefault((name, gx, gy, gz), []).append(d)
+    con.close()
+    rows = []
+    for (name, gx, gy, gz), v in by.items():
+        w = sorted(v)
+        k = len(w)
+        med = w[k // 2] if k % 2 else 0.5 * (w[k // 2 - 1] + w[k // 2])
+        rows.append((name, (gx, gy, gz), k, sum(v), sum(v) / k, med, w[0], w[-1]))
+    return sorted(rows, key=lambda r: -r[3])
+
+
 def kernel_medians(path: str) -> dict:
     """Median dispatch duration per kernel name."""
     con = sqlite3.connect(path)
@@ -99,6 +118,8 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("db", nargs="?")
     ap.add_argument("--counter", default="")
+    ap.add_argument("--by-grid", action="store_true",
+                    help="one row per (kernel, grid size in work-items) instead of per kernel name")
     ap.add_argument("--traffic", nargs=4, metavar=("FETCH_DB", "WRITE_DB", "COPY_FETCH_DB", "COPY_WRITE_DB"))
     ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--out", default="")
@@ -147,6 +168,15 @@ def main(argv=None) -> int:
         print(f"{'kernel':64s} {'dispatches':>10s} {'avg ' + args.counter:>18s}")
         for name, n, avg in counter_stats(args.db, args.counter):
             print(f"{name[:64]:64s} {n:10d} {avg:18.1f}")
+        return 0
+    if args.by_grid:
+        rows = kernel_stats_by_grid(args.db)
+        total = sum(r[3] for r in rows) or 1
+        print(f"{'kernel':56s} {'grid':>20s} {'calls':>6s} {'avg_us':>8s} {'med_us':>8s} "
+              f"{'min_us':>8s} {'pct':>6s}")
+        for name, grid, n, tot, avg, med, mn, mx in rows:
+            print(f"{name[:56]:56s} {'x'.join(str(g) for g in grid):>20s} {n:6d} {avg / 1e3:8.2f} "
+                  f"{med / 1e3:8.2f} {mn / 1e3:8.2f} {100.0 * tot / total:6.2f}")
         return 0
     rows = kernel_stats(args.db)
     med = kernel_medians(args.db)
