@@ -45,7 +45,8 @@ import numpy as np
 
 from mdlc_amd.codegen.hip import templates as T
 from mdlc_amd.codegen.hip.emit_int8 import Int8LoweringMixin
-from mdlc_amd.codegen.hip.plan import LIBRARY_PARTS, QUANT_OPS, HipModule, Launch, round4, round16  # noqa: F401
+from mdlc_amd.codegen.hip.plan import (LIBRARY_PARTS, QUANT_OPS, HipModule, Launch,  # noqa: F401
+                                       library_parts, round4, round16)
 from mdlc_amd.codegen.schedule import (WINO_BK, WINO_BM, WINO_BN, MfmaSchedule, default_schedule,
                                       smallc_fits, smallc_pairs, smallc_tile, split_slices,
                                       unsplit_if_one_slice, wino_fits,
@@ -197,7 +198,7 @@ class HipCodegen(Int8LoweringMixin):
                 getattr(self, "_lower_" + op.lower())(g, node)
             else:
                 raise NotImplementedError(f"HIP codegen: no device lowering for {op!r}")
-        lib = LIBRARY_PARTS + (("int8",) if any(n.op_type in QUANT_OPS for n in g.nodes) else ())
+        lib = library_parts({l.kind for l in self.plan})
         return HipModule(g, self.kernels, self.plan, self.scratch, self.consts, lib,
                          scratch_class=self.scratch_class, device_layout=dict(self.layout))
 
@@ -226,11 +227,14 @@ class HipCodegen(Int8LoweringMixin):
             return
         # the Winograd kernel reads its input, bias and residual through buffer
         # resources of byte offsets below 2^31 (offsets at 0x7ffffff0 read as zeros) and
-        # divides tile indices below 2^21 in float
+        # divides tile indices and workgroup indices (at most one per channel-block,
+        # tile-block and chunk) below 2^21 in float
+        wino_tiles = geo["N"] * -(-geo["OH"] // 2) * -(-geo["OW"] // 2)
         if (self.conv_mode == "implicit" and self.winograd and wino_fits(geo)
                 and geo["N"] * geo["C"] * geo["H"] * geo["W"] * 4 < 0x7ffffff0
                 and geo["N"] * geo["OC"] * geo["OH"] * geo["OW"] * 4 < 0x7ffffff0
-                and geo["N"] * -(-geo["OH"] // 2) * -(-geo["OW"] // 2) < 2 ** 21
+                and wino_tiles < 2 ** 21
+                and -(-geo["OC"] // WINO_BM) * -(-wino_tiles // WINO_BN) * -(-geo["C"] // WINO_BK) < 2 ** 21
                 and (self.winograd is True or wino_pays(
                     geo["OC"], geo["N"] * -(-geo["OH"] // 2) * -(-geo["OW"] // 2), geo["C"]))):
             self._lower_wino(g, node, geo, has_bias)

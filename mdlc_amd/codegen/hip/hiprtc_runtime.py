@@ -153,7 +153,12 @@ def compile_code_object(source: str, name: str = "kernels.hip", arch: str = HIP_
     path = os.path.join(CACHE_DIR, key + ".co")
     if use_cache and os.path.exists(path):
         with open(path, "rb") as f:
-            return f.read()
+            blob = f.read()
+        try:
+            os.utime(path)          # last use, so stale objects can be told apart by age
+        except OSError:
+            pass
+        return blob
     arr = (ctypes.c_char_p * len(opts))(*[o.encode() for o in opts])
     code = ctypes.c_void_p()
     size = ctypes.c_size_t()

@@ -113,9 +113,17 @@ __device__ __forceinline__ void conv_wino_f32(const WinoArgs& g) {
 
   const int P = g.N * g.TH * g.TW;                  // < 2^21 (checked by the host)
   const int tiles_n = (P + 63) >> 6;
-  const int ocb = wino_div(blockIdx.x, tiles_n, __builtin_amdgcn_rcpf((float)tiles_n));
-  const int t0 = (blockIdx.x - ocb * tiles_n) * 64;
-  const int slice = SPLIT ? blockIdx.y : 0;
+  // Work item w = (ocb * slices + slice) * tiles_n + tile block, spread so
+  // that each XCD (workgroups are dispatched to XCD linear id % 8) runs a
+  // contiguous range of w: the workgroups that stream one channel block's
+  // filter images share an XCD and its L2 instead of every XCD fetching
+  // every block's filters.
+  const int slices = SPLIT ? (int)gridDim.y : 1;
+  const int w = xcd_remap(blockIdx.x + (int)gridDim.x * (int)blockIdx.y, (int)gridDim.x * slices);
+  const int os = wino_div(w, tiles_n, __builtin_amdgcn_rcpf((float)tiles_n));
+  const int t0 = (w - os * tiles_n) * 64;
+  const int ocb = SPLIT ? os / slices : os;
+  const int slice = SPLIT ? os - ocb * slices : 0;
   const int chunk0 = slice * g.nchunk;
   const int HW = g.H * g.W;
   const float* ublk = g.U + (size_t)ocb * (g.CP / 8) * WINO_USTAGE;
