@@ -16,7 +16,8 @@ import numpy as np
 from mdlc_amd.codegen.hip import templates as T
 from mdlc_amd.codegen.hip.plan import Launch, round16
 from mdlc_amd.codegen.schedule import (
-    default_qdw_schedule, default_qschedule, qdw_valid, qmlp_latency_form, qmlp_layout, qsched_valid,
+    LDS_LIMIT, default_qdw_schedule, default_qschedule, qdw_valid, qmlp_latency_form, qmlp_layout,
+    qmlp_lds_bytes, qsched_valid,
 )
 from mdlc_amd.passes.shape_inference import conv_geometry
 
@@ -267,7 +268,8 @@ class Int8LoweringMixin:
             raise ValueError("QMlp weights do not match the input's channels")
         if np.asarray(g.initializers[tab]).size != 256:
             raise NotImplementedError("HIP codegen: QMlp needs a constant 256-entry table")
-        lay = self._qmlp_layout(node, C, E, M)
+        taps = int(np.prod(mixer["kernel_shape"])) if mixer else 0
+        lay = self._qmlp_layout(node, C, E, M, taps)
         if lay is None:
             raise NotImplementedError(f"HIP codegen: no fused MLP tiling for C={C}, E={E}")
         if M * C >= 2 ** 31 - 2 ** 20:
@@ -320,10 +322,14 @@ class Int8LoweringMixin:
              # algorithmic HBM bytes: x (or z) once, y once, the weights, bias and mult
              "bytes": 2 * M * C + 2 * C * E + 8 * (C + E) + 256 + wbytes}))
 
-    def _qmlp_layout(self, node, C, E, M):
+    def _qmlp_layout(self, node, C, E, M, taps):
+        """The schedule source's tiling when it gives one that fits LDS with
+        the node's token mixer, else the default for these sizes."""
         fn = getattr(self.schedule_fn, "qmlp_layout", None)
         lay = fn(C, E, M) if fn is not None else None
-        return lay if lay is not None else qmlp_layout(C, E, M)
+        if lay is not None and qmlp_lds_bytes(C, E, lay.BM, taps) <= LDS_LIMIT:
+            return lay
+        return qmlp_layout(C, E, M, mixer_taps=taps)
 
     def _lower_qgemm(self, g, node):
         x, w, b, m = node.inputs[:4]

@@ -766,26 +766,58 @@ struct QMlpArgs {
 // rounded up to 64). The int32 sums are exact, so this equals the unfused
 // depthwise conv bit for bit.
 // A wave's tiles are handled in batches of MIXB (at most 3, or all of them):
-// the loads of every tile of a batch (its Z fragments and block-diagonal
-// weights, KD / 64 steps each) are issued before the first MFMA, so a batch
-// costs one memory round trip instead of one per tile.
+// the loads of every tile of a batch (its Z fragments, KD / 64 steps each)
+// are issued before the first MFMA, so a batch costs one memory round trip
+// instead of one per tile. The block-diagonal weights, bias and multipliers
+// are read from LDS: the workgroup copies them there once (Wds rows padded
+// to KD + 16 bytes, so the 16 lanes reading one 16-byte column of 16 rows hit
+// distinct banks), the copy's global loads issued ahead of the first batch's
+// Z loads and its LDS stores and barrier after them; every tile used to load
+// its channel block's weights from L2 again.
+template <int C, int KH, int KW>
+struct QMixDims {
+  static constexpr int KD = (KH * KW * 16 + 63) / 64 * 64;   // Wd row (bytes) in global memory
+  static constexpr int WS = KD + 16;                          // and in LDS
+};
+
 template <int C, int BM, int XS, int KH, int KW, int PT, int PL, int LOD, int MIXB_MAX>
-__device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ Xs, int m0) {
+__device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ Xs, int m0,
+                                           i8* __restrict__ Wds, int* __restrict__ bds,
+                                           float* __restrict__ mds) {
   constexpr int TAPS = KH * KW;
-  constexpr int KD = (TAPS * 16 + 63) / 64 * 64;
+  constexpr int KD = QMixDims<C, KH, KW>::KD, WS = QMixDims<C, KH, KW>::WS;
   constexpr int NS = KD / 64;
   constexpr int CB = C / 16, TILES = (BM / 16) * CB;
   constexpr int TPW = (TILES + 3) / 4;                // tiles per wave
   constexpr int MIXB = TPW < MIXB_MAX ? TPW : MIXB_MAX;  // tiles per batch
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  constexpr int WCH = C * KD / 16;                    // 16-byte chunks of Wd
+  constexpr int WPT = (WCH + 255) / 256;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int li = lane & 15, lk = lane >> 4;
   const int hw = g.H * g.W;
   const __amdgpu_buffer_rsrc_t rZ = buffer_over(g.X, g.M * C);
   const __amdgpu_buffer_rsrc_t rW = buffer_over(g.Wd, C * KD);
+  intx4 wst[WPT];
+#pragma unroll
+  for (int i = 0; i < WPT; ++i) {
+    const int idx = tid + 256 * i;
+    wst[i] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(
+        rW, idx < WCH ? idx * 16 : kOutside, 0, 0));
+  }
+  constexpr int CPT = (C + 255) / 256;
+  int bdv[CPT];
+  float mdv[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = tid + 256 * i;
+    bdv[i] = c < C ? g.bd[c] : 0;
+    mdv[i] = c < C ? g.md[c] : 0.f;
+  }
 #pragma unroll
   for (int b0 = 0; b0 < TPW; b0 += MIXB) {
-    intx4 a[MIXB][NS], w[MIXB][NS];
+    intx4 a[MIXB][NS];
     int row[MIXB], cbv[MIXB];
 #pragma unroll
     for (int u = 0; u < MIXB; ++u) {
@@ -811,9 +843,24 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
         const bool ok = tap < TAPS && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
         const int off = ok ? ((n * g.H + ih) * g.W + iw) * C + cb * 16 : kOutside;
         a[u][s] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rZ, off, 0, 0));
-        w[u][s] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(
-            rW, tile_ok ? ((cb * 16 + li) * KD + s * 64 + lk * 16) : kOutside, 0, 0));
       }
+    }
+    if (b0 == 0) {                                    // the weights reach LDS (once)
+#pragma unroll
+      for (int i = 0; i < WPT; ++i) {
+        const int idx = tid + 256 * i;
+        if (WCH % 256 == 0 || idx < WCH)
+          *reinterpret_cast<intx4*>(&Wds[(idx / (KD / 16)) * WS + (idx % (KD / 16)) * 16]) = wst[i];
+      }
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int c = tid + 256 * i;
+        if (c < C) {
+          bds[c] = bdv[i];
+          mds[c] = mdv[i];
+        }
+      }
+      __syncthreads();
     }
 #pragma unroll
     for (int u = 0; u < MIXB; ++u) {
@@ -821,11 +868,14 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
       if (b0 + u >= TPW || t >= TILES) continue;
       intx4 acc = intx4{0, 0, 0, 0};
 #pragma unroll
-      for (int s = 0; s < NS; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[u][s], a[u][s], acc, 0, 0, 0);
+      for (int s = 0; s < NS; ++s) {
+        const intx4 w = *reinterpret_cast<const intx4*>(&Wds[(cbv[u] * 16 + li) * WS + s * 64 + lk * 16]);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, a[u][s], acc, 0, 0, 0);
+      }
       // acc[j]: row `row`, channel cb*16 + lk*4 + j
       const int c = cbv[u] * 16 + lk * 4;
-      const intx4 bv = *reinterpret_cast<const intx4*>(g.bd + c);
-      const floatx4 mv = *reinterpret_cast<const floatx4*>(g.md + c);
+      const intx4 bv = *reinterpret_cast<const intx4*>(&bds[c]);
+      const floatx4 mv = *reinterpret_cast<const floatx4*>(&mds[c]);
       union { int w; i8 b[4]; } o;
 #pragma unroll
       for (int j = 0; j < 4; ++j) o.b[j] = requant(acc[j] + bv[j], mv[j], (float)LOD);
@@ -912,6 +962,10 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   __shared__ __attribute__((aligned(16))) float m1s[E];
   __shared__ __attribute__((aligned(16))) int b2s[C];
   __shared__ __attribute__((aligned(16))) float m2s[C];
+  // the token mixer's weights, bias and multipliers (a byte when there is none)
+  __shared__ __attribute__((aligned(16))) i8 Wds[MIX ? C * QMixDims<C, KH, KW>::WS : 16];
+  __shared__ __attribute__((aligned(16))) int bds[MIX ? C : 4];
+  __shared__ __attribute__((aligned(16))) float mds[MIX ? C : 4];
   const int tid = threadIdx.x;
   const int m0 = blockIdx.x * BM;
 
@@ -921,7 +975,7 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   QMlpFrags<EP, EP, NI2> w2f;
   if constexpr (EW2) w2f.load(g.W2, qmlp_col0<WGN2, NI2>(0));
   if constexpr (MIX) {
-    qmlp_mixer<C, BM, XS, KH, KW, PT, PL, LOD, MIXB_MAX>(g, Xs, m0);
+    qmlp_mixer<C, BM, XS, KH, KW, PT, PL, LOD, MIXB_MAX>(g, Xs, m0, Wds, bds, mds);
   } else {
     const __amdgpu_buffer_rsrc_t rX = buffer_over(g.X, g.M * C);
     constexpr int CPR = CP / 16;

@@ -358,15 +358,22 @@ def qmlp_grid(ncols: int, k: int, bm: int) -> Optional[tuple]:
     return None
 
 
-def qmlp_lds_bytes(C: int, E: int, bm: int) -> int:
-    return bm * (_round64(C) + 16 + _round64(E) + 16) + 256
+def qmlp_lds_bytes(C: int, E: int, bm: int, mixer_taps: int = 0) -> int:
+    """LDS of the fused MLP: the X and hidden tiles, the lookup table, both
+    GEMMs' bias and multipliers, and with a token mixer of ``mixer_taps``
+    taps its block-diagonal weights (rows of KD + 16 bytes), bias and
+    multipliers."""
+    mixer = C * (_round64(mixer_taps * 16) + 16 + 8) if mixer_taps else 0
+    return bm * (_round64(C) + 16 + _round64(E) + 16) + 256 + 8 * (C + E) + mixer
 
 
-def qmlp_layout(C: int, E: int, M: int, bm: Optional[int] = None) -> Optional[QMlpLayout]:
+def qmlp_layout(C: int, E: int, M: int, bm: Optional[int] = None,
+                mixer_taps: int = 0) -> Optional[QMlpLayout]:
     """The default tiling: 64-row workgroups when that still gives one per
     CU, else 32 rows when that gives 128, else 16 — or the next larger row
-    count that tiles both GEMMs; ``bm`` forces one. None when the channel
-    counts admit no tiling (C and E must be multiples of 16)."""
+    count that tiles both GEMMs and fits LDS with a token mixer of
+    ``mixer_taps`` taps; ``bm`` forces one. None when the channel counts admit
+    no tiling (C and E must be multiples of 16)."""
     if C % 16 or E % 16:
         return None
     if bm is None:
@@ -376,7 +383,7 @@ def qmlp_layout(C: int, E: int, M: int, bm: Optional[int] = None) -> Optional[QM
         rows = [bm]
     for r in rows:
         g1, g2 = qmlp_grid(E, C, r), qmlp_grid(C, E, r)
-        if g1 is not None and g2 is not None and qmlp_lds_bytes(C, E, r) <= LDS_LIMIT:
+        if g1 is not None and g2 is not None and qmlp_lds_bytes(C, E, r, mixer_taps) <= LDS_LIMIT:
             return QMlpLayout(r, g1, g2)
     return None
 

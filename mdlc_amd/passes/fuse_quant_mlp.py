@@ -134,6 +134,10 @@ class FuseQuantMixer(Pass):
                     or any(int(v) != 1 for v in a.get("dilations", [1, 1]))
                     or pads != [kh // 2, kw // 2, kh // 2, kw // 2]):
                 continue
+            E = graph.initializers[q.inputs[1]].shape[0]
+            M = zi.shape[0] * zi.shape[2] * zi.shape[3]
+            if qmlp_layout(C, E, M or 1, mixer_taps=int(kh) * int(kw)) is None:
+                continue                 # the mixer's weights leave no tiling room in LDS
             mixer = {"kernel_shape": [int(kh), int(kw)], "pads": pads, "activation": a.get("activation")}
             fused = Node("QMlp", list(d.inputs[:4]) + list(q.inputs[1:]), list(q.outputs),
                          dict(q.attrs, mixer=mixer, mixed=x), (d.name or "QConv") + "+" + (q.name or "mlp"),
