@@ -47,8 +47,8 @@ from mdlc_amd.codegen.hip import templates as T
 from mdlc_amd.codegen.hip.emit_int8 import Int8LoweringMixin
 from mdlc_amd.codegen.hip.plan import (LIBRARY_PARTS, QUANT_OPS, HipModule, Launch,  # noqa: F401
                                        library_parts, round4, round16)
-from mdlc_amd.codegen.schedule import (WINO_BK, WINO_BM, WINO_BN, MfmaSchedule, default_schedule,
-                                      smallc_fits, smallc_pairs, smallc_tile, split_slices,
+from mdlc_amd.codegen.schedule import (WINO_BK, WINO_BM, WINO_BN, MfmaSchedule, conv_pool_band,
+                                      default_schedule, smallc_fits, smallc_pairs, smallc_tile, split_slices,
                                       unsplit_if_one_slice, wino_fits,
                                       wino_patch, wino_pays, wino_slices)
 from mdlc_amd.ir import DType, Graph, Node
@@ -211,6 +211,9 @@ class HipCodegen(Int8LoweringMixin):
         y = node.outputs[0]
         a = node.attrs
         act = a.get("activation")
+        if a.get("maxpool"):
+            self._lower_conv_pool(g, node, geo, has_bias)
+            return
         if geo["group"] != 1:
             if geo["ICG"] == 1 and geo["OC"] % geo["C"] == 0:
                 self._lower_dwconv(g, node, geo, has_bias)
@@ -424,6 +427,53 @@ class HipCodegen(Int8LoweringMixin):
             (256, 1, 1),
             {"S": slices, "M": OC, "N": P, "ldc": 0, "hw": OH * OW, "node": node,
              "bytes": 4 * (slices + 1 + len(extra)) * OC * P}))
+
+    def _lower_conv_pool(self, g: Graph, node: Node, geo: dict, has_bias: bool) -> None:
+        """A small-channel conv carrying the 3x3 stride-2 max pool that
+        followed it (``attrs["maxpool"]``, folded by ``FuseConvMaxPool``): one
+        launch writes the pooled output. The weights are packed here as
+        [16-channel block][4-deep k step][lane], lane 16 lk + li holding
+        w[16 block + li][4 step + lk] in (c, kh, kw) order, zeros past K and
+        past OC."""
+        mp = node.attrs["maxpool"]
+        if (list(mp["kernel_shape"]) != [3, 3] or list(mp["strides"]) != [2, 2]
+                or list(mp["pads"]) != [1, 1, 1, 1]):
+            raise NotImplementedError(f"HIP codegen: fused max pool {mp} (only 3x3, stride 2, pad 1)")
+        if self.conv_mode != "implicit" or not self.small_conv or geo["group"] != 1:
+            raise NotImplementedError("HIP codegen: a conv with a folded max pool needs the implicit "
+                                      "small-channel lowering")
+        C, KH, KW, SH, SW = geo["C"], geo["KH"], geo["KW"], geo["SH"], geo["SW"]
+        OC, OH, OW, N, H, W = geo["OC"], geo["OH"], geo["OW"], geo["N"], geo["H"], geo["W"]
+        R = conv_pool_band(C, KH, KW, SH, SW, geo["DH"], geo["DW"], N, OH, OW)
+        if R is None:
+            raise NotImplementedError(f"HIP codegen: no fused conv + pool band for {geo}")
+        PH, PW = OH // 2, OW // 2
+        if 4 * N * max(C * H * W, OC * PH * PW) >= 0x7ffffff0:
+            raise NotImplementedError("HIP codegen: fused conv + pool tensors of 2^31 bytes or more")
+        x, w, y = node.inputs[0], node.inputs[1], node.outputs[0]
+        K = C * KH * KW
+        ns = -(-K // 4)
+        groups = -(-OC // 64)
+        wpad = np.zeros((groups * 64, ns * 4), np.float32)
+        wpad[:OC, :K] = np.asarray(g.initializers[w], np.float32).reshape(OC, K)
+        packed = wpad.reshape(groups * 4, 16, ns, 4).transpose(0, 2, 3, 1).reshape(groups * 4, ns, 64)
+        wdev = self._pack(f"{w}__dev_convpool", packed)
+        bias = [node.inputs[2]] if has_bias else []
+        a = node.attrs
+        act = a.get("activation")
+        if act not in (None, "Identity", "Relu", "Relu6", "Clip"):
+            raise NotImplementedError(f"HIP codegen: max pool after {act!r} (not non-decreasing)")
+        win = (C, KH, KW, SH, SW, geo["PT"], geo["PL"])
+        sig = ("conv_pool", win, R, OW // 16, has_bias, self._act_sig(a))
+        kname = self._kernel(sig, lambda i: T.conv_pool_kernel(
+            f"conv_pool_{KH}x{KW}s{SH}_{act or 'none'}_R{R}_{i}", win, R, OW // 16,
+            with_bias=has_bias, activation=act, attrs=self._act_attrs(a)))
+        P = N * OH * OW
+        self.plan.append(Launch(
+            "conv_pool", kname, [x, wdev] + bias, [y], (N * (PH // R), groups, 1), (256, 1, 1),
+            {"M": OC, "N": P, "K": K, "batch": N, "H": H, "W": W, "OC": OC, "OH": OH, "OW": OW,
+             "band": R, "node": node, "flops": 2 * OC * P * K,
+             "bytes": 4 * (N * C * H * W + OC * K + N * OC * PH * PW + (OC if has_bias else 0))}))
 
     def _lower_conv_smallc(self, g: Graph, node: Node, geo: dict, has_bias: bool) -> None:
         """A conv with few input channels (a network's stem): the direct

@@ -326,6 +326,9 @@ def launch_args(l: Launch, arg_ptr) -> list:
     elif k == "conv_smallc":
         args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
         args += [I(m[f]) for f in ("batch", "H", "W", "OC", "OH", "OW")]
+    elif k == "conv_pool":
+        args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
+        args += [I(m[f]) for f in ("batch", "H", "W", "OC", "OH")]
     elif k == "streamk_fixup":
         args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
         args += [I(m[f]) for f in ("M", "N", "K", "full", "ldc", "hw")]

@@ -326,6 +326,29 @@ def conv_smallc_kernel(name: str, win: tuple, tile: tuple, *, with_bias: bool,
         f"{'res' if residual else 'nullptr'}, y, N, H, W, OC, OH, OW);\n}}\n")
 
 
+def conv_pool_kernel(name: str, win: tuple, band: int, nbx: int, *, with_bias: bool,
+                     activation: Optional[str], attrs: dict) -> tuple:
+    """Small-channel convolution fused with the 3x3 stride-2 max pool that
+    follows it (the activation must be non-decreasing: none, Relu, Relu6,
+    Clip). ``win`` = (C, KH, KW, SH, SW, PT, PL); a workgroup computes
+    ``band`` pooled rows of one image for 64 output channels, the conv
+    output being ``nbx`` column blocks of 16 wide.
+    ABI: (x, wp, [bias], y, int N, int H, int W, int OC, int OH) with ``wp``
+    the weights packed [16-channel block][4-deep k step][lane]; grid x =
+    images x bands, y = 64-channel groups; 256 threads."""
+    epi = f"{name}_epi"
+    src = epilogue_struct(epi, bias_mode="row" if with_bias else None, activation=activation,
+                          attrs=attrs)
+    bias_arg = "const float* __restrict__ bias, " if with_bias else ""
+    targs = ", ".join(str(int(v)) for v in tuple(win) + (band, nbx))
+    return name, src + (
+        f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
+        f"    const float* __restrict__ x, const float* __restrict__ wp, {bias_arg}"
+        "float* __restrict__ y,\n    int N, int H, int W, int OC, int OH) {\n"
+        f"  mdlc::conv_pool_f32<{epi}, {targs}>(x, wp, {'bias' if with_bias else 'nullptr'}, "
+        "y, N, H, W, OC, OH);\n}\n")
+
+
 def wino_kernel(name: str, *, split: bool, ploads: int, full: bool, with_bias: bool,
                 activation: Optional[str], attrs: dict, residual: Optional[str] = None) -> tuple:
     """3x3 stride-1 convolution by Winograd F(2x2, 3x3) on the matrix cores.

@@ -436,6 +436,42 @@ def smallc_lds_bytes(C: int, KH: int, KW: int, SH: int, SW: int, TR: int, TC: in
     return 4 * C * ((TR - 1) * SH + KH) * ((TC - 1) * SW + KW)
 
 
+# ----- small-channel convolution fused with the 3x3 stride-2 max pool -------
+
+POOL_BAND_MAX = 7         # pooled rows per band at most (2R+1 conv-row accumulators of 4)
+POOL_BAND_MIN = 4         # fewer, and the band's extra conv row outweighs the pool launch
+CONV_POOL_LDS = 150 * 1024
+CONV_POOL_MAX_K = 256     # weights (and their patch offsets) held in registers per k step
+
+
+def conv_pool_band(C: int, KH: int, KW: int, SH: int, SW: int, DH: int, DW: int, N: int,
+                   OH: int, OW: int) -> Optional[int]:
+    """Pooled rows per workgroup band of the fused small-channel conv + max
+    pool (3x3, stride 2, padding 1, pooled size OH/2 x OW/2): the largest R
+    in [POOL_BAND_MIN, POOL_BAND_MAX] dividing OH/2 whose input patch (2R
+    conv-row steps plus the kernel, every column) fits the LDS; None when the
+    fused kernel does not apply — more than SMALLC_MAX_C input channels,
+    dilation, OW not a multiple of 16 or odd OH, a patch row wider than the
+    workgroup, or fewer bands than CUs (one band per CU is what keeps the
+    chip busy; smaller batches run the two launches)."""
+    if C > SMALLC_MAX_C or DH != 1 or DW != 1 or C * KH * KW > CONV_POOL_MAX_K:
+        return None
+    if OW % 16 or OH % 2 or OW <= 0 or OH <= 0:
+        return None
+    PC = (OW - 1) * SW + KW
+    if PC > 256:
+        return None
+    PH = OH // 2
+    for R in range(POOL_BAND_MAX, POOL_BAND_MIN - 1, -1):
+        if PH % R:
+            continue
+        PR = 2 * R * SH + KH
+        if 4 * C * PR * PC > CONV_POOL_LDS or 4 * (2 * R + 1) * SH * PC >= 65536:
+            continue
+        return R if N * (PH // R) >= CUS else None
+    return None
+
+
 
 # ----- Winograd F(2x2, 3x3) convolution -------------------------------------
 

@@ -23,6 +23,7 @@ from mdlc_amd.passes.base import PassManager
 from mdlc_amd.passes.fold_flatten import FoldPoolFlatten
 from mdlc_amd.passes.fuse_quant_epilogue import FuseInputQuantize, FuseQuantEpilogue
 from mdlc_amd.passes.fuse_quant_mlp import FuseQuantMixer, FuseQuantMlp
+from mdlc_amd.passes.fuse_conv_pool import FuseConvMaxPool
 from mdlc_amd.passes.fuse_residual import FuseResidualEpilogue
 from mdlc_amd.passes.shape_inference import infer_shapes, make_dummy_feeds
 from mdlc_amd.runtime.memory_planner import MemoryPlan, plan_memory
@@ -84,7 +85,8 @@ def compile_graph(graph: Graph, *, batch: int = 1, feeds: Optional[dict] = None,
                   schedule_fn=None, verify: Optional[Callable] = None,
                   conv_mode: str = "implicit", fuse_int8_epilogues: bool = True,
                   int8_depthwise: str = "mfma", fuse_residual: bool = True,
-                  fuse_int8_mlp=True, small_conv: bool = True, winograd="auto") -> Compiled:
+                  fuse_int8_mlp=True, small_conv: bool = True, winograd="auto",
+                  fuse_pool: bool = True) -> Compiled:
     """Optimize, plan and lower ``graph``. The reference pipeline runs first,
     unchanged. Then backend epilogue folds: ``fuse_int8_epilogues`` folds a
     QLut or QAdd into the QConv that feeds it; ``fuse_residual`` folds a
@@ -99,7 +101,9 @@ def compile_graph(graph: Graph, *, batch: int = 1, feeds: Optional[dict] = None,
     ("mfma" or "vector"). ``small_conv`` runs convs with at most four input
     channels (stems) on the direct small-channel kernel in implicit mode. ``winograd``
     runs 3x3 stride-1 convs as Winograd F(2x2, 3x3) in implicit mode: "auto" where its
-    grid fills at least half the CUs, True always, False never (the implicit GEMM)."""
+    grid fills at least half the CUs, True always, False never (the implicit GEMM).
+    ``fuse_pool`` (with ``small_conv`` in implicit mode) folds a 3x3 stride-2 max pool
+    into the small-channel conv that feeds it where every CU gets a band of its rows."""
     original = graph.clone()
     if feeds is None:
         feeds = make_dummy_feeds(graph, batch=batch)
@@ -112,7 +116,8 @@ def compile_graph(graph: Graph, *, batch: int = 1, feeds: Optional[dict] = None,
     post = ([FuseResidualEpilogue()] if fuse_residual else []) + \
         ([FuseQuantMlp(always=fuse_int8_mlp == "always"), FuseQuantMixer()]
          if quant and fuse_int8_mlp else []) + \
-        ([FuseInputQuantize()] if quant else []) + ([FoldPoolFlatten()] if fuse_residual else [])
+        ([FuseInputQuantize()] if quant else []) + ([FoldPoolFlatten()] if fuse_residual else []) + \
+        ([FuseConvMaxPool()] if fuse_pool and small_conv and conv_mode == "implicit" else [])
     if post:
         PassManager(post, verify=_structural_verifier(verify), history=pm.history).run(graph)
     mem_plan = plan_memory(graph)

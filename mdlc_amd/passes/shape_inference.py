@@ -105,6 +105,9 @@ def node_output_infos(node: Node, shape_of, dtype_of, const_of) -> list:
     if op in ("Conv", "FusedConvAct", "FusedConvBNAct", "QConv"):
         g = conv_geometry(node, s0, shape_of(ins[1]))
         dt = DType.INT8 if op == "QConv" else d0
+        if a.get("maxpool"):             # a folded max pool: the pooled output
+            return [(_pool_shape(Node("MaxPool", [], [], dict(a["maxpool"])),
+                                 (g["N"], g["OC"], g["OH"], g["OW"])), dt)]
         return [((g["N"], g["OC"], g["OH"], g["OW"]), dt)]
     if op == "QMlp":                 # [token mixer,] two 1x1 QConvs C -> E -> C, residual
         return [((s0[0], shape_of(ins[-3])[0]) + tuple(s0[2:]), DType.INT8)]

@@ -97,6 +97,13 @@ class ReferenceExecutor:
                     if name:
                         local[name] = val
             return [local[node.outputs[0]]]
+        if op in ("Conv", "FusedConvAct", "FusedConvBNAct") and a.get("maxpool"):
+            # backend pool fold: the conv (and its activation), then the max
+            # pool the reference ran as its own host op (ops.py:109-125)
+            mp = a["maxpool"]
+            y = act(a.get("activation"), ops.conv(ins[0], ins[1], opt(2), **_conv_kw(a)), a)
+            return [ops.maxpool(y, kernel=mp["kernel_shape"], strides=mp["strides"], pads=mp["pads"],
+                                dilations=[1, 1], auto_pad="NOTSET", ceil_mode=0)]
         if op in ("FusedConvAct", "FusedConvBNAct"):
             return [act(a.get("activation"), ops.conv(ins[0], ins[1], opt(2), **_conv_kw(a)), a)]
         if op == "FusedGemmAct":

@@ -303,6 +303,43 @@ def test_conv_small_channels_residual(hip_ctx):
     assert_close("z", got["z"], want["z"])
 
 
+CONV_POOL_CASES = [   # (N, C, H, W, OC, K, S, P, activation, bias)
+    (2, 3, 32, 32, 20, 7, 2, 3, "Relu", True),      # OC not a multiple of 16: masked channels
+    (1, 3, 64, 64, 64, 7, 2, 3, "Relu", True),      # two column blocks: the carried column
+    (1, 2, 32, 32, 16, 3, 1, 1, "Clip", False),
+    (1, 1, 64, 32, 40, 5, 2, 2, None, True),
+    (3, 3, 224, 224, 64, 7, 2, 3, "Relu", True),    # the ResNet stem's width, bands of 7 rows
+]
+
+
+@pytest.mark.parametrize("case", CONV_POOL_CASES, ids=lambda c: "x".join(map(str, c[:8])))
+def test_conv_pool_fused(case, hip_ctx, monkeypatch):
+    """The small-channel conv with the 3x3 stride-2 max pool after it in one
+    launch, against the oracle's conv -> activation -> pool on the unfolded
+    graph (rtol 1e-4 / atol 1e-5), and equal to a repeat run. The CU count is
+    lowered so that small shapes take the fused kernel (the fold wants a band
+    of pooled rows per CU)."""
+    import mdlc_amd.codegen.schedule as S
+    from mdlc_amd.codegen.hip.hip_executor import HipExecutor
+    from mdlc_amd.compiler import compile_graph
+    from oracle.reference import run_reference
+    from test_conv_pool import _graph as conv_pool_graph
+
+    monkeypatch.setattr(S, "CUS", 2)
+    n, c_in, h, w, oc, k, s, p, act, bias = case
+    g, feeds = conv_pool_graph(n, c_in, h, w, oc, k, s, p, act=act, bias=bias)
+    c = compile_graph(g.clone(), feeds=feeds)
+    assert [l.kind for l in c.module.plan] == ["conv_pool"]
+    ex = HipExecutor(c.module, hip_ctx)
+    try:
+        z1 = ex.run(feeds)["outputs"]["z"]
+        z2 = ex.run(feeds)["outputs"]["z"]
+    finally:
+        ex.close()
+    assert_close("z", z1, run_reference(g, feeds)["z"])
+    np.testing.assert_array_equal(z1, z2)
+
+
 @pytest.mark.parametrize("mode", ["implicit", "im2col"])
 @pytest.mark.parametrize("sk", [2, 4, 5])
 @pytest.mark.parametrize("case", [CONV_CASES[2], CONV_CASES[4], CONV_CASES[6]],
