@@ -392,8 +392,11 @@ class Int8LoweringMixin:
         kname = "qgap_wg" if per_image else "qgap"
         self._kernel(kname, lambda i: T.qgap_kernel(kname, per_image))
         self.layout[node.outputs[0]] = "NHWC"
-        grid = n if per_image else -(-(n * c) // 256)
-        self.plan.append(Launch("qgap", kname, [x], [node.outputs[0]], (grid, 1, 1),
+        # per image, blocks of 64 channels where they divide C (16 channel
+        # quads x 16 pixel lanes a workgroup), else all of C
+        cblocks = c // 64 if per_image and c % 64 == 0 else 1
+        grid = (n, cblocks, 1) if per_image else (-(-(n * c) // 256), 1, 1)
+        self.plan.append(Launch("qgap", kname, [x], [node.outputs[0]], grid,
                                 (256, 1, 1), {"N": n, "C": c, "HW": h * w,
                                               "m": float(node.attrs["mult"]), "node": node,
                                               "bytes": n * c * (h * w + 1)}))

@@ -1029,27 +1029,29 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   }, [] {});
 }
 
-// The same pool with one workgroup per image for C % 4 == 0, C <= 1024:
-// thread t sums channels [4g, 4g+4) (g = t % (C/4)) over the pixels
-// p = t / (C/4) (mod R), R = 256 / (C/4), with 32-bit loads coalesced along
-// the channels; the R partial sums of each channel meet in LDS. Integer
-// sums are exact, so the result equals qgap_nhwc's.
+// The same pool with one workgroup per image (blockIdx.x) and block of CB =
+// C / gridDim.y channels (blockIdx.y; CB % 4 == 0, CB <= 1024): thread t sums
+// channels c0 + [4g, 4g+4) (g = t % (CB/4)) over the pixels p = t / (CB/4)
+// (mod R), R = 256 / (CB/4), with 32-bit loads coalesced along the channels;
+// the R partial sums of each channel meet in LDS. Integer sums are exact, so
+// the result equals qgap_nhwc's.
 __device__ __forceinline__ void qgap_nhwc_wg(const i8* __restrict__ x, i8* __restrict__ y, int C,
                                              int HW, float m) {
   __shared__ int part[1024];
   const int n = blockIdx.x;
-  const int G = C / 4, R = 256 / G;
+  const int CB = C / (int)gridDim.y, c0 = (int)blockIdx.y * CB;
+  const int G = CB / 4, R = 256 / G;
   const int t = threadIdx.x, gi = t % G, r = t / G;
   int s0 = 0, s1 = 0, s2 = 0, s3 = 0;
   if (r < R) {
-    const i8* xp = x + (size_t)n * HW * C + 4 * gi;
+    const i8* xp = x + (size_t)n * HW * C + c0 + 4 * gi;
     for (int p = r; p < HW; p += R) {
       union { int w; i8 b[4]; } v;
       v.w = *reinterpret_cast<const int*>(xp + (size_t)p * C);
       s0 += v.b[0]; s1 += v.b[1]; s2 += v.b[2]; s3 += v.b[3];
     }
   }
-  for (int c = t; c < C; c += 256) part[c] = 0;
+  for (int c = t; c < CB; c += 256) part[c] = 0;
   __syncthreads();
   if (r < R) {
     atomicAdd(&part[4 * gi], s0);
@@ -1058,7 +1060,7 @@ __device__ __forceinline__ void qgap_nhwc_wg(const i8* __restrict__ x, i8* __res
     atomicAdd(&part[4 * gi + 3], s3);
   }
   __syncthreads();
-  for (int c = t; c < C; c += 256) y[(size_t)n * C + c] = requant(part[c], m, -127.0f);
+  for (int c = t; c < CB; c += 256) y[(size_t)n * C + c0 + c] = requant(part[c], m, -127.0f);
 }
 
 // Dequantize: float(q) * s; an NHWC 4-D input is written back as NCHW.

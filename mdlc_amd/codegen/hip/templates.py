@@ -716,7 +716,8 @@ def qlut_kernel(name: str = "qlut") -> tuple:
 
 
 def qgap_kernel(name: str = "qgap", per_image: bool = False) -> tuple:
-    """int8 global average pool; ``per_image``: one workgroup per image (C % 4 == 0).
+    """int8 global average pool; ``per_image``: one workgroup per image and
+    channel block (grid y: C / block channels; C % 4 == 0).
     ABI: (x, y, int N, int C, int HW, float m)."""
     body = "mdlc::qgap_nhwc_wg(x, y, C, HW, m);" if per_image else "mdlc::qgap_nhwc(x, y, N, C, HW, m);"
     return name, (

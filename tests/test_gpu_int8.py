@@ -141,11 +141,14 @@ def test_qgemm_bit_exact(sched, out, hip_ctx):
     np.testing.assert_array_equal(got["y"], want["y"])
 
 
-def test_qadd_qlut_qgap(hip_ctx):
+@pytest.mark.parametrize("c", [32, 192])
+def test_qadd_qlut_qgap(c, hip_ctx):
+    """Add, lookup and the pool, bit-exact; C = 192 spreads each image's pool
+    over three 64-channel workgroups."""
     rng = np.random.default_rng(5)
     b = GraphBuilder("q")
-    b.input("x", (2, 32, 7, 7))
-    b.input("z", (2, 32, 7, 7))
+    b.input("x", (2, c, 7, 7))
+    b.input("z", (2, c, 7, 7))
     b.node("QuantizeLinear", ["x"], "xq", inv_scale=10.0)
     b.node("QuantizeLinear", ["z"], "zq", inv_scale=30.0)
     b.node("QAdd", ["xq", "zq"], "s", ma=0.75, mb=0.5)
@@ -155,9 +158,11 @@ def test_qadd_qlut_qgap(hip_ctx):
     b.node("Flatten", ["p"], "f", axis=1)
     for o in ("s", "l", "f"):
         b.output(o)
-    feeds = {"x": (rng.standard_normal((2, 32, 7, 7)) * 5).astype(np.float32),
-             "z": (rng.standard_normal((2, 32, 7, 7)) * 5).astype(np.float32)}
-    _, got, want = device_run(b.graph(), feeds, ctx=hip_ctx, all_tensors=True)
+    feeds = {"x": (rng.standard_normal((2, c, 7, 7)) * 5).astype(np.float32),
+             "z": (rng.standard_normal((2, c, 7, 7)) * 5).astype(np.float32)}
+    cm, got, want = device_run(b.graph(), feeds, ctx=hip_ctx, all_tensors=True)
+    (gap,) = [l for l in cm.module.plan if l.kind == "qgap"]
+    assert gap.grid[1] == (c // 64 if c % 64 == 0 else 1)
     for name in want:
         if name in got:
             np.testing.assert_array_equal(got[name], want[name], err_msg=name)
