@@ -17,9 +17,14 @@ from mdlc_amd.codegen.hip import templates as T
 from mdlc_amd.codegen.hip.plan import Launch, round16
 from mdlc_amd.codegen.schedule import (
     LDS_LIMIT, default_qdw_schedule, default_qschedule, qdw_valid, qmlp_latency_form, qmlp_layout,
-    qmlp_lds_bytes, qsched_valid,
+    qconv_first_band, qmlp_lds_bytes, qsched_valid,
 )
 from mdlc_amd.passes.shape_inference import conv_geometry
+
+
+def wdev_bytes(nob: int, ns: int) -> int:
+    """Bytes of the first int8 conv's packed MFMA weight fragments."""
+    return nob * ns * 64 * 16
 
 
 class Int8LoweringMixin:
@@ -105,23 +110,30 @@ class Int8LoweringMixin:
                                               "bytes": 5 * total}))
 
     def _lower_qconv_first(self, g, node):
-        """A QConv that quantizes its own float32 NCHW input (few channels):
-        one thread per output pixel, v_dot4 over the packed window."""
+        """A QConv that quantizes its own float32 NCHW input (at most four
+        channels): one workgroup per band of output rows quantizes the band's
+        input into LDS once and forms the outputs on 16x16x64 int8 MFMAs."""
         x, w, b, m = node.inputs[:4]
         geo = conv_geometry(node, self._shape(g, x), self._shape(g, w))
         OC, C, KH, KW = geo["OC"], geo["C"], geo["KH"], geo["KW"]
-        K = C * KH * KW
-        if geo["group"] != 1 or K > 64 or OC % 4 or OC > 64 or geo["DH"] != 1 or geo["DW"] != 1:
+        band = None
+        if geo["group"] == 1 and geo["DH"] == 1 and geo["DW"] == 1:
+            band = qconv_first_band(C, KH, KW, geo["SH"], geo["SW"], geo["N"], geo["OH"], geo["OW"], OC)
+        if band is None:
             raise NotImplementedError("HIP codegen: fused input quantization needs a small "
-                                      "ungrouped conv (C*KH*KW <= 64, OC <= 64 and % 4 == 0, "
-                                      "no dilation)")
+                                      "ungrouped conv (C <= 4, KH*KW <= 32, OC <= 64 and % 4 == 0, "
+                                      "no dilation, a band of output rows within the LDS)")
         self._check_dtype(g, x, "float32")
         y = node.outputs[0]
         self.layout[y] = "NHWC"
-        kq = -(-K // 4)
-        wp = np.zeros((OC, kq * 4), np.int8)
-        wp[:, :K] = np.asarray(g.initializers[w], np.int8).reshape(OC, K)     # k = (c, kh, kw)
-        wdev = self._pack_raw(f"{w}__dev_dot4", wp.view(np.int32).copy())
+        # row operand fragments: [block][step][lane 16 lk + li][word j] = the C
+        # weight bytes of output channel 16 block + li at tap 16 step + 4 lk + j
+        T_, nob, ns = KH * KW, -(-OC // 16), -(-KH * KW // 16)
+        wq = np.asarray(g.initializers[w], np.int8).reshape(OC, C, T_).transpose(0, 2, 1)
+        wb = np.zeros((16 * nob, 16 * ns, 4), np.int8)
+        wb[:OC, :T_, :C] = wq
+        words = wb.view(np.int32).reshape(nob, 16, ns, 4, 4)            # [ob][li][s][lk][j]
+        wdev = self._pack_raw(f"{w}__dev_qfirst", np.ascontiguousarray(words.transpose(0, 2, 3, 1, 4)))
         epi, tab = 0, None
         kind = node.attrs.get("epilogue")
         if kind == "lut":
@@ -132,18 +144,20 @@ class Int8LoweringMixin:
             raise NotImplementedError(f"HIP codegen: epilogue {kind!r} on a conv that quantizes its input")
         lo = 0 if node.attrs.get("activation") == "Relu" else -127
         win = (KH, KW, geo["SH"], geo["SW"], geo["PT"], geo["PL"])
-        kname = self._kernel(("qconv_first", C, win, OC, lo, epi), lambda i: T.qconv_first_kernel(
-            f"qconv_first_c{C}_{'x'.join(map(str, win))}_oc{OC}{'_lut' if epi else ''}_{i}", C, win, OC,
-            lo=lo, epi=epi))
+        dims = (geo["H"], geo["W"], geo["OH"], geo["OW"])
+        kname = self._kernel(("qconv_first", C, win, OC, lo, epi, dims, band), lambda i: T.qconv_first_kernel(
+            f"qconv_first_c{C}_{'x'.join(map(str, win))}_oc{OC}_R{band}{'_lut' if epi else ''}_{i}", C, win,
+            OC, dims, band, lo=lo, epi=epi))
         P = geo["N"] * geo["OH"] * geo["OW"]
-        if P * OC >= 2 ** 31:
-            raise NotImplementedError("HIP codegen: int8 conv output of 2 GiB or more")
+        if P * OC >= 2 ** 31 or 4 * C * geo["H"] * geo["W"] >= 2 ** 31:
+            raise NotImplementedError("HIP codegen: int8 conv tensors of 2 GiB or more")
         ins = [x, wdev, self._padded_vector(g, b, OC, np.int32), self._padded_vector(g, m, OC, np.float32)]
+        grid = (geo["N"] * -(-geo["OH"] // band), 1, 1)
         self.plan.append(Launch(
-            "qconv_first", kname, ins + ([tab] if tab else []), [y], (-(-P // 256), 1, 1), (256, 1, 1),
+            "qconv_first", kname, ins + ([tab] if tab else []), [y], grid, (256, 1, 1),
             {**{k: geo[k] for k in ("N", "H", "W", "OH", "OW")}, "inv_s": float(node.attrs["quantize_input"]),
-             "node": node, "ops": 2 * P * OC * K,
-             "bytes": 4 * geo["N"] * C * geo["H"] * geo["W"] + P * OC + OC * (kq * 4 + 8)}))
+             "node": node, "band": band, "ops": 2 * P * OC * C * KH * KW,
+             "bytes": 4 * geo["N"] * C * geo["H"] * geo["W"] + P * OC + wdev_bytes(nob, ns) + OC * 8}))
 
     def _lower_qconv(self, g, node):
         if node.attrs.get("quantize_input") is not None:

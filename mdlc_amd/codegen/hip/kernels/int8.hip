@@ -22,6 +22,11 @@ __device__ __forceinline__ int requant_word(int acc, float m, float lo) {
 __device__ __forceinline__ i8 requant(int acc, float m, float lo) {
   return (i8)requant_word(acc, m, lo);
 }
+// QuantizeLinear's code clamp(rint(v * inv_s), -127, 127) in the low byte,
+// by the same clamp-then-round steps.
+__device__ __forceinline__ int quantize_word(float v, float inv_s) {
+  return __builtin_bit_cast(int, fminf(fmaxf(v * inv_s, -127.0f), 127.0f) + 12582912.0f);
+}
 // The low bytes of four words as one word (byte j from x_j): three byte
 // permutes instead of masks, shifts and ors.
 __device__ __forceinline__ int pack4(int x0, int x1, int x2, int x3) {
@@ -575,74 +580,145 @@ __device__ __forceinline__ void qdwconv_nhwc(const i8* __restrict__ x, const i8*
   }
 }
 
-// First conv of an int8 network fused with its input quantization. x is the
-// float32 NCHW network input with few channels (K = C*KH*KW <= 64). One
-// thread per output pixel quantizes its receptive field with the
-// QuantizeLinear arithmetic (clamp(rint(x * inv_s), -127, 127); zeros where
-// the window leaves the image, as the conv pads the quantized tensor), packs
-// the codes four to a register in k = (c, kh, kw) order and forms every
-// output channel with v_dot4_i32_i8 against the weights, packed the same way
-// ([OC][KP/4], K zero padded to KP) and staged in LDS. Then the usual
-// requant (bias added to the exact int32 sum), an optional fused lookup, and
-// OC channels-last bytes per pixel.
-template <int C, int KH, int KW, int SH, int SW, int PT, int PL, int OC, int LO, int EPI>
+// First conv of an int8 network fused with its input quantization, on the
+// matrix cores. x is the float32 NCHW network input with at most four
+// channels; y is int8 channels-last. A workgroup owns a band of R output rows
+// of one image, whose outputs are one contiguous range of y:
+//  1. it quantizes the input rows the band reads into LDS with the
+//     QuantizeLinear arithmetic (clamp(rint(x * inv_s), -127, 127); zeros where
+//     the window leaves the image, as the conv pads the quantized tensor), one
+//     word per input pixel holding its C codes (the bytes past C zero), so
+//     every input value is read from HBM and quantized once;
+//  2. v_mfma_i32_16x16x64_i8 forms 16 output channels x 16 output pixels a
+//     step. The row operand is the weights (lane 16 lk + li: output channel li
+//     of the block, taps 16 s + 4 lk .. 16 s + 4 lk + 3, one word per tap
+//     packed like the input pixels, zero past the kernel's taps), the column
+//     operand the same taps of pixel li, read from the LDS patch; K runs over
+//     (tap, input channel) with every padding byte zero in the weights;
+//  3. the accumulator holds channels 4 lk + r of pixel li in lane 16 lk + li:
+//     the requant (bias added to the exact int32 sum), the optional lookup,
+//     four channels packed into one word of the band's output, which is
+//     staged in LDS and written with 16-byte stores.
+template <int C, int KH, int KW, int SH, int SW, int PT, int PL, int OC, int LO, int EPI,
+          int H, int W, int OH, int OW, int R>
 __device__ __forceinline__ void qconv_first(const float* __restrict__ x, float inv_s,
-                                            const int* __restrict__ w, const int* __restrict__ bias,
+                                            const intx4* __restrict__ w,
+                                            const int* __restrict__ bias,
                                             const float* __restrict__ mult,
-                                            const i8* __restrict__ table, i8* __restrict__ y,
-                                            int N, int H, int W, int OH, int OW) {
-  constexpr int K = C * KH * KW, KQ = (K + 3) / 4;
-  static_assert(K <= 64 && OC % 4 == 0 && OC <= 64, "small first-layer convs only");
-  __shared__ int ws[OC * KQ];
-  __shared__ int bs[OC];
-  __shared__ float ms[OC];
-  __shared__ i8 tab[256];
-  for (int i = threadIdx.x; i < OC * KQ; i += 256) ws[i] = w[i];
-  if (threadIdx.x < OC) {
-    bs[threadIdx.x] = bias[threadIdx.x];
-    ms[threadIdx.x] = mult[threadIdx.x];
+                                            const i8* __restrict__ table, i8* __restrict__ y) {
+  constexpr int T = KH * KW;                   // taps
+  constexpr int NS = (T + 15) / 16;            // MFMA steps of 16 taps
+  constexpr int NOB = (OC + 15) / 16;          // 16-channel output blocks
+  constexpr int PR = (R - 1) * SH + KH;        // patch rows
+  constexpr int PCW = (OW - 1) * SW + KW;      // patch columns (padding included)
+  constexpr int NE = PR * PCW;                 // patch words
+  constexpr int NP = R * OW;                   // band pixels
+  constexpr int NG = (NP + 15) / 16;           // 16-pixel groups
+  constexpr int BANDS = (OH + R - 1) / R;
+  static_assert(C <= 4 && OC % 4 == 0 && OC <= 64, "first convs with few channels only");
+  static_assert((NE + NP * OC / 4) * 4 + 256 <= 64 * 1024, "band exceeds the LDS budget");
+  __shared__ int patch[NE];
+  __shared__ __attribute__((aligned(16))) int outs[NP * OC / 4];
+  __shared__ unsigned char tab[256];
+  const int n = blockIdx.x / BANDS;
+  const int oh0 = (blockIdx.x - n * BANDS) * R;
+  if (EPI == 1) tab[threadIdx.x] = (unsigned char)table[threadIdx.x];
+
+  // 1. the band's quantized input patch; every load is issued before the first is used
+  {
+    const __amdgpu_buffer_rsrc_t rx = buffer_over(x + (size_t)n * C * H * W, C * H * W * 4);
+    constexpr int NL = (NE + 255) / 256;
+    float v[NL][C];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int e = i * 256 + (int)threadIdx.x;
+      const int pr = e / PCW, pc = e - pr * PCW;
+      const int ih = oh0 * SH - PT + pr, iw = pc - PL;
+      const bool ok = e < NE && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+#pragma unroll
+      for (int c = 0; c < C; ++c)
+        v[i][c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+            rx, ok ? ((c * H + ih) * W + iw) * 4 : kOutside, 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int e = i * 256 + (int)threadIdx.x;
+      int q[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int c = 0; c < C; ++c) q[c] = quantize_word(v[i][c], inv_s);
+      if (e < NE) patch[e] = pack4(q[0], q[1], q[2], q[3]);
+    }
   }
-  if (EPI == 1) tab[threadIdx.x] = table[threadIdx.x];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = lane & 15, lk = lane >> 4;
+  intx4 wf[NOB][NS];
+#pragma unroll
+  for (int ob = 0; ob < NOB; ++ob)
+#pragma unroll
+    for (int s = 0; s < NS; ++s) wf[ob][s] = w[(ob * NS + s) * 64 + lane];
+  int bv[NOB][4];
+  float mv[NOB][4];
+#pragma unroll
+  for (int ob = 0; ob < NOB; ++ob)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int oc = 16 * ob + 4 * lk + r;
+      bv[ob][r] = oc < OC ? bias[oc] : 0;
+      mv[ob][r] = oc < OC ? mult[oc] : 0.f;
+    }
+  // the lane's patch offsets of taps 16 s + 4 lk + j (a tap past the kernel
+  // reads offset 0: its weights are zero)
+  int toff[NS][4];
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 16 * s + 4 * lk + j;
+      toff[s][j] = t < T ? (t / KW) * PCW + t % KW : 0;
+    }
   __syncthreads();
-  const long long p = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (p >= (long long)N * OH * OW) return;
-  const int ow = (int)(p % OW);
-  const int oh = (int)((p / OW) % OH);
-  const int n = (int)(p / ((long long)OW * OH));
-  // the whole window is loaded before any of it is used (a tap outside the
-  // image reads the image's first element and is then replaced by zero), so
-  // the K loads are in flight together instead of one after another
-  const float* xn = x + (size_t)n * C * H * W;
-  float xv[K];
-  bool ok[K];
+
+  // 2 + 3. 16-pixel groups, strided over the waves
+#pragma unroll 1
+  for (int g = wave; g < NG; g += 4) {
+    const int p0 = 16 * g + li;
+    const bool pv = p0 < NP;
+    const int p = pv ? p0 : 0;
+    const int r = p / OW, ow = p - r * OW;
+    const int* pb = patch + r * SH * PCW + ow * SW;
+    intx4 b[NS];
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int c = k / (KH * KW), kh = (k / KW) % KH, kw = k % KW;
-    const int ih = oh * SH - PT + kh, iw = ow * SW - PL + kw;
-    ok[k] = (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
-    xv[k] = xn[ok[k] ? ((size_t)c * H + ih) * W + iw : 0];
+    for (int s = 0; s < NS; ++s) b[s] = intx4{pb[toff[s][0]], pb[toff[s][1]], pb[toff[s][2]], pb[toff[s][3]]};
+#pragma unroll
+    for (int ob = 0; ob < NOB; ++ob) {
+      intx4 acc = {0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < NS; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[ob][s], b[s], acc, 0, 0, 0);
+      if (pv && 16 * ob + 4 * lk < OC) {
+        int c4[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int word = requant_word(acc[j] + bv[ob][j], mv[ob][j], (float)LO);
+          c4[j] = EPI == 1 ? (int)tab[(word & 0xff) ^ 0x80] : word;
+        }
+        outs[(p * OC + 16 * ob + 4 * lk) >> 2] = pack4(c4[0], c4[1], c4[2], c4[3]);
+      }
+    }
   }
-  int q[KQ];
-#pragma unroll
-  for (int j = 0; j < KQ; ++j) q[j] = 0;
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const float r = rintf(xv[k] * inv_s);
-    const int code = ok[k] ? (int)fminf(fmaxf(r, -127.0f), 127.0f) : 0;
-    q[k / 4] |= (code & 0xff) << (8 * (k % 4));
+  __syncthreads();
+
+  // 4. the band's rows of y: one contiguous range
+  const int rows = OH - oh0 < R ? OH - oh0 : R;
+  i8* yb = y + (size_t)(n * OH + oh0) * OW * OC;
+  if constexpr ((OW * OC) % 16 == 0) {
+    const int n16 = rows * (OW * OC / 16);
+    for (int i = threadIdx.x; i < n16; i += 256)
+      reinterpret_cast<intx4*>(yb)[i] = reinterpret_cast<const intx4*>(outs)[i];
+  } else {
+    const int n4 = rows * (OW * OC / 4);
+    for (int i = threadIdx.x; i < n4; i += 256) reinterpret_cast<int*>(yb)[i] = outs[i];
   }
-  union { int w[OC / 4]; i8 b[OC]; } out;
-#pragma unroll
-  for (int oc = 0; oc < OC; ++oc) {
-    int acc = 0;
-#pragma unroll
-    for (int j = 0; j < KQ; ++j) acc = __builtin_amdgcn_sdot4(q[j], ws[oc * KQ + j], acc, false);
-    const i8 code = requant(acc + bs[oc], ms[oc], (float)LO);
-    out.b[oc] = EPI == 1 ? tab[(int)code + 128] : code;
-  }
-  int* yp = reinterpret_cast<int*>(y + p * OC);
-#pragma unroll
-  for (int j = 0; j < OC / 4; ++j) yp[j] = out.w[j];
 }
 
 // Quantize float32 NCHW -> int8 NHWC: clamp(rint(x * inv_s), -127, 127).

@@ -665,19 +665,24 @@ def qmlp_kernel(name: str, C: int, E: int, layout, *, lo1: int, lo2: int,
         f"  mdlc::qmlp_i8<{', '.join(str(v) for v in args)}>(g);\n}}\n")
 
 
-def qconv_first_kernel(name: str, C: int, win: tuple, OC: int, *, lo: int, epi: int) -> tuple:
+def qconv_first_kernel(name: str, C: int, win: tuple, OC: int, dims: tuple, band: int, *, lo: int,
+                       epi: int) -> tuple:
     """First int8 conv fused with its input quantization (float32 NCHW in,
-    int8 NHWC out); ``win`` = (KH, KW, SH, SW, PT, PL).
+    int8 NHWC out) on the matrix cores, one workgroup per band of ``band``
+    output rows of an image; ``win`` = (KH, KW, SH, SW, PT, PL), ``dims`` =
+    (H, W, OH, OW), compiled in. ``w`` is packed [block][step][lane] in 16-byte
+    MFMA fragments.
     ABI: (x, float inv_s, w, bias, mult, table, y, int N, int H, int W, int OH, int OW)."""
-    args = (C,) + tuple(int(v) for v in win) + (OC, int(lo), int(epi))
+    args = (C,) + tuple(int(v) for v in win) + (OC, int(lo), int(epi)) + tuple(int(v) for v in dims) \
+        + (int(band),)
     return name, (
         f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
         "    const float* __restrict__ x, float inv_s, const int* __restrict__ w,\n"
         "    const int* __restrict__ bias, const float* __restrict__ mult,\n"
         "    const signed char* __restrict__ table, signed char* __restrict__ y,\n"
         "    int N, int H, int W, int OH, int OW) {\n"
-        f"  mdlc::qconv_first<{', '.join(str(v) for v in args)}>(x, inv_s, w, bias, mult, table, y,\n"
-        "                                      N, H, W, OH, OW);\n}\n")
+        f"  mdlc::qconv_first<{', '.join(str(v) for v in args)}>(\n"
+        "      x, inv_s, reinterpret_cast<const mdlc::intx4*>(w), bias, mult, table, y);\n}\n")
 
 
 def qdwconv_kernel(name: str, win: tuple, *, cv: int, lo: int) -> tuple:

@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 from gpu_util import assert_close, device_run
+import mdlc_amd.codegen.schedule as S
 from mdlc_amd.codegen.schedule import MfmaSchedule
 from mdlc_amd.tools.build_repvit_int8 import build_repvit_int8, gelu_table, make_input
 from mdlc_amd.tools.graph_builder import GraphBuilder
@@ -410,14 +411,17 @@ def test_int8_gemm_4096_cube_rows_exact(hip_ctx):
 
 @pytest.mark.parametrize("case", [(2, 3, 31, 24, 3, 2, "lut"), (1, 3, 16, 24, 3, 2, None),
                                   (2, 1, 9, 8, 5, 1, "lut"), (1, 4, 12, 16, 3, 1, "relu"),
-                                  (3, 2, 7, 12, 3, 2, None)],
+                                  (3, 2, 7, 12, 3, 2, None), (1, 3, 20, 36, 3, 2, "lut")],
                          ids=lambda c: "n{}c{}hw{}oc{}k{}s{}_{}".format(*c))
-def test_first_conv_quantizes_its_input(case, hip_ctx):
-    """QuantizeLinear folded into a small first QConv (float NCHW in, one
-    thread per output pixel, dot4 over the packed window), with a fused
-    lookup, a ReLU or neither: equal to the oracle and to the separate
-    quantize + conv launches."""
+@pytest.mark.parametrize("cus", [256, 2], ids=["bands1", "bandsR"])
+def test_first_conv_quantizes_its_input(case, cus, hip_ctx, monkeypatch):
+    """QuantizeLinear folded into a small first QConv (float NCHW in, bands of
+    output rows quantized into LDS once, 16x16x64 int8 MFMAs over (tap,
+    channel)), with a fused lookup, a ReLU or neither, single-row and
+    several-row bands (a partial last band included): equal to the oracle
+    and to the separate quantize + conv launches."""
     n, c, hw, oc, k, s, post = case
+    monkeypatch.setattr(S, "CUS", cus)      # few CUs: the shapes take bands of several rows
 
     def graph():
         rng = np.random.default_rng(21)
