@@ -17,7 +17,7 @@ from mdlc_amd.codegen.hip import templates as T
 from mdlc_amd.codegen.hip.plan import Launch, round16
 from mdlc_amd.codegen.schedule import (
     LDS_LIMIT, default_qdw_schedule, default_qschedule, qdw_valid, qmlp_latency_form, qmlp_layout,
-    qconv_first_band, qmlp_lds_bytes, qsched_valid,
+    qconv_first_band, qconv_first_grid, qmlp_lds_bytes, qsched_valid,
 )
 from mdlc_amd.passes.shape_inference import conv_geometry
 
@@ -152,7 +152,7 @@ class Int8LoweringMixin:
         if P * OC >= 2 ** 31 or 4 * C * geo["H"] * geo["W"] >= 2 ** 31:
             raise NotImplementedError("HIP codegen: int8 conv tensors of 2 GiB or more")
         ins = [x, wdev, self._padded_vector(g, b, OC, np.int32), self._padded_vector(g, m, OC, np.float32)]
-        grid = (geo["N"] * -(-geo["OH"] // band), 1, 1)
+        grid = (min(geo["N"] * -(-geo["OH"] // band), qconv_first_grid()), 1, 1)
         self.plan.append(Launch(
             "qconv_first", kname, ins + ([tab] if tab else []), [y], grid, (256, 1, 1),
             {**{k: geo[k] for k in ("N", "H", "W", "OH", "OW")}, "inv_s": float(node.attrs["quantize_input"]),

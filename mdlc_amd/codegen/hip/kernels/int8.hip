@@ -582,30 +582,34 @@ __device__ __forceinline__ void qdwconv_nhwc(const i8* __restrict__ x, const i8*
 
 // First conv of an int8 network fused with its input quantization, on the
 // matrix cores. x is the float32 NCHW network input with at most four
-// channels; y is int8 channels-last. A workgroup owns a band of R output rows
-// of one image, whose outputs are one contiguous range of y:
-//  1. it quantizes the input rows the band reads into LDS with the
-//     QuantizeLinear arithmetic (clamp(rint(x * inv_s), -127, 127); zeros where
-//     the window leaves the image, as the conv pads the quantized tensor), one
-//     word per input pixel holding its C codes (the bytes past C zero), so
-//     every input value is read from HBM and quantized once;
+// channels; y is int8 channels-last. The work is split in bands of R output
+// rows of one image, whose outputs are one contiguous range of y; workgroup
+// b takes bands b, b + gridDim.x, ... and loads the next band's input while
+// it computes the current one. For a band:
+//  1. the input rows it reads are quantized into LDS with the QuantizeLinear
+//     arithmetic (clamp(rint(x * inv_s), -127, 127); zeros where the window
+//     leaves the image, as the conv pads the quantized tensor), one word per
+//     input pixel holding its C codes (the bytes past C zero), so every input
+//     value is read from HBM and quantized once;
 //  2. v_mfma_i32_16x16x64_i8 forms 16 output channels x 16 output pixels a
-//     step. The row operand is the weights (lane 16 lk + li: output channel li
-//     of the block, taps 16 s + 4 lk .. 16 s + 4 lk + 3, one word per tap
+//     step. The row operand is the weights (lane 16 lk + li: output channel
+//     li of the block, taps 16 s + 4 lk .. 16 s + 4 lk + 3, one word per tap
 //     packed like the input pixels, zero past the kernel's taps), the column
 //     operand the same taps of pixel li, read from the LDS patch; K runs over
-//     (tap, input channel) with every padding byte zero in the weights;
+//     (tap, input channel) with every padding byte zero in the weights; the
+//     accumulator starts at the bias, so the sum is the exact int32 acc + bias;
 //  3. the accumulator holds channels 4 lk + r of pixel li in lane 16 lk + li:
-//     the requant (bias added to the exact int32 sum), the optional lookup,
-//     four channels packed into one word of the band's output, which is
-//     staged in LDS and written with 16-byte stores.
+//     the requant, the optional lookup, four channels packed into one word of
+//     the band's output, which is staged in LDS and written with 16-byte
+//     stores.
 template <int C, int KH, int KW, int SH, int SW, int PT, int PL, int OC, int LO, int EPI,
           int H, int W, int OH, int OW, int R>
 __device__ __forceinline__ void qconv_first(const float* __restrict__ x, float inv_s,
                                             const intx4* __restrict__ w,
                                             const int* __restrict__ bias,
                                             const float* __restrict__ mult,
-                                            const i8* __restrict__ table, i8* __restrict__ y) {
+                                            const i8* __restrict__ table, i8* __restrict__ y,
+                                            int N) {
   constexpr int T = KH * KW;                   // taps
   constexpr int NS = (T + 15) / 16;            // MFMA steps of 16 taps
   constexpr int NOB = (OC + 15) / 16;          // 16-channel output blocks
@@ -619,36 +623,54 @@ __device__ __forceinline__ void qconv_first(const float* __restrict__ x, float i
   static_assert((NE + NP * OC / 4) * 4 + 256 <= 64 * 1024, "band exceeds the LDS budget");
   __shared__ int patch[NE];
   __shared__ __attribute__((aligned(16))) int outs[NP * OC / 4];
-  __shared__ unsigned char tab[256];
-  const int n = blockIdx.x / BANDS;
-  const int oh0 = (blockIdx.x - n * BANDS) * R;
-  if (EPI == 1) tab[threadIdx.x] = (unsigned char)table[threadIdx.x];
+  __shared__ unsigned char tab[256];           // tab[b] = table[code b + 128]
+  const int total = N * BANDS;
+  int band = blockIdx.x;
 
-  // 1. the band's quantized input patch; every load is issued before the first is used
-  {
+  // the band's input values of this thread's patch columns (column pc = t +
+  // 256 q of every patch row; every load is issued before the first is
+  // used), and their codes into the LDS patch. A row's offset is uniform
+  // and goes in the scalar offset (clamped into the image); a row or column
+  // outside the image reads zero through a vector offset past the buffer.
+  constexpr int NQ = (PCW + 255) / 256;        // patch columns a thread stages
+  float v[PR][NQ][C];
+  auto load = [&](int b) {
+    const int n = b / BANDS;
+    const int ih0 = (b - n * BANDS) * R * SH - PT;
     const __amdgpu_buffer_rsrc_t rx = buffer_over(x + (size_t)n * C * H * W, C * H * W * 4);
-    constexpr int NL = (NE + 255) / 256;
-    float v[NL][C];
 #pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      const int e = i * 256 + (int)threadIdx.x;
-      const int pr = e / PCW, pc = e - pr * PCW;
-      const int ih = oh0 * SH - PT + pr, iw = pc - PL;
-      const bool ok = e < NE && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+    for (int q = 0; q < NQ; ++q) {
+      const int pc = (int)threadIdx.x + 256 * q;
+      const int iw = pc - PL;
+      const int voff = pc < PCW && (unsigned)iw < (unsigned)W ? iw * 4 : kOutside;
 #pragma unroll
-      for (int c = 0; c < C; ++c)
-        v[i][c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-            rx, ok ? ((c * H + ih) * W + iw) * 4 : kOutside, 0, 0));
+      for (int pr = 0; pr < PR; ++pr) {
+        const int ih = ih0 + pr;
+        const bool row_ok = (unsigned)ih < (unsigned)H;
+        const int vo = row_ok ? voff : kOutside;
+        const int ihc = row_ok ? ih : 0;
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+          v[pr][q][c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+              rx, vo, (c * H + ihc) * W * 4, 0));
+      }
     }
+  };
+  auto stage = [&]() {
 #pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      const int e = i * 256 + (int)threadIdx.x;
-      int q[4] = {0, 0, 0, 0};
+    for (int q = 0; q < NQ; ++q) {
+      const int pc = (int)threadIdx.x + 256 * q;
 #pragma unroll
-      for (int c = 0; c < C; ++c) q[c] = quantize_word(v[i][c], inv_s);
-      if (e < NE) patch[e] = pack4(q[0], q[1], q[2], q[3]);
+      for (int pr = 0; pr < PR; ++pr) {
+        int qc[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < C; ++c) qc[c] = quantize_word(v[pr][q][c], inv_s);
+        if (pc < PCW) patch[pr * PCW + pc] = pack4(qc[0], qc[1], qc[2], qc[3]);
+      }
     }
-  }
+  };
+  load(band);
+  if (EPI == 1) tab[threadIdx.x] = (unsigned char)table[threadIdx.x ^ 0x80];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int li = lane & 15, lk = lane >> 4;
@@ -657,7 +679,7 @@ __device__ __forceinline__ void qconv_first(const float* __restrict__ x, float i
   for (int ob = 0; ob < NOB; ++ob)
 #pragma unroll
     for (int s = 0; s < NS; ++s) wf[ob][s] = w[(ob * NS + s) * 64 + lane];
-  int bv[NOB][4];
+  intx4 bv[NOB];
   float mv[NOB][4];
 #pragma unroll
   for (int ob = 0; ob < NOB; ++ob)
@@ -677,47 +699,60 @@ __device__ __forceinline__ void qconv_first(const float* __restrict__ x, float i
       const int t = 16 * s + 4 * lk + j;
       toff[s][j] = t < T ? (t / KW) * PCW + t % KW : 0;
     }
+  stage();
   __syncthreads();
 
-  // 2 + 3. 16-pixel groups, strided over the waves
 #pragma unroll 1
-  for (int g = wave; g < NG; g += 4) {
-    const int p0 = 16 * g + li;
-    const bool pv = p0 < NP;
-    const int p = pv ? p0 : 0;
-    const int r = p / OW, ow = p - r * OW;
-    const int* pb = patch + r * SH * PCW + ow * SW;
-    intx4 b[NS];
+  for (; band < total; band += gridDim.x) {
+    const int next = band + gridDim.x;
+    if (next < total) load(next);            // in flight while this band computes
+
+    // 2 + 3. 16-pixel groups, strided over the waves
+#pragma unroll 1
+    for (int g = wave; g < NG; g += 4) {
+      const int p0 = 16 * g + li;
+      const bool pv = p0 < NP;
+      const int p = pv ? p0 : 0;
+      const int r = p / OW, ow = p - r * OW;
+      const int* pb = patch + r * SH * PCW + ow * SW;
+      intx4 b[NS];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) b[s] = intx4{pb[toff[s][0]], pb[toff[s][1]], pb[toff[s][2]], pb[toff[s][3]]};
+      for (int s = 0; s < NS; ++s)
+        b[s] = intx4{pb[toff[s][0]], pb[toff[s][1]], pb[toff[s][2]], pb[toff[s][3]]};
 #pragma unroll
-    for (int ob = 0; ob < NOB; ++ob) {
-      intx4 acc = {0, 0, 0, 0};
+      for (int ob = 0; ob < NOB; ++ob) {
+        intx4 acc = bv[ob];
 #pragma unroll
-      for (int s = 0; s < NS; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[ob][s], b[s], acc, 0, 0, 0);
-      if (pv && 16 * ob + 4 * lk < OC) {
-        int c4[4];
+        for (int s = 0; s < NS; ++s)
+          acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[ob][s], b[s], acc, 0, 0, 0);
+        if (pv && 16 * ob + 4 * lk < OC) {
+          int c4[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int word = requant_word(acc[j] + bv[ob][j], mv[ob][j], (float)LO);
-          c4[j] = EPI == 1 ? (int)tab[(word & 0xff) ^ 0x80] : word;
+          for (int j = 0; j < 4; ++j) {
+            const int word = requant_word(acc[j], mv[ob][j], (float)LO);
+            c4[j] = EPI == 1 ? (int)tab[word & 0xff] : word;
+          }
+          outs[(p * OC + 16 * ob + 4 * lk) >> 2] = pack4(c4[0], c4[1], c4[2], c4[3]);
         }
-        outs[(p * OC + 16 * ob + 4 * lk) >> 2] = pack4(c4[0], c4[1], c4[2], c4[3]);
       }
     }
-  }
-  __syncthreads();
+    __syncthreads();
 
-  // 4. the band's rows of y: one contiguous range
-  const int rows = OH - oh0 < R ? OH - oh0 : R;
-  i8* yb = y + (size_t)(n * OH + oh0) * OW * OC;
-  if constexpr ((OW * OC) % 16 == 0) {
-    const int n16 = rows * (OW * OC / 16);
-    for (int i = threadIdx.x; i < n16; i += 256)
-      reinterpret_cast<intx4*>(yb)[i] = reinterpret_cast<const intx4*>(outs)[i];
-  } else {
-    const int n4 = rows * (OW * OC / 4);
-    for (int i = threadIdx.x; i < n4; i += 256) reinterpret_cast<int*>(yb)[i] = outs[i];
+    // 4. the band's rows of y: one contiguous range
+    const int n = band / BANDS;
+    const int oh0 = (band - n * BANDS) * R;
+    const int rows = OH - oh0 < R ? OH - oh0 : R;
+    i8* yb = y + (size_t)(n * OH + oh0) * OW * OC;
+    if constexpr ((OW * OC) % 16 == 0) {
+      const int n16 = rows * (OW * OC / 16);
+      for (int i = threadIdx.x; i < n16; i += 256)
+        reinterpret_cast<intx4*>(yb)[i] = reinterpret_cast<const intx4*>(outs)[i];
+    } else {
+      const int n4 = rows * (OW * OC / 4);
+      for (int i = threadIdx.x; i < n4; i += 256) reinterpret_cast<int*>(yb)[i] = outs[i];
+    }
+    if (next < total) stage();               // every wave has read the patch (barrier above)
+    __syncthreads();
   }
 }
 

@@ -668,10 +668,10 @@ def qmlp_kernel(name: str, C: int, E: int, layout, *, lo1: int, lo2: int,
 def qconv_first_kernel(name: str, C: int, win: tuple, OC: int, dims: tuple, band: int, *, lo: int,
                        epi: int) -> tuple:
     """First int8 conv fused with its input quantization (float32 NCHW in,
-    int8 NHWC out) on the matrix cores, one workgroup per band of ``band``
-    output rows of an image; ``win`` = (KH, KW, SH, SW, PT, PL), ``dims`` =
-    (H, W, OH, OW), compiled in. ``w`` is packed [block][step][lane] in 16-byte
-    MFMA fragments.
+    int8 NHWC out) on the matrix cores, in bands of ``band`` output rows of
+    an image (workgroup b takes bands b, b + gridDim.x, ...); ``win`` = (KH,
+    KW, SH, SW, PT, PL), ``dims`` = (H, W, OH, OW), compiled in. ``w`` is
+    packed [block][step][lane] in 16-byte MFMA fragments.
     ABI: (x, float inv_s, w, bias, mult, table, y, int N, int H, int W, int OH, int OW)."""
     args = (C,) + tuple(int(v) for v in win) + (OC, int(lo), int(epi)) + tuple(int(v) for v in dims) \
         + (int(band),)
@@ -682,7 +682,7 @@ def qconv_first_kernel(name: str, C: int, win: tuple, OC: int, dims: tuple, band
         "    const signed char* __restrict__ table, signed char* __restrict__ y,\n"
         "    int N, int H, int W, int OH, int OW) {\n"
         f"  mdlc::qconv_first<{', '.join(str(v) for v in args)}>(\n"
-        "      x, inv_s, reinterpret_cast<const mdlc::intx4*>(w), bias, mult, table, y);\n}\n")
+        "      x, inv_s, reinterpret_cast<const mdlc::intx4*>(w), bias, mult, table, y, N);\n}\n")
 
 
 def qdwconv_kernel(name: str, win: tuple, *, cv: int, lo: int) -> tuple:

@@ -476,6 +476,7 @@ def conv_pool_band(C: int, KH: int, KW: int, SH: int, SW: int, DH: int, DW: int,
 QFIRST_LDS = 64 * 1024    # LDS of a first int8 conv's band: quantized patch + staged output
 QFIRST_MAX_TAPS = 32      # two 16-tap MFMA steps
 QFIRST_MAX_LOADS = 64     # input floats a thread holds while staging the patch
+QFIRST_WG_PER_CU = 4      # workgroups of the first int8 conv a CU runs at once
 
 
 def qconv_first_band(C: int, KH: int, KW: int, SH: int, SW: int, N: int, OH: int, OW: int,
@@ -483,8 +484,8 @@ def qconv_first_band(C: int, KH: int, KW: int, SH: int, SW: int, N: int, OH: int
     """Output rows per workgroup of the first int8 conv with its input
     quantization: the largest of 8, 4, 2, 1 whose band (quantized patch of
     (R-1)*SH + KH input rows, staged R x OW x OC output bytes, lookup table)
-    fits QFIRST_LDS and whose grid still has two workgroups a CU; the
-    smallest that fits where none has. None when the kernel does not apply:
+    fits QFIRST_LDS and which still gives QFIRST_WG_PER_CU bands a CU; the
+    smallest that fits where none does. None when the kernel does not apply:
     more than four input channels, more than QFIRST_MAX_TAPS taps, OC above
     64 or not a multiple of 4, or no band fits."""
     if C > 4 or KH * KW > QFIRST_MAX_TAPS or OC > 64 or OC % 4 or OW <= 0 or OH <= 0:
@@ -493,15 +494,25 @@ def qconv_first_band(C: int, KH: int, KW: int, SH: int, SW: int, N: int, OH: int
     fits = []
     for R in (8, 4, 2, 1):
         words = ((R - 1) * SH + KH) * PCW
-        if (words + R * OW * OC // 4) * 4 + 256 <= QFIRST_LDS and -(-words // 256) * C <= QFIRST_MAX_LOADS:
+        rows = (R - 1) * SH + KH
+        if (words + R * OW * OC // 4) * 4 + 256 <= QFIRST_LDS and rows * -(-PCW // 256) * C <= QFIRST_MAX_LOADS:
             fits.append(R)
     if not fits:
         return None
     for R in fits:
-        if N * -(-OH // R) >= 2 * CUS:
+        if N * -(-OH // R) >= QFIRST_WG_PER_CU * CUS:
             return R
     return fits[-1]
 
+
+def qconv_first_grid() -> int:
+    """Workgroups of the first int8 conv at most (larger batches loop over
+    their bands, the next band's input loads in flight under the current
+    band's matrix and epilogue work). On RepViT's stem at batch 32 one band
+    a workgroup (1792 workgroups, all resident at once) measured 8.3 us
+    against 8.9 us for 1024 workgroups and 10.5 us for 512 taking bands in
+    turn, so the cap only bounds the grid of large batches."""
+    return 8 * CUS
 
 # ----- Winograd F(2x2, 3x3) convolution -------------------------------------
 

@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 from gpu_util import assert_close, device_run
+import mdlc_amd.codegen.hip.emit_int8 as emit_int8
 import mdlc_amd.codegen.schedule as S
 from mdlc_amd.codegen.schedule import MfmaSchedule
 from mdlc_amd.tools.build_repvit_int8 import build_repvit_int8, gelu_table, make_input
@@ -413,8 +414,8 @@ def test_int8_gemm_4096_cube_rows_exact(hip_ctx):
                                   (2, 1, 9, 8, 5, 1, "lut"), (1, 4, 12, 16, 3, 1, "relu"),
                                   (3, 2, 7, 12, 3, 2, None), (1, 3, 20, 36, 3, 2, "lut")],
                          ids=lambda c: "n{}c{}hw{}oc{}k{}s{}_{}".format(*c))
-@pytest.mark.parametrize("cus", [256, 2], ids=["bands1", "bandsR"])
-def test_first_conv_quantizes_its_input(case, cus, hip_ctx, monkeypatch):
+@pytest.mark.parametrize("cus,cap", [(256, None), (2, None), (2, 3)], ids=["bands1", "bandsR", "loop"])
+def test_first_conv_quantizes_its_input(case, cus, cap, hip_ctx, monkeypatch):
     """QuantizeLinear folded into a small first QConv (float NCHW in, bands of
     output rows quantized into LDS once, 16x16x64 int8 MFMAs over (tap,
     channel)), with a fused lookup, a ReLU or neither, single-row and
@@ -422,6 +423,8 @@ def test_first_conv_quantizes_its_input(case, cus, hip_ctx, monkeypatch):
     and to the separate quantize + conv launches."""
     n, c, hw, oc, k, s, post = case
     monkeypatch.setattr(S, "CUS", cus)      # few CUs: the shapes take bands of several rows
+    if cap:                                 # three workgroups taking the bands in turn
+        monkeypatch.setattr(emit_int8, "qconv_first_grid", lambda: cap)
 
     def graph():
         rng = np.random.default_rng(21)
@@ -447,6 +450,8 @@ def test_first_conv_quantizes_its_input(case, cus, hip_ctx, monkeypatch):
     g, feeds, out = graph()
     cmod, got, want = device_run(g, feeds, ctx=hip_ctx)
     assert [l.kind for l in cmod.module.plan] == ["qconv_first"]
+    if cap:
+        assert cmod.module.plan[0].grid[0] == cap
     np.testing.assert_array_equal(got[out], want[out])
     g2, _, _ = graph()
     _, got2, want2 = device_run(g2, feeds, ctx=hip_ctx, fuse_int8_epilogues=False)
