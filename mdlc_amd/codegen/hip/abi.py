@@ -19,7 +19,7 @@ from __future__ import annotations
 import re
 from typing import Dict, Sequence
 
-_DECL = re.compile(r'extern "C"\s+__global__\s+(?:__launch_bounds__\(\s*\d+\s*\)\s+)?void\s+'
+_DECL = re.compile(r'extern "C"\s+__global__\s+(?:__launch_bounds__\(\s*\d+\s*(?:,\s*\d+\s*)?\)\s+)?void\s+'
                    r"(\w+)\s*\(([^)]*)\)")
 
 

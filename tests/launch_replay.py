@@ -29,7 +29,7 @@ from mdlc_amd.codegen.hip.hiprtc_runtime import Arg
 BASE = 0x7F3A_1234_5000          # a plausible device address for the arena
 WS_BASE = 0x7F3B_0000_0000       # and for a static workspace
 
-_DECL = re.compile(r'extern "C"\s+__global__\s+(?:__launch_bounds__\(\s*\d+\s*\)\s+)?void\s+'
+_DECL = re.compile(r'extern "C"\s+__global__\s+(?:__launch_bounds__\(\s*\d+\s*(?:,\s*\d+\s*)?\)\s+)?void\s+'
                    r"(\w+)\s*\(([^)]*)\)")
 
 
