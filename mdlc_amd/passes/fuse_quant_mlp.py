@@ -20,7 +20,8 @@ other consumer and is not a graph output; the second conv's residual is the
 first conv's input; and the device kernel has a tiling for the channel
 counts (both multiples of 16, K small enough for its register budget). Run
 after shape inference, it also leaves the pair alone when the weights are
-large next to the rows they serve (see ``MAX_WEIGHT_BYTES_PER_ROW``).
+both large next to the rows they serve and large outright (see
+``MAX_WEIGHT_BYTES_PER_ROW`` and ``MAX_FUSED_WEIGHT_BYTES``).
 """
 
 from __future__ import annotations
@@ -44,10 +45,16 @@ def _pointwise_qconv(graph: Graph, n: Node) -> bool:
 
 
 # Each workgroup of the fused kernel streams both weight matrices for its
-# rows; past this many weight bytes per row of x (2*C*E / M) the two
-# separately tiled launches are faster (measured on MI355X at RepViT's batch
-# 32 shapes: 23.5 B/row fused wins 7.8 vs 14.0 us, 376 B/row loses 20 vs 13.8).
+# rows. The fold fires where those weights are small next to the rows they
+# serve (at most MAX_WEIGHT_BYTES_PER_ROW bytes per row of x, 2*C*E / M) or
+# small outright (at most MAX_FUSED_WEIGHT_BYTES): measured on MI355X at
+# RepViT's shapes, 23.5 B/row (stage 3, batch 32) fused wins 7.8 vs 14.0 us;
+# 376 B/row with 590 KB of weights (stage 4, batch 32) loses 20 vs 13.8 us;
+# stage 3 at batch 1 (147 KB, 752 B/row) wins 8.1-8.5 us against ~15 us for
+# the depthwise conv and the two convs, while stage 4 there (590 KB) loses
+# 25-28 us against ~15.
 MAX_WEIGHT_BYTES_PER_ROW = 64
+MAX_FUSED_WEIGHT_BYTES = 256 * 1024
 
 
 class FuseQuantMlp(Pass):
@@ -78,7 +85,8 @@ class FuseQuantMlp(Pass):
             C, E = w1.shape[1], w1.shape[0]
             info = graph.info(x)
             M = int(np.prod(info.shape)) // C if info is not None and info.shape else None
-            if not self.always and M is not None and 2 * C * E > MAX_WEIGHT_BYTES_PER_ROW * M:
+            if (not self.always and M is not None and 2 * C * E > MAX_WEIGHT_BYTES_PER_ROW * M
+                    and 2 * C * E > MAX_FUSED_WEIGHT_BYTES):
                 continue
             if qmlp_layout(C, E, M or 1) is None:                    # no kernel tiling
                 continue

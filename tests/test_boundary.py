@@ -143,7 +143,7 @@ def test_repvit_int8_module_compiles_and_is_channels_last():
         assert ("quantize" in kinds) != fused and ("qconv_first" in kinds) == fused
         assert ("qlut" in kinds and "qadd" in kinds) != fused
         assert ("qdwconv" in kinds) == (dw == "vector")
-        assert ("qmlp" in kinds) == fused                   # stages 1-2 fold at batch 2
+        assert ("qmlp" in kinds) == fused                   # stages 1-3 fold at batch 2
         assert c.module.fallbacks() == []
         assert all(c.module.device_layout.get(l.outputs[0]) == "NHWC"
                    for l in c.module.plan if (l.kind in ("qdwconv", "qlut", "qadd", "qgemm")

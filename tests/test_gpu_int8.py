@@ -185,7 +185,7 @@ def test_repvit_int8_every_tensor_bit_exact(batch, mode, hip_ctx):
                               int8_depthwise="vector" if mode == "unfused" else "mfma")
     assert c.module.fallbacks() == []
     nq = sum(l.kind == "qmlp" for l in c.module.plan)
-    assert nq == ({2: 6, 32: 21}[batch] if mode == "mlp" else 0)
+    assert nq == (21 if mode == "mlp" else 0)
     nf = sum(l.kind == "qconv_first" for l in c.module.plan)     # stem + its GELU + the quantize
     assert nf == (0 if mode == "unfused" else 1)
     epis = [l.meta.get("epilogue", 0) for l in c.module.plan if l.kind == "qgemm"]

@@ -9,6 +9,7 @@ import numpy as np
 from mdlc_amd.compiler import compile_graph
 from mdlc_amd.ir import verify_graph
 from mdlc_amd.passes.fuse_quant_epilogue import FuseQuantEpilogue
+from mdlc_amd.passes import fuse_quant_mlp
 from mdlc_amd.passes.fuse_quant_mlp import FuseQuantMixer, FuseQuantMlp
 from mdlc_amd.passes.shape_inference import infer_shapes
 from mdlc_amd.tools.build_repvit_int8 import build_repvit_int8, make_input
@@ -110,8 +111,10 @@ def test_add_multipliers_follow_operand_order():
 
 def test_repvit_channel_mixers_fold_into_qmlp():
     """At batch 32 the 21 channel mixers of stages 1-3 become one QMlp each;
-    stage 4's two, whose weights are large next to their 1568 rows, keep
-    their fused-epilogue convs; forced, all 23 fold."""
+    stage 4's two, whose 590 KB of weights are large outright and next to
+    their 1568 rows, keep their fused-epilogue convs; at batch 1 the same 21
+    fold (stage 3's 147 KB of weights are small outright, although large
+    next to its 196 rows); forced, all 23 fold."""
     c = compile_graph(build_repvit_int8(batch=32), feeds={"input": make_input(32)})
     hist = c.graph.op_histogram()
     assert hist["QMlp"] == 21 and "QLut" not in hist and "QAdd" not in hist
@@ -119,6 +122,8 @@ def test_repvit_channel_mixers_fold_into_qmlp():
     assert sum(1 for n in c.graph.nodes if n.op_type == "QMlp" and n.attrs.get("mixer")) == 19
     epis = [n.attrs.get("epilogue") for n in c.graph.nodes if n.op_type == "QConv"]
     assert epis.count("lut") == 3 and epis.count("add") == 2
+    c1 = compile_graph(build_repvit_int8(batch=1), feeds={"input": make_input(1)})
+    assert c1.graph.op_histogram()["QMlp"] == 21
     ca = compile_graph(build_repvit_int8(batch=1), feeds={"input": make_input(1)},
                        fuse_int8_mlp="always")
     assert ca.graph.op_histogram()["QMlp"] == 23
@@ -133,11 +138,11 @@ def test_mlp_fold_equals_unfolded_everywhere():
     feeds = {"input": make_input(2, image=64)}
     cm = compile_graph(_small_repvit(), feeds=feeds)
     ce = compile_graph(_small_repvit(), feeds=feeds, fuse_int8_mlp=False)
-    assert cm.graph.op_histogram()["QMlp"] == 3            # stages 1-2 at this size
+    assert cm.graph.op_histogram()["QMlp"] == 6            # every stage: its weights are small
     a = run_reference(cm.graph, feeds, return_all=True)
     b = run_reference(ce.graph, feeds, return_all=True)
     common = [k for k in a if k in b and k not in cm.graph.initializers]
-    assert len(common) > 20 and "logits" in common
+    assert len(common) > 12 and "logits" in common
     for k in common:
         np.testing.assert_array_equal(a[k], b[k], err_msg=k)
 
@@ -171,7 +176,7 @@ def _mlp(*, k1=1, hidden_use=False, other_residual=False, c=16, e=32):
     return g
 
 
-def test_mlp_fold_conditions():
+def test_mlp_fold_conditions(monkeypatch):
     g = _mlp()
     assert FuseQuantMlp().run(g)
     (node,) = [n for n in g.nodes if n.op_type == "QMlp"]
@@ -182,9 +187,13 @@ def test_mlp_fold_conditions():
     for kw in (dict(k1=3), dict(hidden_use=True), dict(other_residual=True), dict(c=24, e=40)):
         g = _mlp(**kw)
         assert not FuseQuantMlp().run(g), kw
-    # 25 rows against 2 * 64 * 128 weight bytes: only when forced
+    # 25 rows against 2 * 64 * 128 weight bytes (655 a row): folded while the
+    # weights are small outright, else only when forced
+    assert FuseQuantMlp().run(_mlp(c=64, e=128))
+    monkeypatch.setattr(fuse_quant_mlp, "MAX_FUSED_WEIGHT_BYTES", 8 * 1024)
     assert not FuseQuantMlp().run(_mlp(c=64, e=128))
     assert FuseQuantMlp(always=True).run(_mlp(c=64, e=128))
+    assert FuseQuantMlp().run(_mlp(c=16, e=32))            # 41 bytes a row
 
 
 def _mixed(*, stride=1, second_use=False, epilogue=False):
