@@ -172,7 +172,7 @@ def test_qadd_qlut_qgap(c, hip_ctx):
 
 
 @pytest.mark.parametrize("mode", ["mlp", "epilogues", "unfused"])
-@pytest.mark.parametrize("batch", [2, 32])
+@pytest.mark.parametrize("batch", [1, 2, 32])
 def test_repvit_int8_every_tensor_bit_exact(batch, mode, hip_ctx):
     """Every int8 tensor the module materializes, and the logits, equal the
     oracle's — with the channel mixers as fused MLP launches, with the GELU
