@@ -47,6 +47,7 @@ from mdlc_amd.codegen.hip import templates as T
 from mdlc_amd.codegen.hip.emit_int8 import Int8LoweringMixin
 from mdlc_amd.codegen.hip.plan import (LIBRARY_PARTS, QUANT_OPS, HipModule, Launch,  # noqa: F401
                                        library_parts, round4, round16)
+from mdlc_amd.codegen import schedule as schedule_mod
 from mdlc_amd.codegen.schedule import (WINO_BK, WINO_BM, WINO_BN, MfmaSchedule, conv_pool_band,
                                       default_schedule, smallc_fits, smallc_pairs, smallc_tile, split_slices,
                                       unsplit_if_one_slice, wino_fits,
@@ -54,12 +55,14 @@ from mdlc_amd.codegen.schedule import (WINO_BK, WINO_BM, WINO_BN, MfmaSchedule, 
 from mdlc_amd.ir import DType, Graph, Node
 from mdlc_amd.passes.fuse_elementwise import ELEMENTWISE
 from mdlc_amd.passes.shape_inference import conv_geometry
+from mdlc_amd.runtime.memory_planner import plan_memory
 
 ScheduleFn = Callable[[Optional[Node], tuple], MfmaSchedule]
 
 VIEW_OPS = {"Flatten", "Reshape", "Identity", "Squeeze", "Unsqueeze"}
 REDUCE_VEC = 4        # outputs per thread of the split-K reduce where the layout allows (else 1)
 STREAM_K_WGS = 256    # stream-K workgroups: one per CU
+PAIR_MIN_IDLE = 32    # idle CUs a conv's grid must leave for a second conv to share its launch
 SMALLC_WGS = 512      # workgroups stepping through the blocks of the small-channel conv
 
 
@@ -80,14 +83,16 @@ def dw_rows_per_thread(oh: int) -> int:
 class HipCodegen(Int8LoweringMixin):
     def __init__(self, schedule_fn: Optional[ScheduleFn] = None, *, conv_mode: str = "implicit",
                  int8_depthwise: str = "mfma", small_conv: bool = True,
-                 winograd="auto") -> None:
+                 winograd="auto", pair_convs: bool = True) -> None:
         """``int8_depthwise``: "mfma" runs 16-channel-aligned int8 depthwise
         convs as block-diagonal GEMMs on the matrix cores, "vector" keeps
         them on the per-pixel vector kernel. ``small_conv``: convs with few
         input channels take the direct kernel (implicit mode). ``winograd``:
         3x3 stride-1 convs run as Winograd F(2x2, 3x3) (implicit mode): True
         always, "auto" where its grid fills at least half the CUs
-        (``wino_pays``), False never."""
+        (``wino_pays``), False never. ``pair_convs``: two adjacent independent
+        implicit-GEMM convolutions run as one launch where the first leaves
+        CUs idle (``_pair_convs``)."""
         if winograd not in (True, False, "auto"):
             raise ValueError(f"winograd must be True, False or 'auto', not {winograd!r}")
         if conv_mode not in ("implicit", "im2col"):
@@ -103,6 +108,7 @@ class HipCodegen(Int8LoweringMixin):
         self.conv_mode = conv_mode
         self.small_conv = small_conv
         self.winograd = winograd
+        self.pair_convs = pair_convs
         self.kernels: dict = {}
         self.plan: list = []
         self.scratch: dict = {}
@@ -198,9 +204,58 @@ class HipCodegen(Int8LoweringMixin):
                 getattr(self, "_lower_" + op.lower())(g, node)
             else:
                 raise NotImplementedError(f"HIP codegen: no device lowering for {op!r}")
+        if self.pair_convs:
+            self._pair_convs(g)
         lib = library_parts({l.kind for l in self.plan})
         return HipModule(g, self.kernels, self.plan, self.scratch, self.consts, lib,
                          scratch_class=self.scratch_class, device_layout=dict(self.layout))
+
+    def _pair_convs(self, g: Graph) -> None:
+        """Run two adjacent implicit-GEMM convolutions as one launch where the
+        first's grid leaves at least PAIR_MIN_IDLE CUs idle and the second
+        reads nothing the first writes (ResNet's stride-2 conv and its 1x1
+        downsample both read the block input): the first keeps its grid, the
+        idle CUs take the second's tiles in turn (``conv_pair_kernel``). Both
+        are one-slice launches of the same workgroup size, the second's work
+        per idle CU is at most the first's per workgroup, and the memory plan
+        gives no tensor of one a buffer that a tensor of the other uses, so
+        running them at once changes no value (each tile is computed by the
+        same code as before)."""
+        mem = plan_memory(g)
+
+        def bufs(names):
+            return {mem.assignment[e] for e in names if e in mem.assignment}
+
+        def one_slice_conv(l):
+            return (l.kind == "conv" and not l.meta.get("partial") and not l.meta.get("stream_k")
+                    and l.grid[1:] == (1, 1) and l.meta.get("ksplit", 1) == 1)
+
+        cus = schedule_mod.CUS
+        out, i = [], 0
+        while i < len(self.plan):
+            a = self.plan[i]
+            b = self.plan[i + 1] if i + 1 < len(self.plan) else None
+            ok = (b is not None and one_slice_conv(a) and one_slice_conv(b) and a.block == b.block
+                  and cus - a.grid[0] >= PAIR_MIN_IDLE
+                  and not set(b.inputs) & set(a.outputs) and not set(a.inputs) & set(b.outputs)
+                  and not set(a.outputs) & set(b.outputs)
+                  and not bufs(b.outputs) & bufs(a.inputs + a.outputs)
+                  and not bufs(a.outputs) & bufs(b.inputs + b.outputs)
+                  and b.meta.get("flops", 0) * a.grid[0] <= a.meta.get("flops", 0) * (cus - a.grid[0]))
+            if not ok:
+                out.append(a)
+                i += 1
+                continue
+            kname = self._kernel(("conv_pair", a.kernel_name, b.kernel_name), lambda j: T.conv_pair_kernel(
+                f"conv_pair_{j}", (a.kernel_name, self.kernels[a.kernel_name]),
+                (b.kernel_name, self.kernels[b.kernel_name])))
+            meta = {"first": a, "second": b, "g0": a.grid[0], "nb": b.grid[0], "node": a.meta["node"],
+                    "flops": a.meta.get("flops", 0) + b.meta.get("flops", 0),
+                    "bytes": a.meta.get("bytes", 0) + b.meta.get("bytes", 0)}
+            out.append(Launch("conv_pair", kname, a.inputs + b.inputs, a.outputs + b.outputs,
+                              (cus, 1, 1), a.block, meta))
+            i += 2
+        self.plan = out
 
     def _lower_conv(self, g: Graph, node: Node) -> None:
         x, w = node.inputs[0], node.inputs[1]
@@ -1028,6 +1083,6 @@ def wino_pack_filters(u: np.ndarray, OCP: int, CP: int) -> np.ndarray:
 
 def emit_hip_module(graph: Graph, schedule_fn: Optional[ScheduleFn] = None, *,
                     conv_mode: str = "implicit", int8_depthwise: str = "mfma",
-                    small_conv: bool = True, winograd="auto") -> HipModule:
+                    small_conv: bool = True, winograd="auto", pair_convs: bool = True) -> HipModule:
     return HipCodegen(schedule_fn, conv_mode=conv_mode, int8_depthwise=int8_depthwise,
-                      small_conv=small_conv, winograd=winograd).lower(graph)
+                      small_conv=small_conv, winograd=winograd, pair_convs=pair_convs).lower(graph)

@@ -246,25 +246,29 @@ class HipExecutor:
         """Run each launch group on the tensors in ``env`` (e.g. the oracle's
         values of its inputs) and return what each group wrote."""
         got = {}
-        groups: list = []
+        groups: list = []                       # (the nodes a group computes, its launches)
         for i, l in enumerate(self.module.plan):
             node = l.meta.get("node")
-            if groups and groups[-1][0] is node:
+            nodes = ([l.meta["first"].meta["node"], l.meta["second"].meta["node"]]
+                     if l.kind == "conv_pair" else [node])
+            if groups and groups[-1][0][-1] is node and l.kind != "conv_pair":
                 groups[-1][1].append(i)
             else:
-                groups.append((node, [i]))
+                groups.append((nodes, [i]))
         singles = self._singles()
         consts = set(self.module.device_constants) | set(self.module.graph.initializers)
-        for node, idxs in groups:
-            for e in node.real_inputs():
-                if e in env and e not in consts:
-                    self.write(e, env[e])
+        for nodes, idxs in groups:
+            for node in nodes:
+                for e in node.real_inputs():
+                    if e in env and e not in consts:
+                        self.write(e, env[e])
             for i in idxs:
                 self._run_plan(singles[i])
             self.ctx.synchronize()
-            for o in node.outputs:
-                if o:
-                    got[o] = self.read(o)
+            for node in nodes:
+                for o in node.outputs:
+                    if o:
+                        got[o] = self.read(o)
         return got
 
     def profile(self, iters: int = 25) -> list:
@@ -311,6 +315,9 @@ def launch_args(l: Launch, arg_ptr) -> list:
         args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
         args += [I(m[f]) for f in ("M", "N", "K", "lda", "Cin", "H", "W", "OH", "OW", "ldc",
                                    "kchunk")]
+    elif k == "conv_pair":
+        args = launch_args(m["first"], arg_ptr) + launch_args(m["second"], arg_ptr)
+        args += [I(m["g0"]), I(m["nb"])]
     elif k == "conv":
         args = [P(e) for e in l.inputs] + [P(l.outputs[0])]
         args += [I(m["M"]), I(m["N"]), I(m["K"]), I(m["lda"]), I(m["Cin"]), I(m["H"]),

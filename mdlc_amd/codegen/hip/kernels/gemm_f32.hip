@@ -490,7 +490,9 @@ __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0,
   }
 }
 
-// Entry. Without stream-K (SKW == 0) workgroup b owns one (K slice, tile):
+// Entry (``bid`` >= 0 stands in for blockIdx.x, for a launch that runs this
+// GEMM on part of its grid). Without stream-K (SKW == 0) workgroup b owns one
+// (K slice, tile):
 // logical order (slice, n-block, m-block), m fastest, so workgroups sharing a
 // B slab are consecutive and land on the same XCD.
 //
@@ -504,12 +506,12 @@ __device__ __forceinline__ void gemm_f32_tile(const GemmArgs& g, int m0, int n0,
 // K order and applies the epilogue.
 template <int BM, int BN, int BK, int WGM, int WGN, int MS, bool DB, bool VA, int BMODE, int OUT,
           class Epi, class Win, int SKW = 0, int UN = 1>
-__device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
+__device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g, int bid = -1) {
   const int tiles_m = (g.M + BM - 1) / BM;
   const int tiles_n = (g.N + BN - 1) / BN;
   const int tiles = tiles_m * tiles_n;
   if (SKW == 0) {
-    const int t = xcd_remap(blockIdx.x, tiles * g.ksplit);
+    const int t = xcd_remap(bid < 0 ? (int)blockIdx.x : bid, tiles * g.ksplit);
     const int ks = t / tiles;
     const int tt = t - ks * tiles;
     const int kbeg = ks * g.kchunk;
@@ -520,7 +522,7 @@ __device__ __forceinline__ void gemm_f32_mfma(const GemmArgs& g) {
   // One call site for whole tiles and pieces, so that the tile body is
   // inlined once: a whole tile is the step range [tt*KT, (tt+1)*KT).
   const int full = g.ksplit;
-  const int b = blockIdx.x;
+  const int b = bid < 0 ? (int)blockIdx.x : bid;
   const int KT = (g.K + BK - 1) / BK;
   long long it, it1;
   int slot = -1;

@@ -16,6 +16,7 @@ kernel uses the same float32 bits as the NumPy oracle.
 from __future__ import annotations
 
 import os
+import re
 from typing import Optional
 
 from mdlc_amd.codegen.schedule import MfmaSchedule
@@ -258,6 +259,47 @@ def conv_wsplit_kernel(name: str, sched: MfmaSchedule, win: tuple, *, with_bias:
         f"{'true' if split else 'false'}, {winty}, true>(A, B, "
         f"{'bias' if with_bias else 'nullptr'}, C, M, N, K, lda, 0, ldc, kchunk, "
         f"{'res' if residual else 'nullptr'}, Cin, H, W, OH, OW);\n}}\n")
+
+
+_CONV_KERNEL = re.compile(r'extern "C" __global__ __launch_bounds__\((\d+)\) void (\w+)\(\n(.*?)\) \{\n'
+                          r"(.*?)\n\}\n?$", re.S)
+
+
+def conv_pair_kernel(name: str, first: tuple, second: tuple) -> tuple:
+    """One launch of two independent implicit-GEMM convolutions (``first`` and
+    ``second`` are (kernel name, source) as ``gemm_kernel`` made them, one
+    K slice, no stream-K): workgroups below ``g0`` run the first's grid,
+    the others take the second's tiles in turn (t = b - g0, then every
+    gridDim.x - g0), so the second runs on the CUs the first leaves idle.
+    Each body is its kernel's own, parameters renamed with a suffix; the
+    first's workgroup keeps its block index, the second's takes t in its
+    place. The two kernels' epilogue structs come from their own sources.
+    ABI: (first's arguments, second's arguments, int g0, int nb)."""
+    parts = []
+    for suf, (kname, src) in (("_a", first), ("_b", second)):
+        m = _CONV_KERNEL.search(src)
+        if m is None or m.group(2) != kname:
+            raise ValueError(f"{kname}: not a kernel of the implicit-GEMM conv form")
+        params = [p.strip() for p in m.group(3).replace("\n", " ").split(",")]
+        body = m.group(4)
+        if body.count("(g);") != 1 or "ws" in [p.split()[-1] for p in params]:
+            raise ValueError(f"{kname}: not a one-slice conv kernel")
+        names = [p.split()[-1] for p in params]
+        decl = [p[: len(p) - len(n)] + n + suf for p, n in zip(params, names)]
+        for n in sorted(names, key=len, reverse=True):
+            body = re.sub(r"\b" + re.escape(n) + r"\b", n + suf, body)
+        parts.append((int(m.group(1)), decl, body))
+    (nta, da, ba), (ntb, db, bb) = parts
+    if nta != ntb:
+        raise ValueError("paired convolutions must use the same workgroup size")
+    ba = ba.replace("(g);", "(g, (int)blockIdx.x);")
+    bb = bb.replace("(g);", "(g, t);")
+    return name, (
+        f'extern "C" __global__ __launch_bounds__({nta}) void {name}(\n    '
+        + ", ".join(da + db) + ", int g0, int nb) {\n"
+        "  if ((int)blockIdx.x < g0) {\n" + ba + "\n  } else {\n"
+        "    for (int t = (int)blockIdx.x - g0; t < nb; t += (int)gridDim.x - g0) {\n" + bb
+        + "\n    }\n  }\n}\n")
 
 
 def splitk_reduce_kernel(name: str, *, with_bias: bool, bias_mode: str,

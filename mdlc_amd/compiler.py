@@ -86,7 +86,7 @@ def compile_graph(graph: Graph, *, batch: int = 1, feeds: Optional[dict] = None,
                   conv_mode: str = "implicit", fuse_int8_epilogues: bool = True,
                   int8_depthwise: str = "mfma", fuse_residual: bool = True,
                   fuse_int8_mlp=True, small_conv: bool = True, winograd="auto",
-                  fuse_pool: bool = True) -> Compiled:
+                  fuse_pool: bool = True, pair_convs: bool = True) -> Compiled:
     """Optimize, plan and lower ``graph``. The reference pipeline runs first,
     unchanged. Then backend epilogue folds: ``fuse_int8_epilogues`` folds a
     QLut or QAdd into the QConv that feeds it; ``fuse_residual`` folds a
@@ -103,7 +103,9 @@ def compile_graph(graph: Graph, *, batch: int = 1, feeds: Optional[dict] = None,
     runs 3x3 stride-1 convs as Winograd F(2x2, 3x3) in implicit mode: "auto" where its
     grid fills at least half the CUs, True always, False never (the implicit GEMM).
     ``fuse_pool`` (with ``small_conv`` in implicit mode) folds a 3x3 stride-2 max pool
-    into the small-channel conv that feeds it where every CU gets a band of its rows."""
+    into the small-channel conv that feeds it where every CU gets a band of its rows.
+    ``pair_convs`` runs two adjacent independent implicit-GEMM convs as one launch
+    where the first leaves CUs idle (ResNet's stride-2 conv and its downsample)."""
     original = graph.clone()
     if feeds is None:
         feeds = make_dummy_feeds(graph, batch=batch)
@@ -122,7 +124,7 @@ def compile_graph(graph: Graph, *, batch: int = 1, feeds: Optional[dict] = None,
         PassManager(post, verify=_structural_verifier(verify), history=pm.history).run(graph)
     mem_plan = plan_memory(graph)
     module = emit_hip_module(graph, schedule_fn, conv_mode=conv_mode, int8_depthwise=int8_depthwise,
-                             small_conv=small_conv, winograd=winograd)
+                             small_conv=small_conv, winograd=winograd, pair_convs=pair_convs)
     return Compiled(original, graph, module, mem_plan, pm, feeds)
 
 

@@ -140,6 +140,17 @@ def store_ranges(rep: PlanReplay, launch) -> list:
     """[(pointer parameter, its value, lowest byte, one past the highest
     byte)] the launch's epilogue stores to, as the kernel computes them;
     None for a kernel this replay does not model."""
+    if launch.kind == "conv_pair":
+        # the first conv on workgroups 0 .. g0-1 with their own block indices,
+        # the second's tiles t < nb in turn on the others: each stores what
+        # its own launch would
+        out = []
+        for part in (launch.meta["first"], launch.meta["second"]):
+            r = store_ranges(rep, part)
+            if r is None:
+                return None
+            out += r
+        return out
     src = rep.module.kernels[launch.kernel_name]
     v = rep.kernel_view(launch)
     gx, gy = launch.grid[0], launch.grid[1]
