@@ -97,15 +97,14 @@ __device__ __forceinline__ void qgemm_epilogue(const QGemmArgs& g, Acc& acc, int
   // (MS = 32; for MS = 16 the single group is at lk*4 + j).
   constexpr int NG = MfmaI8<MS>::kAcc / 4;
   const bool vec_ok = (g.ldc & 3) == 0;
-  // The tile's bias and multipliers (and the lookup table) go through LDS:
-  // read from global memory between the output stores, each would wait for
-  // the store before it (the compiler cannot tell them apart from the output).
+  // The tile's multipliers (and the lookup table) go through LDS: read from
+  // global memory between the output stores, each would wait for the store
+  // before it (the compiler cannot tell them apart from the output). The
+  // bias is already in the accumulators (they start at it).
   __shared__ i8 table[EPI == 1 ? 256 : 1];
-  __shared__ int bias_s[BN];
   __shared__ float mult_s[BN];
   for (int i = tid; i < BN; i += NT) {        // the K loop ended with a barrier: LDS is free
     const bool ok = n0 + i < g.N;
-    bias_s[i] = ok ? g.bias[n0 + i] : 0;
     mult_s[i] = ok ? g.mult[n0 + i] : 0.f;
   }
   if (EPI == 1)
@@ -125,7 +124,6 @@ __device__ __forceinline__ void qgemm_epilogue(const QGemmArgs& g, Acc& acc, int
     for (int q = 0; q < NG; ++q) {
       const int col = n0 + wn0 + ni * MS + q * 8 + lk * 4;
       if (col >= g.N) continue;
-      const intx4 bv = *reinterpret_cast<const intx4*>(&bias_s[col - n0]);
       const floatx4 mv = *reinterpret_cast<const floatx4*>(&mult_s[col - n0]);
       const bool full = vec_ok && col + 4 <= g.N;
       // the residual words of all the group's rows before its first store
@@ -146,7 +144,7 @@ __device__ __forceinline__ void qgemm_epilogue(const QGemmArgs& g, Acc& acc, int
           int* cp = static_cast<int*>(g.C) + (size_t)row * g.ldc + col;
           int o[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) o[j] = acc[mi][ni][4 * q + j] + bv[j];
+          for (int j = 0; j < 4; ++j) o[j] = acc[mi][ni][4 * q + j];
           if (full) {
             *reinterpret_cast<intx4*>(cp) = intx4{o[0], o[1], o[2], o[3]};
           } else {
@@ -158,7 +156,7 @@ __device__ __forceinline__ void qgemm_epilogue(const QGemmArgs& g, Acc& acc, int
           float* cp = static_cast<float*>(g.C) + (size_t)row * g.ldc + col;
           float o[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) o[j] = (float)(acc[mi][ni][4 * q + j] + bv[j]) * mv[j];
+          for (int j = 0; j < 4; ++j) o[j] = (float)acc[mi][ni][4 * q + j] * mv[j];
           if (full) {
             *reinterpret_cast<float4*>(cp) = make_float4(o[0], o[1], o[2], o[3]);
           } else {
@@ -183,12 +181,12 @@ __device__ __forceinline__ void qgemm_epilogue(const QGemmArgs& g, Acc& acc, int
           if (EPI == 0) {
             int wq[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) wq[j] = requant_word(acc[mi][ni][4 * q + j] + bv[j], mv[j], (float)LO);
+            for (int j = 0; j < 4; ++j) wq[j] = requant_word(acc[mi][ni][4 * q + j], mv[j], (float)LO);
             o.w = pack4(wq[0], wq[1], wq[2], wq[3]);
           } else {
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-              o.b[j] = finish(requant(acc[mi][ni][4 * q + j] + bv[j], mv[j], (float)LO), r.b[j]);
+              o.b[j] = finish(requant(acc[mi][ni][4 * q + j], mv[j], (float)LO), r.b[j]);
           }
           if (full) {
             *reinterpret_cast<int*>(cp) = o.w;
@@ -386,13 +384,27 @@ __device__ __forceinline__ void qgemm_i8_mfma(const QGemmArgs& g) {
     }
   };
 
+  // The accumulators start at their columns' bias (the epilogue's layout:
+  // acc[mi][ni][4q + j] is column n0 + wn0 + ni*MS + q*8 + lk*4 + j), so the
+  // MFMAs leave the exact int32 acc + bias and the epilogue adds nothing. The
+  // bias is zero padded to a multiple of 16 columns; four columns past that
+  // read zeros through the buffer's range check.
+  constexpr int NG = MfmaI8<MS>::kAcc / 4;
   acc_t acc[MI][NI];
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
+  {
+    const __amdgpu_buffer_rsrc_t rbias = buffer_over(g.bias, (g.N + 15) / 16 * 64);
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
-      for (int r = 0; r < MfmaI8<MS>::kAcc; ++r) acc[mi][ni][r] = 0;
+      for (int q = 0; q < NG; ++q) {
+        const int col = n0 + wn0 + ni * MS + q * 8 + lk * 4;
+        const intx4 bv = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rbias, col * 4, 0, 0));
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[mi][ni][4 * q + j] = bv[j];
+      }
+  }
 
   auto compute = [&](int buf) {
     const i8* as = &As[buf][0];
@@ -977,19 +989,18 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
     for (int u = 0; u < MIXB; ++u) {
       const int t = wave + 4 * (b0 + u);
       if (b0 + u >= TPW || t >= TILES) continue;
-      intx4 acc = intx4{0, 0, 0, 0};
+      // acc[j]: row `row`, channel cb*16 + lk*4 + j, starting at its bias
+      const int c = cbv[u] * 16 + lk * 4;
+      intx4 acc = *reinterpret_cast<const intx4*>(&bds[c]);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         const intx4 w = *reinterpret_cast<const intx4*>(&Wds[(cbv[u] * 16 + li) * WS + s * 64 + lk * 16]);
         acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, a[u][s], acc, 0, 0, 0);
       }
-      // acc[j]: row `row`, channel cb*16 + lk*4 + j
-      const int c = cbv[u] * 16 + lk * 4;
-      const intx4 bv = *reinterpret_cast<const intx4*>(&bds[c]);
       const floatx4 mv = *reinterpret_cast<const floatx4*>(&mds[c]);
       union { int w; i8 b[4]; } o;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o.b[j] = requant(acc[j] + bv[j], mv[j], (float)LOD);
+      for (int j = 0; j < 4; ++j) o.b[j] = requant(acc[j], mv[j], (float)LOD);
       *reinterpret_cast<int*>(&Xs[row[u] * XS + c]) = o.w;
     }
   }
@@ -1012,9 +1023,12 @@ struct QMlpFrags {                   // B fragments of one column chunk, whole K
 template <int WGN, int NI>
 __device__ __forceinline__ int qmlp_col0(int c0) { return c0 + ((threadIdx.x >> 6) % WGN) * NI * 16; }
 
+// The accumulators of a column chunk start at the columns' bias (LDS), so
+// the epilogue gets the exact int32 acc + bias.
 template <int NK, int LDA, int LDB, int NCOLS, int BM, int WGM, int WGN, int NI, class Epi, class Hook>
 __device__ __forceinline__ void qmlp_gemm(const i8* __restrict__ As, const i8* __restrict__ Bg,
-                                          const QMlpFrags<NK, LDB, NI>& first, Epi epi, Hook hook) {
+                                          const QMlpFrags<NK, LDB, NI>& first,
+                                          const int* __restrict__ bias_lds, Epi epi, Hook hook) {
   constexpr int MI = BM / WGM / 16;
   constexpr int CHUNK = WGN * NI * 16;
   static_assert(NCOLS % CHUNK == 0 && (BM / WGM) % 16 == 0, "column chunks must tile the output");
@@ -1029,9 +1043,11 @@ __device__ __forceinline__ void qmlp_gemm(const i8* __restrict__ As, const i8* _
     if (c0 == 0) fr = first; else fr.load(Bg, col0);
     intx4 acc[MI][NI];
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
+    for (int ni = 0; ni < NI; ++ni) {
+      const intx4 bv = *reinterpret_cast<const intx4*>(&bias_lds[col0 + ni * 16 + lk * 4]);
 #pragma unroll
-      for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = intx4{0, 0, 0, 0};
+      for (int mi = 0; mi < MI; ++mi) acc[mi][ni] = bv;
+    }
 #pragma unroll
     for (int s = 0; s < NK / 64; ++s) {
       intx4 af[MI];
@@ -1109,30 +1125,28 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   }
   __syncthreads();
 
-  qmlp_gemm<CP, XS, CP, E, BM, WGM1, WGN1, NI1>(Xs, g.W1, w1f, [&](int r, int n, const intx4& acc,
-                                                                    int, int) {
-    const intx4 bv = *reinterpret_cast<const intx4*>(&b1s[n]);
+  qmlp_gemm<CP, XS, CP, E, BM, WGM1, WGN1, NI1>(Xs, g.W1, w1f, b1s, [&](int r, int n, const intx4& acc,
+                                                                         int, int) {
     const floatx4 mv = *reinterpret_cast<const floatx4*>(&m1s[n]);
     union { int w; i8 b[4]; } o;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o.b[j] = tab[(int)requant(acc[j] + bv[j], mv[j], (float)LO1) + 128];
+    for (int j = 0; j < 4; ++j) o.b[j] = tab[(int)requant(acc[j], mv[j], (float)LO1) + 128];
     *reinterpret_cast<int*>(&Hs[r * HS + n]) = o.w;
   }, [&]() {
     if constexpr (!EW2) w2f.load(g.W2, qmlp_col0<WGN2, NI2>(0));
   });
   __syncthreads();
 
-  qmlp_gemm<EP, HS, EP, C, BM, WGM2, WGN2, NI2>(Hs, g.W2, w2f, [&](int r, int n, const intx4& acc,
-                                                                   int, int) {
+  qmlp_gemm<EP, HS, EP, C, BM, WGM2, WGN2, NI2>(Hs, g.W2, w2f, b2s, [&](int r, int n, const intx4& acc,
+                                                                        int, int) {
     const int m = m0 + r;
     if (m >= g.M) return;
-    const intx4 bv = *reinterpret_cast<const intx4*>(&b2s[n]);
     const floatx4 mv = *reinterpret_cast<const floatx4*>(&m2s[n]);
     union { int w; i8 b[4]; } x, o;
     x.w = *reinterpret_cast<const int*>(&Xs[r * XS + n]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const i8 code = requant(acc[j] + bv[j], mv[j], (float)LO2);
+      const i8 code = requant(acc[j], mv[j], (float)LO2);
       const float v = (float)x.b[j] * g.res_mult + (float)code * g.acc_mult;
       o.b[j] = (i8)(int)fminf(fmaxf(rintf(v), -127.0f), 127.0f);
     }
