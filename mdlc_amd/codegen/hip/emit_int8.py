@@ -323,11 +323,11 @@ class Int8LoweringMixin:
                         self._padded_vector(g, bd, C, np.int32), self._padded_vector(g, md, C, np.float32)]
             ops += 2 * M * C * kh * kw
             wbytes = C * (kh * kw + 8)
-        mixb, ew2 = qmlp_latency_form(C, E, M, lay, mix)
-        kname = self._kernel(("qmlp", C, E, lay, lo1, lo2, mix, mixb, ew2), lambda i: T.qmlp_kernel(
+        mixb, ew2, wregs = qmlp_latency_form(C, E, M, lay, mix)
+        kname = self._kernel(("qmlp", C, E, lay, lo1, lo2, mix, mixb, ew2, wregs), lambda i: T.qmlp_kernel(
             f"qmlp_c{C}_e{E}_{lay.key()}{'_dw%dx%d' % mix[:2] if mix else ''}"
-            f"{'_b%d' % mixb if mixb != 3 else ''}{'_w2' if ew2 else ''}_{i}", C, E, lay,
-            lo1=lo1, lo2=lo2, mixer=mix, mix_batch=mixb, early_w2=ew2))
+            f"{'_b%d' % mixb if mixb != 3 else ''}{'_w2' if ew2 else ''}{'_wr' if wregs else ''}_{i}",
+            C, E, lay, lo1=lo1, lo2=lo2, mixer=mix, mix_batch=mixb, early_w2=ew2, mixer_regs=wregs))
         self.plan.append(Launch(
             "qmlp", kname, ins, [y], (-(-M // lay.BM), 1, 1), (256, 1, 1),
             {"M": M, "C": C, "E": E, "H": H, "W": W, "layout": lay, "node": node, "mixer": bool(mix),

@@ -892,18 +892,25 @@ struct QMlpArgs {
 // the loads of every tile of a batch (its Z fragments, KD / 64 steps each)
 // are issued before the first MFMA, so a batch costs one memory round trip
 // instead of one per tile. The block-diagonal weights, bias and multipliers
-// are read from LDS: the workgroup copies them there once (Wds rows padded
-// to KD + 16 bytes, so the 16 lanes reading one 16-byte column of 16 rows hit
-// distinct banks), the copy's global loads issued ahead of the first batch's
-// Z loads and its LDS stores and barrier after them; every tile used to load
-// its channel block's weights from L2 again.
+// come one of two ways:
+//  * MIXW = 0: the workgroup copies them into LDS once (Wds rows padded to
+//    KD + 16 bytes, so the 16 lanes reading one 16-byte column of 16 rows hit
+//    distinct banks), the copy's global loads issued ahead of the first
+//    batch's Z loads and its LDS stores and barrier after them;
+//  * MIXW = 1 (launches with at most one workgroup per CU, where registers
+//    cost no occupancy): tile u of wave w (t = w + 4u) takes channel block
+//    (w + 4u) % CB, which repeats every P = CB / gcd(4, CB) tiles, so the
+//    wave loads the fragments, bias and multipliers of its P channel blocks
+//    once, straight from global memory into registers (the rows are small and
+//    L2 resident) with the first batch's Z loads, and tile u uses set u % P:
+//    no LDS copy, no barrier for the weights.
 template <int C, int KH, int KW>
 struct QMixDims {
   static constexpr int KD = (KH * KW * 16 + 63) / 64 * 64;   // Wd row (bytes) in global memory
   static constexpr int WS = KD + 16;                          // and in LDS
 };
 
-template <int C, int BM, int XS, int KH, int KW, int PT, int PL, int LOD, int MIXB_MAX>
+template <int C, int BM, int XS, int KH, int KW, int PT, int PL, int LOD, int MIXB_MAX, int MIXW>
 __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ Xs, int m0,
                                            i8* __restrict__ Wds, int* __restrict__ bds,
                                            float* __restrict__ mds) {
@@ -914,7 +921,10 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
   constexpr int TPW = (TILES + 3) / 4;                // tiles per wave
   constexpr int MIXB = TPW < MIXB_MAX ? TPW : MIXB_MAX;  // tiles per batch
   constexpr int WCH = C * KD / 16;                    // 16-byte chunks of Wd
-  constexpr int WPT = (WCH + 255) / 256;
+  constexpr int WPT = MIXW ? 1 : (WCH + 255) / 256;
+  constexpr int CPT = MIXW ? 1 : (C + 255) / 256;
+  constexpr int G4 = CB % 4 == 0 ? 4 : (CB % 2 == 0 ? 2 : 1);   // gcd(4, CB)
+  constexpr int P = !MIXW ? 1 : (CB / G4 < TPW ? CB / G4 : TPW);   // weight sets a wave holds
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -923,20 +933,38 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
   const __amdgpu_buffer_rsrc_t rZ = buffer_over(g.X, g.M * C);
   const __amdgpu_buffer_rsrc_t rW = buffer_over(g.Wd, C * KD);
   intx4 wst[WPT];
-#pragma unroll
-  for (int i = 0; i < WPT; ++i) {
-    const int idx = tid + 256 * i;
-    wst[i] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(
-        rW, idx < WCH ? idx * 16 : kOutside, 0, 0));
-  }
-  constexpr int CPT = (C + 255) / 256;
   int bdv[CPT];
   float mdv[CPT];
+  intx4 wf[P][NS], bf[P];
+  floatx4 mf[P];
+  if constexpr (MIXW) {
+    // set p: channel block (wave + 4p) % CB; lane 16 lk + li holds row cb*16 + li
+    // (taps 4s + lk) and channels cb*16 + 4lk .. +3 of the bias and multipliers
+    const __amdgpu_buffer_rsrc_t rB = buffer_over(g.bd, C * 4);
+    const __amdgpu_buffer_rsrc_t rM = buffer_over(g.md, C * 4);
 #pragma unroll
-  for (int i = 0; i < CPT; ++i) {
-    const int c = tid + 256 * i;
-    bdv[i] = c < C ? g.bd[c] : 0;
-    mdv[i] = c < C ? g.md[c] : 0.f;
+    for (int p = 0; p < P; ++p) {
+      const int cb = (wave + 4 * p) % CB;
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        wf[p][s] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(
+            rW, (cb * 16 + li) * KD + s * 64 + lk * 16, 0, 0));
+      bf[p] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rB, (cb * 16 + lk * 4) * 4, 0, 0));
+      mf[p] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rM, (cb * 16 + lk * 4) * 4, 0, 0));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < WPT; ++i) {
+      const int idx = tid + 256 * i;
+      wst[i] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(
+          rW, idx < WCH ? idx * 16 : kOutside, 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i;
+      bdv[i] = c < C ? g.bd[c] : 0;
+      mdv[i] = c < C ? g.md[c] : 0.f;
+    }
   }
 #pragma unroll
   for (int b0 = 0; b0 < TPW; b0 += MIXB) {
@@ -968,7 +996,7 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
         a[u][s] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rZ, off, 0, 0));
       }
     }
-    if (b0 == 0) {                                    // the weights reach LDS (once)
+    if (!MIXW && b0 == 0) {                           // the weights reach LDS (once)
 #pragma unroll
       for (int i = 0; i < WPT; ++i) {
         const int idx = tid + 256 * i;
@@ -991,13 +1019,15 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
       if (b0 + u >= TPW || t >= TILES) continue;
       // acc[j]: row `row`, channel cb*16 + lk*4 + j, starting at its bias
       const int c = cbv[u] * 16 + lk * 4;
-      intx4 acc = *reinterpret_cast<const intx4*>(&bds[c]);
+      const int p = (b0 + u) % P;                     // compile time: b0 and u are unrolled
+      intx4 acc = MIXW ? bf[p] : *reinterpret_cast<const intx4*>(&bds[c]);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        const intx4 w = *reinterpret_cast<const intx4*>(&Wds[(cbv[u] * 16 + li) * WS + s * 64 + lk * 16]);
+        const intx4 w = MIXW ? wf[p][s]
+                             : *reinterpret_cast<const intx4*>(&Wds[(cbv[u] * 16 + li) * WS + s * 64 + lk * 16]);
         acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, a[u][s], acc, 0, 0, 0);
       }
-      const floatx4 mv = *reinterpret_cast<const floatx4*>(&mds[c]);
+      const floatx4 mv = MIXW ? mf[p] : *reinterpret_cast<const floatx4*>(&mds[c]);
       union { int w; i8 b[4]; } o;
 #pragma unroll
       for (int j = 0; j < 4; ++j) o.b[j] = requant(acc[j], mv[j], (float)LOD);
@@ -1069,12 +1099,14 @@ __device__ __forceinline__ void qmlp_gemm(const i8* __restrict__ As, const i8* _
   }
 }
 
-// MIXB_MAX: the token mixer's tiles per load batch. EW2: fetch the second
+// MIXB_MAX: the token mixer's tiles per load batch; MIXW: its weights in
+// registers (1) or in LDS (0), see qmlp_mixer. EW2: fetch the second
 // GEMM's weight fragments at the start with the first's (registers for both
 // sets; chosen where the launch has at most one workgroup per CU, so the
 // registers cost no occupancy) instead of under the first GEMM's epilogue.
 template <int C, int E, int BM, int WGM1, int WGN1, int NI1, int WGM2, int WGN2, int NI2, int LO1,
-          int LO2, int MIX, int KH, int KW, int PT, int PL, int LOD, int MIXB_MAX = 3, bool EW2 = false>
+          int LO2, int MIX, int KH, int KW, int PT, int PL, int LOD, int MIXB_MAX = 3, bool EW2 = false,
+          int MIXW = 0>
 __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   constexpr int CP = (C + 63) / 64 * 64, EP = (E + 63) / 64 * 64;
   constexpr int XS = CP + 16, HS = EP + 16;    // LDS row strides (bytes)
@@ -1089,10 +1121,12 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   __shared__ __attribute__((aligned(16))) float m1s[E];
   __shared__ __attribute__((aligned(16))) int b2s[C];
   __shared__ __attribute__((aligned(16))) float m2s[C];
-  // the token mixer's weights, bias and multipliers (a byte when there is none)
-  __shared__ __attribute__((aligned(16))) i8 Wds[MIX ? C * QMixDims<C, KH, KW>::WS : 16];
-  __shared__ __attribute__((aligned(16))) int bds[MIX ? C : 4];
-  __shared__ __attribute__((aligned(16))) float mds[MIX ? C : 4];
+  // the token mixer's weights, bias and multipliers in LDS (MIXW = 0; a few
+  // bytes otherwise)
+  constexpr bool kMixLds = MIX && !MIXW;
+  __shared__ __attribute__((aligned(16))) i8 Wds[kMixLds ? C * QMixDims<C, KH, KW>::WS : 16];
+  __shared__ __attribute__((aligned(16))) int bds[kMixLds ? C : 4];
+  __shared__ __attribute__((aligned(16))) float mds[kMixLds ? C : 4];
   const int tid = threadIdx.x;
   const int m0 = blockIdx.x * BM;
 
@@ -1102,7 +1136,7 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   QMlpFrags<EP, EP, NI2> w2f;
   if constexpr (EW2) w2f.load(g.W2, qmlp_col0<WGN2, NI2>(0));
   if constexpr (MIX) {
-    qmlp_mixer<C, BM, XS, KH, KW, PT, PL, LOD, MIXB_MAX>(g, Xs, m0, Wds, bds, mds);
+    qmlp_mixer<C, BM, XS, KH, KW, PT, PL, LOD, MIXB_MAX, MIXW>(g, Xs, m0, Wds, bds, mds);
   } else {
     const __amdgpu_buffer_rsrc_t rX = buffer_over(g.X, g.M * C);
     constexpr int CPR = CP / 16;

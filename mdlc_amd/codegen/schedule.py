@@ -20,6 +20,8 @@ cross product of a few proven values, as in the reference.
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 
 from dataclasses import asdict, dataclass, replace
@@ -390,21 +392,30 @@ def qmlp_layout(C: int, E: int, M: int, bm: Optional[int] = None,
 
 def qmlp_latency_form(C: int, E: int, M: int, layout: QMlpLayout, mixer) -> tuple:
     """(token-mixer tiles per load batch, fetch both weight sets at the
-    start) for the fused MLP. A launch with at most one workgroup per CU has
-    one wave per SIMD, so registers cost no occupancy: every mixer tile of a
-    wave is loaded in one batch (while its fragments fit in 160 registers)
-    and the second GEMM's weights come with the first's, leaving one memory
-    round trip for each. Larger grids keep batches of three and the second
-    weights under the first GEMM's epilogue."""
+    start, token-mixer weights in registers) for the fused MLP. A launch with
+    at most one workgroup per CU has one wave per SIMD, so registers cost no
+    occupancy: every mixer tile of a wave is loaded in one batch (while its
+    fragments fit in 160 registers), the second GEMM's weights come with the
+    first's, and each wave holds the mixer weights of its channel blocks in
+    registers (while they fit in QMIX_REG_MAX) instead of copying them to LDS
+    behind a barrier. Larger grids keep batches of three, the second weights
+    under the first GEMM's epilogue and the mixer weights in LDS."""
     if -(-M // layout.BM) > CUS:
-        return 3, False
+        return 3, False, False
     tiles_per_wave = -(-(layout.BM // 16) * (C // 16) // 4)
+    regs = False
     if mixer:
         steps = -(-mixer[0] * mixer[1] * 16 // 64)
         batch = tiles_per_wave if tiles_per_wave * steps * 8 <= 160 else 3
+        cb = C // 16
+        sets = min(cb // math.gcd(4, cb), max(tiles_per_wave, 1))
+        regs = sets * (4 * steps + 8) <= QMIX_REG_MAX
     else:
         batch = 3
-    return max(1, min(batch, max(tiles_per_wave, 1))), True
+    return max(1, min(batch, max(tiles_per_wave, 1))), True, regs
+
+
+QMIX_REG_MAX = 96         # registers a lane may give the token mixer's weights, bias and multipliers
 
 
 # ----- direct convolution for few input channels ---------------------------

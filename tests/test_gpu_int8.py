@@ -282,15 +282,24 @@ def test_qmlp_bit_exact(case, bm, hip_ctx):
                                   (1, 192, 384, 7, 3, True), (3, 64, 128, 5, 3, False),
                                   (1, 32, 64, 7, 5, True), (2, 16, 32, 4, 3, False)],
                          ids=lambda c: "n{}c{}e{}hw{}k{}{}".format(*c[:5], "_relu" if c[5] else ""))
-def test_qmlp_token_mixer_bit_exact(case, hip_ctx):
+@pytest.mark.parametrize("weights", ["regs", "lds"])
+def test_qmlp_token_mixer_bit_exact(case, weights, hip_ctx, monkeypatch):
     """The depthwise token mixer computed in the fused kernel's prologue:
     image borders (3x3 and 5x5 windows), row tails that cross images, and a
-    ReLU clamp — against the oracle and against the separate launches."""
+    ReLU clamp — against the oracle and against the separate launches, with
+    the mixer's weights in registers (these grids fit one workgroup per CU)
+    and in LDS (the form of grids larger than the chip, forced here)."""
+    import mdlc_amd.codegen.hip.emit_int8 as emit_int8
+
     n, c, e, hw, k, relu = case
+    if weights == "lds":
+        form = emit_int8.qmlp_latency_form
+        monkeypatch.setattr(emit_int8, "qmlp_latency_form", lambda *a: form(*a)[:2] + (False,))
     g, feeds = _mlp_graph(n, c, e, hw, mixer=k, relu_dw=relu, seed=9)
     cmod, got, want = device_run(g, feeds, ctx=hip_ctx, fuse_int8_mlp="always")
     assert [l.kind for l in cmod.module.plan] == ["quantize", "qmlp"]
     assert cmod.module.plan[1].meta["mixer"]
+    assert ("_wr_" in cmod.module.plan[1].kernel_name) == (weights == "regs")
     np.testing.assert_array_equal(got["y"], want["y"])
     v = want["y"].astype(int)
     assert v.std() > 3 and np.mean(np.abs(v) == 127) < 0.5

@@ -134,6 +134,32 @@ def test_repvit_channel_mixers_fold_into_qmlp():
     verify_graph(c.graph)
 
 
+def test_mixer_weights_in_registers_where_grids_fit_the_chip(monkeypatch):
+    """The fused blocks whose launch has at most one workgroup per CU keep
+    their token mixer's weights in registers (stage 3's 196-workgroup grid at
+    batch 32, every mixer block at batch 1); larger grids (stages 1 and 2 at
+    batch 32) and blocks without a mixer keep the LDS form; and a mixer whose
+    weights would need more than QMIX_REG_MAX registers per lane stays in LDS."""
+    import mdlc_amd.codegen.schedule as S
+    from mdlc_amd.codegen.schedule import QMlpLayout, qmlp_latency_form, qmlp_layout
+
+    for batch, want in ((32, {48: 0, 96: 0, 192: 14}), (1, {48: 3, 96: 2, 192: 14})):
+        c = compile_graph(build_repvit_int8(batch=batch), feeds={"input": make_input(batch)})
+        got = {}
+        for l in c.module.plan:
+            if l.kind == "qmlp":
+                got[l.meta["C"]] = got.get(l.meta["C"], 0) + ("_wr_" in l.kernel_name)
+                assert ("_wr_" in l.kernel_name) <= (l.meta["mixer"] and l.grid[0] <= S.CUS)
+        assert got == want
+    lay = qmlp_layout(192, 384, 32 * 14 * 14)
+    assert qmlp_latency_form(192, 384, 32 * 14 * 14, lay, (3, 3, 1, 1, -127))[2]
+    assert not qmlp_latency_form(192, 384, 32 * 14 * 14, lay, None)[2]
+    # 7x7 taps: 13 steps of 64 bytes, three weight sets of 60 registers each
+    assert not qmlp_latency_form(192, 384, 32 * 14 * 14, lay, (7, 7, 3, 3, -127))[2]
+    monkeypatch.setattr(S, "CUS", 64)
+    assert not qmlp_latency_form(192, 384, 32 * 14 * 14, lay, (3, 3, 1, 1, -127))[2]
+
+
 def test_mlp_fold_equals_unfolded_everywhere():
     feeds = {"input": make_input(2, image=64)}
     cm = compile_graph(_small_repvit(), feeds=feeds)
