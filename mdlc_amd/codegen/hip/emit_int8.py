@@ -310,8 +310,9 @@ class Int8LoweringMixin:
             wdarr = np.asarray(g.initializers[wd], np.int8)
             if wdarr.shape != (C, 1, kh, kw) or C % 16:
                 raise NotImplementedError("HIP codegen: QMlp token mixer must be depthwise over C % 16 == 0")
+            # the image size is compiled in (the pixel decomposition divides by it)
             mix = (kh, kw, mixer["pads"][0], mixer["pads"][1],
-                   0 if mixer.get("activation") == "Relu" else -127)
+                   0 if mixer.get("activation") == "Relu" else -127, H, W)
             # block-diagonal [C][KD]: k = (tap, channel within its 16-channel block)
             taps = kh * kw
             kd = -(-taps * 16 // 64) * 64

@@ -910,7 +910,8 @@ struct QMixDims {
   static constexpr int WS = KD + 16;                          // and in LDS
 };
 
-template <int C, int BM, int XS, int KH, int KW, int PT, int PL, int LOD, int MIXB_MAX, int MIXW>
+template <int C, int BM, int XS, int KH, int KW, int PT, int PL, int LOD, int MIXB_MAX, int MIXW,
+          int H, int W>
 __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ Xs, int m0,
                                            i8* __restrict__ Wds, int* __restrict__ bds,
                                            float* __restrict__ mds) {
@@ -927,11 +928,23 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
   constexpr int P = !MIXW ? 1 : (CB / G4 < TPW ? CB / G4 : TPW);   // weight sets a wave holds
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // tiles are wave-uniform: scalar
   const int li = lane & 15, lk = lane >> 4;
-  const int hw = g.H * g.W;
   const __amdgpu_buffer_rsrc_t rZ = buffer_over(g.X, g.M * C);
   const __amdgpu_buffer_rsrc_t rW = buffer_over(g.Wd, C * KD);
+  // the taps 4s + lk a lane reads at step s: row and column shifts, and the
+  // neighbour's byte offset from the row's own pixel (rows are NHWC pixels,
+  // so the pixel (n, oh + dy, ow + dx) is row m + dy W + dx)
+  int dyv[NS], dxv[NS], dov[NS];
+  bool tapv[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int tap = s * 4 + lk;
+    dyv[s] = tap / KW - PT;
+    dxv[s] = tap % KW - PL;
+    dov[s] = (dyv[s] * W + dxv[s]) * C;
+    tapv[s] = tap < TAPS;
+  }
   intx4 wst[WPT];
   int bdv[CPT];
   float mdv[CPT];
@@ -948,7 +961,7 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
 #pragma unroll
       for (int s = 0; s < NS; ++s)
         wf[p][s] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(
-            rW, (cb * 16 + li) * KD + s * 64 + lk * 16, 0, 0));
+            rW, (cb * 16 + li) * KD + lk * 16, s * 64, 0));
       bf[p] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rB, (cb * 16 + lk * 4) * 4, 0, 0));
       mf[p] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rM, (cb * 16 + lk * 4) * 4, 0, 0));
     }
@@ -969,31 +982,27 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
 #pragma unroll
   for (int b0 = 0; b0 < TPW; b0 += MIXB) {
     intx4 a[MIXB][NS];
-    int row[MIXB], cbv[MIXB];
 #pragma unroll
     for (int u = 0; u < MIXB; ++u) {
-      // tile t of this wave; past the last tile (TILES % 4 != 0) a tile with
-      // every load out of range, whose result is never stored
+      // tile t of this wave (scalar); past the last tile (TILES % 4 != 0) a
+      // tile with every load out of range, whose result is never stored
       const int t = wave + 4 * (b0 + u);
       const bool tile_ok = b0 + u < TPW && t < TILES;
       const int rb = t / CB, cb = t - (t / CB) * CB;
-      row[u] = rb * 16 + li;
-      cbv[u] = cb;
-      const int m = m0 + row[u];
-      int n = 0, oh = -(1 << 20), ow = 0;
-      if (tile_ok && m < g.M) {
-        n = m / hw;
-        const int sp = m - n * hw;
-        oh = sp / g.W;
-        ow = sp - oh * g.W;
-      }
+      const int m = m0 + rb * 16 + li;
+      // H and W are compiled in: the divisions (of non-negative values) are
+      // multiplies
+      const int n = (int)((unsigned)m / (unsigned)(H * W));
+      const int sp = m - n * (H * W);
+      const int oh0 = (int)((unsigned)sp / (unsigned)W);
+      const int ow = sp - oh0 * W;
+      const int oh = tile_ok && m < g.M ? oh0 : -(1 << 20);
+      const int base = m * C + cb * 16;
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        const int tap = s * 4 + lk;
-        const int ih = oh - PT + tap / KW, iw = ow - PL + tap % KW;
-        const bool ok = tap < TAPS && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
-        const int off = ok ? ((n * g.H + ih) * g.W + iw) * C + cb * 16 : kOutside;
-        a[u][s] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rZ, off, 0, 0));
+        const bool ok = tapv[s] && (unsigned)(oh + dyv[s]) < (unsigned)H && (unsigned)(ow + dxv[s]) < (unsigned)W;
+        a[u][s] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(
+            rZ, ok ? base + dov[s] : kOutside, 0, 0));
       }
     }
     if (!MIXW && b0 == 0) {                           // the weights reach LDS (once)
@@ -1017,21 +1026,21 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
     for (int u = 0; u < MIXB; ++u) {
       const int t = wave + 4 * (b0 + u);
       if (b0 + u >= TPW || t >= TILES) continue;
-      // acc[j]: row `row`, channel cb*16 + lk*4 + j, starting at its bias
-      const int c = cbv[u] * 16 + lk * 4;
+      const int rb = t / CB, cb = t - (t / CB) * CB;
+      // acc[j]: row rb*16 + li, channel cb*16 + lk*4 + j, starting at its bias
+      const int c = cb * 16 + lk * 4;
       const int p = (b0 + u) % P;                     // compile time: b0 and u are unrolled
       intx4 acc = MIXW ? bf[p] : *reinterpret_cast<const intx4*>(&bds[c]);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         const intx4 w = MIXW ? wf[p][s]
-                             : *reinterpret_cast<const intx4*>(&Wds[(cbv[u] * 16 + li) * WS + s * 64 + lk * 16]);
+                             : *reinterpret_cast<const intx4*>(&Wds[(cb * 16 + li) * WS + s * 64 + lk * 16]);
         acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, a[u][s], acc, 0, 0, 0);
       }
       const floatx4 mv = MIXW ? mf[p] : *reinterpret_cast<const floatx4*>(&mds[c]);
-      union { int w; i8 b[4]; } o;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) o.b[j] = requant(acc[j], mv[j], (float)LOD);
-      *reinterpret_cast<int*>(&Xs[row[u] * XS + c]) = o.w;
+      *reinterpret_cast<int*>(&Xs[(rb * 16 + li) * XS + c]) =
+          pack4(requant_word(acc[0], mv[0], (float)LOD), requant_word(acc[1], mv[1], (float)LOD),
+                requant_word(acc[2], mv[2], (float)LOD), requant_word(acc[3], mv[3], (float)LOD));
     }
   }
 }
@@ -1039,38 +1048,45 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
 template <int NK, int LDB, int NI>
 struct QMlpFrags {                   // B fragments of one column chunk, whole K
   intx4 f[NK / 64][NI];
-  __device__ __forceinline__ void load(const i8* __restrict__ Bg, int col0) {
+  // One 32-bit lane offset; each fragment's place in the chunk (a constant)
+  // goes in the scalar offset, so the loads cost no vector instructions.
+  // Every fragment lies inside the weights (col0 + NI*16 <= their rows).
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rB, int col0) {
     const int lane = threadIdx.x & 63;
-    const int li = lane & 15, lk = lane >> 4;
+    const int vo = (col0 + (lane & 15)) * LDB + (lane >> 4) * 16;
 #pragma unroll
     for (int s = 0; s < NK / 64; ++s)
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni)
-        f[s][ni] = *reinterpret_cast<const intx4*>(Bg + (size_t)(col0 + ni * 16 + li) * LDB + s * 64 + lk * 16);
+        f[s][ni] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(
+            rB, vo, ni * 16 * LDB + s * 64, 0));
   }
 };
 
+// the wave index as a scalar (it is uniform over the wave)
+__device__ __forceinline__ int qmlp_wave() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 template <int WGN, int NI>
-__device__ __forceinline__ int qmlp_col0(int c0) { return c0 + ((threadIdx.x >> 6) % WGN) * NI * 16; }
+__device__ __forceinline__ int qmlp_col0(int c0) { return c0 + (qmlp_wave() % WGN) * NI * 16; }
 
 // The accumulators of a column chunk start at the columns' bias (LDS), so
 // the epilogue gets the exact int32 acc + bias.
 template <int NK, int LDA, int LDB, int NCOLS, int BM, int WGM, int WGN, int NI, class Epi, class Hook>
-__device__ __forceinline__ void qmlp_gemm(const i8* __restrict__ As, const i8* __restrict__ Bg,
+__device__ __forceinline__ void qmlp_gemm(const i8* __restrict__ As, __amdgpu_buffer_rsrc_t rB,
                                           const QMlpFrags<NK, LDB, NI>& first,
                                           const int* __restrict__ bias_lds, Epi epi, Hook hook) {
   constexpr int MI = BM / WGM / 16;
   constexpr int CHUNK = WGN * NI * 16;
   static_assert(NCOLS % CHUNK == 0 && (BM / WGM) % 16 == 0, "column chunks must tile the output");
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = qmlp_wave();
   const int li = lane & 15, lk = lane >> 4;
   const int r0 = (wave / WGN) * (BM / WGM);
 #pragma unroll
   for (int c0 = 0; c0 < NCOLS; c0 += CHUNK) {
     const int col0 = qmlp_col0<WGN, NI>(c0);
     QMlpFrags<NK, LDB, NI> fr;
-    if (c0 == 0) fr = first; else fr.load(Bg, col0);
+    if (c0 == 0) fr = first; else fr.load(rB, col0);
     intx4 acc[MI][NI];
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) {
@@ -1106,7 +1122,7 @@ __device__ __forceinline__ void qmlp_gemm(const i8* __restrict__ As, const i8* _
 // registers cost no occupancy) instead of under the first GEMM's epilogue.
 template <int C, int E, int BM, int WGM1, int WGN1, int NI1, int WGM2, int WGN2, int NI2, int LO1,
           int LO2, int MIX, int KH, int KW, int PT, int PL, int LOD, int MIXB_MAX = 3, bool EW2 = false,
-          int MIXW = 0>
+          int MIXW = 0, int MH = 1, int MW = 1>
 __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   constexpr int CP = (C + 63) / 64 * 64, EP = (E + 63) / 64 * 64;
   constexpr int XS = CP + 16, HS = EP + 16;    // LDS row strides (bytes)
@@ -1131,12 +1147,14 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   const int m0 = blockIdx.x * BM;
 
   // the first weight chunk is fetched while the X tile comes in
+  const __amdgpu_buffer_rsrc_t rW1 = buffer_over(g.W1, E * CP);
+  const __amdgpu_buffer_rsrc_t rW2 = buffer_over(g.W2, C * EP);
   QMlpFrags<CP, CP, NI1> w1f;
-  w1f.load(g.W1, qmlp_col0<WGN1, NI1>(0));
+  w1f.load(rW1, qmlp_col0<WGN1, NI1>(0));
   QMlpFrags<EP, EP, NI2> w2f;
-  if constexpr (EW2) w2f.load(g.W2, qmlp_col0<WGN2, NI2>(0));
+  if constexpr (EW2) w2f.load(rW2, qmlp_col0<WGN2, NI2>(0));
   if constexpr (MIX) {
-    qmlp_mixer<C, BM, XS, KH, KW, PT, PL, LOD, MIXB_MAX, MIXW>(g, Xs, m0, Wds, bds, mds);
+    qmlp_mixer<C, BM, XS, KH, KW, PT, PL, LOD, MIXB_MAX, MIXW, MH, MW>(g, Xs, m0, Wds, bds, mds);
   } else {
     const __amdgpu_buffer_rsrc_t rX = buffer_over(g.X, g.M * C);
     constexpr int CPR = CP / 16;
@@ -1148,7 +1166,9 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
           __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rX, off, 0, 0));
     }
   }
-  tab[tid] = g.table[tid];
+  // the table with its halves swapped: code q's entry sits at q's low byte
+  // (q & 0xff = (q + 128) ^ 0x80), which the requantized word holds
+  tab[tid] = g.table[tid ^ 0x80];
   for (int i = tid; i < E; i += NT) {
     b1s[i] = g.b1[i];
     m1s[i] = g.m1[i];
@@ -1159,32 +1179,36 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   }
   __syncthreads();
 
-  qmlp_gemm<CP, XS, CP, E, BM, WGM1, WGN1, NI1>(Xs, g.W1, w1f, b1s, [&](int r, int n, const intx4& acc,
-                                                                         int, int) {
+  qmlp_gemm<CP, XS, CP, E, BM, WGM1, WGN1, NI1>(Xs, rW1, w1f, b1s, [&](int r, int n, const intx4& acc,
+                                                                      int, int) {
     const floatx4 mv = *reinterpret_cast<const floatx4*>(&m1s[n]);
-    union { int w; i8 b[4]; } o;
+    int o[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o.b[j] = tab[(int)requant(acc[j], mv[j], (float)LO1) + 128];
-    *reinterpret_cast<int*>(&Hs[r * HS + n]) = o.w;
+    for (int j = 0; j < 4; ++j) o[j] = tab[requant_word(acc[j], mv[j], (float)LO1) & 0xff];
+    *reinterpret_cast<int*>(&Hs[r * HS + n]) = pack4(o[0], o[1], o[2], o[3]);
   }, [&]() {
-    if constexpr (!EW2) w2f.load(g.W2, qmlp_col0<WGN2, NI2>(0));
+    if constexpr (!EW2) w2f.load(rW2, qmlp_col0<WGN2, NI2>(0));
   });
   __syncthreads();
 
-  qmlp_gemm<EP, HS, EP, C, BM, WGM2, WGN2, NI2>(Hs, g.W2, w2f, b2s, [&](int r, int n, const intx4& acc,
-                                                                        int, int) {
+  qmlp_gemm<EP, HS, EP, C, BM, WGM2, WGN2, NI2>(Hs, rW2, w2f, b2s, [&](int r, int n, const intx4& acc,
+                                                                     int, int) {
     const int m = m0 + r;
     if (m >= g.M) return;
     const floatx4 mv = *reinterpret_cast<const floatx4*>(&m2s[n]);
-    union { int w; i8 b[4]; } x, o;
+    union { int w; i8 b[4]; } x;
     x.w = *reinterpret_cast<const int*>(&Xs[r * XS + n]);
+    int o[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const i8 code = requant(acc[j], mv[j], (float)LO2);
-      const float v = (float)x.b[j] * g.res_mult + (float)code * g.acc_mult;
-      o.b[j] = (i8)(int)fminf(fmaxf(rintf(v), -127.0f), 127.0f);
+      // the requantized code as a float: clamp, then round half to even (the
+      // clamp bounds are integers, so the order does not matter)
+      const float code = rintf(fminf(fmaxf((float)acc[j] * mv[j], (float)LO2), 127.0f));
+      const float v = (float)x.b[j] * g.res_mult + code * g.acc_mult;
+      // clamp(rint(v), -127, 127) in the low byte, as requant_word forms it
+      o[j] = __builtin_bit_cast(int, fminf(fmaxf(v, -127.0f), 127.0f) + 12582912.0f);
     }
-    *reinterpret_cast<int*>(g.Y + (size_t)m * C + n) = o.w;
+    *reinterpret_cast<int*>(g.Y + (size_t)m * C + n) = pack4(o[0], o[1], o[2], o[3]);
   }, [] {});
 }
 

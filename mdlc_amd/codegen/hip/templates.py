@@ -686,15 +686,16 @@ def qmlp_kernel(name: str, C: int, E: int, layout, *, lo1: int, lo2: int,
                 mixer_regs: bool = False) -> tuple:
     """Fused int8 channel mixer (two 1x1 QConvs, lookup, residual add) over
     channels-last rows; ``layout`` is a ``QMlpLayout``; ``mixer`` = (KH, KW,
-    PT, PL, LOD) adds the depthwise stride-1 token mixer that computes X
-    from the kernel's input; ``mix_batch`` tiles of it per load batch;
+    PT, PL, LOD, H, W) adds the depthwise stride-1 token mixer that computes
+    X from the kernel's input (an H x W image, compiled in); ``mix_batch`` tiles of it per load batch;
     ``early_w2`` fetches both GEMMs' weight fragments at the start;
     ``mixer_regs`` keeps the mixer's weights in registers instead of LDS.
     ABI: (X or Z, Wd, bd, md, W1, b1, m1, table, W2, b2, m2, Y, int M,
     int H, int W, float res_mult, float acc_mult)."""
-    mix = (1,) + tuple(int(v) for v in mixer) if mixer else (0, 1, 1, 0, 0, -127)
+    mix = (1,) + tuple(int(v) for v in mixer[:5]) if mixer else (0, 1, 1, 0, 0, -127)
+    image = tuple(int(v) for v in mixer[5:7]) if mixer else (1, 1)
     args = (C, E, layout.BM) + tuple(layout.g1) + tuple(layout.g2) + (int(lo1), int(lo2)) + mix + \
-        (int(mix_batch), "true" if early_w2 else "false", 1 if (mixer and mixer_regs) else 0)
+        (int(mix_batch), "true" if early_w2 else "false", 1 if (mixer and mixer_regs) else 0) + image
     return name, (
         f'extern "C" __global__ __launch_bounds__(256) void {name}(\n'
         "    const signed char* __restrict__ X, const signed char* __restrict__ Wd,\n"
