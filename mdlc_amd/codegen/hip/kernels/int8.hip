@@ -910,11 +910,16 @@ struct QMixDims {
   static constexpr int WS = KD + 16;                          // and in LDS
 };
 
+//
+// `after_first` runs once the first batch's loads are issued, before any
+// wait: the caller issues its own (later needed) loads there, so that the
+// waits of the mixer, which count outstanding loads in issue order, do not
+// wait for them.
 template <int C, int BM, int XS, int KH, int KW, int PT, int PL, int LOD, int MIXB_MAX, int MIXW,
-          int H, int W>
+          int H, int W, class After>
 __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ Xs, int m0,
                                            i8* __restrict__ Wds, int* __restrict__ bds,
-                                           float* __restrict__ mds) {
+                                           float* __restrict__ mds, After after_first) {
   constexpr int TAPS = KH * KW;
   constexpr int KD = QMixDims<C, KH, KW>::KD, WS = QMixDims<C, KH, KW>::WS;
   constexpr int NS = KD / 64;
@@ -929,6 +934,7 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // tiles are wave-uniform: scalar
+  __builtin_assume(wave < 4);                         // 256 threads: with TILES % 4 == 0 every tile is real
   const int li = lane & 15, lk = lane >> 4;
   const __amdgpu_buffer_rsrc_t rZ = buffer_over(g.X, g.M * C);
   const __amdgpu_buffer_rsrc_t rW = buffer_over(g.Wd, C * KD);
@@ -1005,6 +1011,10 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
             rZ, ok ? base + dov[s] : kOutside, 0, 0));
       }
     }
+    if (b0 == 0) {
+      after_first();
+      __builtin_amdgcn_sched_barrier(0);              // every load above issues before the first wait
+    }
     if (!MIXW && b0 == 0) {                           // the weights reach LDS (once)
 #pragma unroll
       for (int i = 0; i < WPT; ++i) {
@@ -1024,9 +1034,12 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
     }
 #pragma unroll
     for (int u = 0; u < MIXB; ++u) {
+      // a tile past the last (TILES % 4 != 0) is computed from its zero
+      // loads and not stored: no branch around its loads and MFMAs
       const int t = wave + 4 * (b0 + u);
-      if (b0 + u >= TPW || t >= TILES) continue;
-      const int rb = t / CB, cb = t - (t / CB) * CB;
+      if (b0 + u >= TPW) continue;                    // compile time
+      const int tt = t < TILES ? t : TILES - 1;
+      const int rb = tt / CB, cb = tt - (tt / CB) * CB;
       // acc[j]: row rb*16 + li, channel cb*16 + lk*4 + j, starting at its bias
       const int c = cb * 16 + lk * 4;
       const int p = (b0 + u) % P;                     // compile time: b0 and u are unrolled
@@ -1038,9 +1051,9 @@ __device__ __forceinline__ void qmlp_mixer(const QMlpArgs& g, i8* __restrict__ X
         acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, a[u][s], acc, 0, 0, 0);
       }
       const floatx4 mv = MIXW ? mf[p] : *reinterpret_cast<const floatx4*>(&mds[c]);
-      *reinterpret_cast<int*>(&Xs[(rb * 16 + li) * XS + c]) =
-          pack4(requant_word(acc[0], mv[0], (float)LOD), requant_word(acc[1], mv[1], (float)LOD),
-                requant_word(acc[2], mv[2], (float)LOD), requant_word(acc[3], mv[3], (float)LOD));
+      const int o = pack4(requant_word(acc[0], mv[0], (float)LOD), requant_word(acc[1], mv[1], (float)LOD),
+                          requant_word(acc[2], mv[2], (float)LOD), requant_word(acc[3], mv[3], (float)LOD));
+      if (TILES % 4 == 0 || t < TILES) *reinterpret_cast<int*>(&Xs[(rb * 16 + li) * XS + c]) = o;
     }
   }
 }
@@ -1146,36 +1159,79 @@ __device__ __forceinline__ void qmlp_i8(const QMlpArgs& g) {
   const int tid = threadIdx.x;
   const int m0 = blockIdx.x * BM;
 
-  // the first weight chunk is fetched while the X tile comes in
+  // The lookup table (with its halves swapped: code q's entry sits at q's
+  // low byte, (q + 128) ^ 0x80 = q & 0xff, which the requantized word holds)
+  // and both GEMMs' bias and multipliers, loaded first into registers and
+  // stored to LDS with the X tile: neither epilogue waits on a global load
+  // in the middle of the chain, and the stores wait for these loads only.
+  constexpr int EPT = (E + NT - 1) / NT, CPT2 = (C + NT - 1) / NT;
+  const i8 tabv = g.table[tid ^ 0x80];
+  int b1v[EPT], b2v[CPT2];
+  float m1v[EPT], m2v[CPT2];
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    const int i = tid + k * NT;
+    b1v[k] = i < E ? g.b1[i] : 0;
+    m1v[k] = i < E ? g.m1[i] : 0.f;
+  }
+#pragma unroll
+  for (int k = 0; k < CPT2; ++k) {
+    const int i = tid + k * NT;
+    b2v[k] = i < C ? g.b2[i] : 0;
+    m2v[k] = i < C ? g.m2[i] : 0.f;
+  }
+
+  // The first weight chunk (with EW2 both GEMMs' fragments) is fetched while
+  // the X tile comes in, issued after the X tile's loads (or the token
+  // mixer's first batch): a wait counts outstanding loads in issue order, so
+  // the X tile is then ready without waiting for the weights.
   const __amdgpu_buffer_rsrc_t rW1 = buffer_over(g.W1, E * CP);
   const __amdgpu_buffer_rsrc_t rW2 = buffer_over(g.W2, C * EP);
   QMlpFrags<CP, CP, NI1> w1f;
-  w1f.load(rW1, qmlp_col0<WGN1, NI1>(0));
   QMlpFrags<EP, EP, NI2> w2f;
-  if constexpr (EW2) w2f.load(rW2, qmlp_col0<WGN2, NI2>(0));
+  const auto weights = [&]() {
+    w1f.load(rW1, qmlp_col0<WGN1, NI1>(0));
+    if constexpr (EW2) w2f.load(rW2, qmlp_col0<WGN2, NI2>(0));
+  };
   if constexpr (MIX) {
-    qmlp_mixer<C, BM, XS, KH, KW, PT, PL, LOD, MIXB_MAX, MIXW, MH, MW>(g, Xs, m0, Wds, bds, mds);
+    qmlp_mixer<C, BM, XS, KH, KW, PT, PL, LOD, MIXB_MAX, MIXW, MH, MW>(g, Xs, m0, Wds, bds, mds, weights);
   } else {
     const __amdgpu_buffer_rsrc_t rX = buffer_over(g.X, g.M * C);
     constexpr int CPR = CP / 16;
+    constexpr int XPT = (BM * CPR + NT - 1) / NT;
+    intx4 xr[XPT];
 #pragma unroll
-    for (int i = tid; i < BM * CPR; i += NT) {
+    for (int k = 0; k < XPT; ++k) {
+      const int i = tid + k * NT;
       const int r = i / CPR, j = i - (i / CPR) * CPR;
-      const int off = (m0 + r < g.M && j * 16 < C) ? (m0 + r) * C + j * 16 : kOutside;
-      *reinterpret_cast<intx4*>(&Xs[r * XS + j * 16]) =
-          __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rX, off, 0, 0));
+      const int off = (i < BM * CPR && m0 + r < g.M && j * 16 < C) ? (m0 + r) * C + j * 16 : kOutside;
+      xr[k] = __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(rX, off, 0, 0));
+    }
+    weights();
+    __builtin_amdgcn_sched_barrier(0);                // every load above issues before the first wait
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) {
+      const int i = tid + k * NT;
+      const int r = i / CPR, j = i - (i / CPR) * CPR;
+      if ((BM * CPR) % NT == 0 || i < BM * CPR) *reinterpret_cast<intx4*>(&Xs[r * XS + j * 16]) = xr[k];
     }
   }
-  // the table with its halves swapped: code q's entry sits at q's low byte
-  // (q & 0xff = (q + 128) ^ 0x80), which the requantized word holds
-  tab[tid] = g.table[tid ^ 0x80];
-  for (int i = tid; i < E; i += NT) {
-    b1s[i] = g.b1[i];
-    m1s[i] = g.m1[i];
+  tab[tid] = tabv;
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    const int i = tid + k * NT;
+    if (i < E) {
+      b1s[i] = b1v[k];
+      m1s[i] = m1v[k];
+    }
   }
-  for (int i = tid; i < C; i += NT) {
-    b2s[i] = g.b2[i];
-    m2s[i] = g.m2[i];
+#pragma unroll
+  for (int k = 0; k < CPT2; ++k) {
+    const int i = tid + k * NT;
+    if (i < C) {
+      b2s[i] = b2v[k];
+      m2s[i] = m2v[k];
+    }
   }
   __syncthreads();
 
