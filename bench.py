@@ -13,6 +13,12 @@ the five fused GEMM+bias+ReLU micro shapes and the int8 GEMM at 4096^3
 ``--workload`` (``mobilenetv2``, ``repvit_int8``, ``micro_gemm``,
 ``int8_gemm``).
 
+Each workload's plan first runs untimed for ``--settle-ms`` of device time
+(100 ms by default; ``settle_ms`` in the line), then ``--warmup`` untimed
+steps, then exactly ``--steps`` timed ones: from an idle device the GPU clock
+needs tens of milliseconds of load to reach its sustained value, and a few
+warm-up steps of a sub-millisecond forward end well before that.
+
 Prints one JSON line: throughput; the dominant kernel's roofline (its
 algorithmic work per launch over its average launch time, timed per launch
 with HIP events on the library's stream), also for the kernel together with
@@ -25,6 +31,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import platform
 import sys
@@ -171,15 +178,38 @@ def cpu_int8(feeds, w, size: int) -> dict:
 
 # ----- device timing ------------------------------------------------------------------
 
+SETTLE_MS = 100.0          # device time run before each workload's warm-up (--settle-ms)
+SETTLE_MAX_STEPS = 20000
+
+
+def settle(ex, settle_ms: float) -> int:
+    """Run the plan for about ``settle_ms`` of device time, untimed, so the
+    GPU is at its sustained clock when the warm-up and timed steps start: from
+    an idle device the clock takes tens of milliseconds of load to settle
+    (ResNet-18 b=32 measured 0.909-0.914 ms a forward after 5 warm-up steps,
+    0.893 ms after 100 or 300; int8 4096^3 74 us against 66 us). Returns the
+    number of plan runs."""
+    if settle_ms <= 0:
+        return 0
+    per = ex.plan.time_ms(0, 2)                 # ms of one run, measured on the device
+    n = int(min(SETTLE_MAX_STEPS, max(1, math.ceil(settle_ms / max(per, 1e-3)))))
+    ex.plan.run(n)
+    ex.ctx.synchronize()
+    return n
+
+
 def time_module(c, feeds, steps: int, warmup: int, profile_iters: int, use_graph: bool = False,
                 host_loop: bool = True):
     """(ms per step by events, host seconds per step including the feed
-    upload and output read, per-launch profile, arena bytes)."""
+    upload and output read, per-launch profile, arena bytes). The plan first
+    runs for SETTLE_MS of device time (``settle``), then ``warmup`` untimed
+    steps, then exactly ``steps`` timed ones."""
     from mdlc_amd.codegen.hip.hip_executor import HipExecutor
 
     ex = HipExecutor(c.module, use_graph=use_graph)
     try:
         ex._upload_feeds(feeds)
+        settle(ex, SETTLE_MS)
         ex.plan.run(warmup)
         ex.ctx.synchronize()
         ms = ex.plan.time_ms(0, steps)
@@ -446,7 +476,8 @@ def full_line(args, part: dict, *, scaling: str, data: str, config: dict) -> dic
             if k in ("launches", "host_buffer_images_per_s", "cold_compile_s", "shapes", "M", "N", "K")
             or k.startswith(("algorithmic_", "executed_", "network_"))}
     out = {"metric": part["metric"], "value": part["value"], "unit": part["unit"], "n_gpus": 1,
-           "steps": part["steps"], "warmup": args.warmup, "ms_per_step": part["ms_per_step"],
+           "steps": part["steps"], "warmup": args.warmup, "settle_ms": SETTLE_MS,
+           "ms_per_step": part["ms_per_step"],
            "higher_is_better": True, "scaling": scaling, "vs_baseline": None,
            "dtype": part["dtype"], "data": data,
            "config": {"workload": part["workload"], **config, **keep}}
@@ -528,6 +559,7 @@ def cold_compile_seconds(c) -> float:
 
 
 def main(argv=None) -> int:
+    global SETTLE_MS
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
@@ -548,9 +580,13 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="measure only the selected workload")
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="device time each workload's plan runs, untimed, before its warm-up "
+                         "steps, so the GPU is at its sustained clock (0: none)")
     ap.add_argument("--profile-iters", type=int, default=25,
                     help="runs of the plan whose per-launch median the roofline uses")
     args = ap.parse_args(argv)
+    SETTLE_MS = args.settle_ms
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "inference shards by batch across GPUs, which is not part of this build",
